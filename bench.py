@@ -1,0 +1,423 @@
+"""Benchmark of the fracture_amd hot path on one MI355X.
+
+Default workload (the metric's configuration): one Llama-3.1-8B decode step's elementwise
+chain at batch 64, fp16 — embedding gather from a [128256, 4096] table, RoPE on
+Q [64, 32, 128] and K [64, 8, 128] (theta 500000, positions in [0, 8192)), SwiGLU on
+[64, 14336], and two residual adds fused with RMSNorm on [64, 4096] — with inputs resident
+in HBM. A step is the five launches, replayed from a HIP graph (eager timing reported too).
+
+Printed: one JSON line with the metric (whole-chain algorithmic GB/s; ms_per_step), per-kernel
+microseconds and GB/s, the roofline object for the dominant kernel (SwiGLU) and the CPU
+baseline (the oracle's restatement of the reference's CPU path, single thread, on this host).
+
+Other workloads (parity-tested configurations, printed as their own JSON lines):
+  --workload prefill      add+RMSNorm [8192,4096], SwiGLU [8192,14336], softmax/argmax [64,128256]
+  --workload tq           TurboQuant compress + dequantize of K and V [32768, 8, 128], 4 and 3 bit
+  --workload attention    decode attention over a K4/V4 page pool, B=64, 32/8 heads, ctx U[1024,32768]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "HBM GB/s (% of peak) per kernel; µs per B=64 decode-step elementwise chain"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="decode",
+                    choices=["decode", "prefill", "tq", "attention", "all"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--eager", action="store_true", help="time the chain without a HIP graph")
+    return ap.parse_args()
+
+
+def gbs(nbytes: float, us: float) -> float:
+    return nbytes / (us * 1e-6) / 1e9
+
+
+class Timer:
+    """HIP events on torch's current stream, which is the stream the kernels launch on."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def time_us(self, fn, reps: int, warmup: int = 3) -> float:
+        t = self.torch
+        for _ in range(warmup):
+            fn()
+        s, e = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        t.cuda.synchronize()
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        e.synchronize()
+        return s.elapsed_time(e) * 1e3 / reps
+
+
+def traffic_of(kernel_key: str):
+    """HBM bytes per dispatch measured with rocprofv3 PMC counters, when recorded."""
+    p = ROOT / "profiles" / "traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get(kernel_key, {}).get("bytes_per_dispatch")
+    except (ValueError, OSError):
+        return None
+
+
+# ---------------------------------------------------------------------------------------
+# decode-step chain (the headline)
+# ---------------------------------------------------------------------------------------
+def decode_inputs(torch, dev, seed=0):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    B, V, H, QH, KVH, HD, FF = 64, 128256, 4096, 32, 8, 128, 14336
+    f16 = torch.float16
+    x = {}
+    x["table"] = (torch.randn((V, H), generator=g, device=dev) * 0.02).to(f16)
+    x["ids"] = torch.randint(0, V, (B,), generator=g, device=dev, dtype=torch.int32)
+    x["emb"] = torch.empty((B, H), dtype=f16, device=dev)
+    x["q"] = torch.randn((B, QH, HD), generator=g, device=dev).to(f16)
+    x["k"] = torch.randn((B, KVH, HD), generator=g, device=dev).to(f16)
+    x["pos"] = torch.randint(0, 8192, (B,), generator=g, device=dev, dtype=torch.int32)
+    from fracture_amd import turboquant as tq
+
+    x["freqs"] = torch.from_numpy(tq.rope_freqs(HD, 500000.0)).to(dev)
+    x["gate"] = torch.randn((B, FF), generator=g, device=dev).to(f16)
+    x["up"] = torch.randn((B, FF), generator=g, device=dev).to(f16)
+    x["act"] = torch.empty((B, FF), dtype=f16, device=dev)
+    x["h"] = torch.randn((B, H), generator=g, device=dev).to(f16)
+    x["d1"] = torch.randn((B, H), generator=g, device=dev).to(f16)
+    x["d2"] = torch.randn((B, H), generator=g, device=dev).to(f16)
+    x["w1"] = (torch.rand((H,), generator=g, device=dev) + 0.5).to(f16)
+    x["w2"] = (torch.rand((H,), generator=g, device=dev) + 0.5).to(f16)
+    x["n1"] = torch.empty((B, H), dtype=f16, device=dev)
+    x["n2"] = torch.empty((B, H), dtype=f16, device=dev)
+    return x
+
+
+def decode_bytes():
+    B, H, QH, KVH, HD, FF = 64, 4096, 32, 8, 128, 14336
+    return {
+        "embedding": 2 * B * H * 2 + B * 4,
+        "rope": 2 * B * (QH + KVH) * HD * 2 + B * 4 + HD // 2 * 4,
+        "silu_mul": 3 * B * FF * 2,
+        "add_rmsnorm": 4 * B * H * 2 + H * 2,
+    }
+
+
+def decode_ops(K, x):
+    return {
+        "embedding": lambda: K.embedding(x["emb"], x["table"], x["ids"]),
+        "rope": lambda: K.rope(x["q"], x["k"], x["pos"], x["freqs"]),
+        "silu_mul": lambda: K.silu_mul(x["act"], x["gate"], x["up"]),
+        "add_rmsnorm": lambda: K.add_rmsnorm(x["h"], x["d1"], x["w1"], 1e-5, x["n1"]),
+        "add_rmsnorm_2": lambda: K.add_rmsnorm(x["h"], x["d2"], x["w2"], 1e-5, x["n2"]),
+    }
+
+
+def decode_step(ops):
+    for f in ops.values():
+        f()
+
+
+def cpu_decode_baseline(seconds: float):
+    """The oracle's restatement of the reference's CPU formulas for the same chain, one
+    thread, median over as many steps as fit in `seconds` (at least 3)."""
+    import numpy as np
+
+    import oracle
+
+    rng = np.random.default_rng(0)
+    B, V, H, QH, KVH, HD, FF = 64, 128256, 4096, 32, 8, 128, 14336
+    table = (np.arange(V, dtype=np.int64)[:, None] * 2654435761 + np.arange(H)[None, :] * 40503)
+    table = (table % 30000).astype(np.int16).view(np.float16)
+    ids = rng.integers(0, V, B).astype(np.uint32)
+    q = rng.standard_normal((B, QH, HD)).astype(np.float16)
+    k = rng.standard_normal((B, KVH, HD)).astype(np.float16)
+    pos = rng.integers(0, 8192, B).astype(np.uint32)
+    fr = oracle.rope_freqs(HD, 500000.0)
+    g = rng.standard_normal((B, FF)).astype(np.float16)
+    u = rng.standard_normal((B, FF)).astype(np.float16)
+    h = rng.standard_normal((B, H)).astype(np.float16)
+    d1 = rng.standard_normal((B, H)).astype(np.float16)
+    d2 = rng.standard_normal((B, H)).astype(np.float16)
+    w = rng.uniform(0.5, 1.5, H).astype(np.float16)
+
+    def step(h):
+        oracle.embedding(table, ids)
+        oracle.rope(q, pos, fr)
+        oracle.rope(k, pos, fr)
+        oracle.silu_mul(g, u)
+        h, _ = oracle.add_rmsnorm(h, d1, w, 1e-5)
+        h, _ = oracle.add_rmsnorm(h, d2, w, 1e-5)
+        return h
+
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < 3 or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        h = step(h)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return med * 1e6, len(times)
+
+
+def run_decode(args, torch, K, dev):
+    x = decode_inputs(torch, dev)
+    ops = decode_ops(K, x)
+    nbytes = decode_bytes()
+    chain_bytes = (nbytes["embedding"] + nbytes["rope"] + nbytes["silu_mul"] +
+                   2 * nbytes["add_rmsnorm"])
+    timer = Timer(torch)
+    torch.cuda.synchronize()
+
+    graph = None
+    if not args.eager:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(3):
+                decode_step(ops)  # warm the launch path on the capture stream
+        torch.cuda.current_stream().wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            decode_step(ops)
+        torch.cuda.synchronize()
+
+    def step():
+        if graph is not None:
+            graph.replay()
+        else:
+            decode_step(ops)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s_ev.record()
+    for _ in range(args.steps):
+        step()
+    e_ev.record()
+    torch.cuda.synchronize()
+    us_step = s_ev.elapsed_time(e_ev) * 1e3 / args.steps
+    eager_us = timer.time_us(lambda: decode_step(ops), max(20, args.steps // 4))
+
+    # per-kernel average launch durations (back-to-back launches between two events)
+    per = {}
+    reps = 400
+    for name in ("embedding", "rope", "silu_mul", "add_rmsnorm"):
+        us = timer.time_us(ops[name], reps)
+        per[name] = {"us": round(us, 3), "GB/s": round(gbs(nbytes[name], us), 1),
+                     "frac_of_peak": round(gbs(nbytes[name], us) / PEAK_HBM_GBS, 4),
+                     "bytes": nbytes[name]}
+    dom = "silu_mul"
+    traffic = traffic_of("silu_mul_64x14336")
+    roof = {"kernel": "silu_mul_vec_kernel<fp16> [64,14336]", "bound": "hbm",
+            "achieved": per[dom]["GB/s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(per[dom]["GB/s"] / PEAK_HBM_GBS, 4), "traffic": traffic,
+            "algorithmic_bytes": nbytes[dom], "avg_launch_us": per[dom]["us"]}
+
+    result = {
+        "metric": METRIC,
+        "value": round(gbs(chain_bytes, us_step), 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us_step / 1e3, 6),
+        "us_per_step": round(us_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded torch.Generator; Llama-3.1-8B shapes)",
+        "config": {"workload": "llama3.1-8b decode-step elementwise chain, batch 64, fp16",
+                   "batch": 64, "hidden": 4096, "vocab": 128256, "q_heads": 32,
+                   "kv_heads": 8, "head_dim": 128, "ffn": 14336, "rope_theta": 500000.0,
+                   "launch": "hip graph" if graph is not None else "eager",
+                   "chain_bytes": chain_bytes},
+        "eager_us_per_step": round(eager_us, 3),
+        "kernels": per,
+        "roofline": roof,
+    }
+    if not args.no_cpu_baseline:
+        cpu_us, n = cpu_decode_baseline(args.cpu_seconds)
+        result["cpu_baseline"] = {
+            "value": round(gbs(chain_bytes, cpu_us), 3), "unit": "GB/s", "cores": 1,
+            "kind": "port", "us_per_step": round(cpu_us, 1),
+            "sample": f"median of {n} steps of the same chain (same shapes) through the C "
+                      f"restatement of the reference's CPU formulas, one thread, "
+                      f"{os.cpu_count()} host cores visible"}
+    return result
+
+
+# ---------------------------------------------------------------------------------------
+# other workloads
+# ---------------------------------------------------------------------------------------
+def run_prefill(args, torch, K, dev):
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    f16 = torch.float16
+    h = torch.randn((8192, 4096), generator=g, device=dev).to(f16)
+    d = torch.randn((8192, 4096), generator=g, device=dev).to(f16)
+    w = (torch.rand((4096,), generator=g, device=dev) + 0.5).to(f16)
+    n = torch.empty_like(h)
+    gate = torch.randn((8192, 14336), generator=g, device=dev).to(f16)
+    up = torch.randn((8192, 14336), generator=g, device=dev).to(f16)
+    act = torch.empty_like(gate)
+    lg = torch.randn((64, 128256), generator=g, device=dev) * 3
+    lg[torch.arange(64, device=dev), torch.randint(0, 128256, (64,), generator=g, device=dev)] += 20
+    probs = torch.empty_like(lg)
+    idx = torch.empty(64, dtype=torch.int32, device=dev)
+    fl = torch.empty(64, dtype=torch.int32, device=dev)
+    ws = K.rows_workspace(64, 128256, dev)
+    timer = Timer(torch)
+    out = {}
+    items = {
+        "add_rmsnorm_8192x4096": (lambda: K.add_rmsnorm(h, d, w, 1e-5, n), 4 * 8192 * 4096 * 2),
+        "silu_mul_8192x14336": (lambda: K.silu_mul(act, gate, up), 3 * 8192 * 14336 * 2),
+        "softmax_64x128256": (lambda: K.softmax_rows(lg, probs, 1.0, ws), 2 * 64 * 128256 * 4),
+        "argmax_64x128256": (lambda: K.argmax_rows(lg, idx, fl, ws), 64 * 128256 * 4),
+        "softmax_argmax_64x128256": (lambda: K.softmax_argmax_rows(lg, probs, idx, fl, 1.0, ws),
+                                     2 * 64 * 128256 * 4),
+    }
+    for name, (fn, nb) in items.items():
+        us = timer.time_us(fn, 50, warmup=5)
+        out[name] = {"us": round(us, 2), "GB/s": round(gbs(nb, us), 1),
+                     "frac_of_peak": round(gbs(nb, us) / PEAK_HBM_GBS, 4), "bytes": nb,
+                     "traffic": traffic_of(name)}
+    return {"workload": "prefill-shaped reductions (fp16 in, fp32 accumulate)", "kernels": out}
+
+
+def run_tq(args, torch, K, dev):
+    from fracture_amd import turboquant as tq
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+    N, H, hd = 32768, 8, 128
+    scale = torch.exp(torch.randn((N, 1, 1), generator=g, device=dev) * 0.5)
+    k = (torch.randn((N, H, hd), generator=g, device=dev) * scale).to(torch.float16)
+    v = (torch.randn((N, H, hd), generator=g, device=dev) * scale).to(torch.float16)
+    krot = torch.from_numpy(tq.rotation_matrix(hd, 42)).to(dev)
+    vrot = torch.from_numpy(tq.rotation_matrix(hd, 542)).to(dev)
+    timer = Timer(torch)
+    out = {}
+    for bits in (4, 3):
+        cent = torch.from_numpy(tq.codebook(hd, bits)[0]).to(dev)
+        pd = K.packed_dim(hd, bits)
+        kp = torch.empty((N, H * pd), dtype=torch.uint8, device=dev)
+        vp = torch.empty_like(kp)
+        kn = torch.empty((N, H), dtype=torch.float16, device=dev)
+        vn = torch.empty_like(kn)
+        kd = torch.empty_like(k)
+        vd = torch.empty_like(v)
+
+        def comp():
+            K.tq_compress(k, krot, cent, bits, kp, kn)
+            K.tq_compress(v, vrot, cent, bits, vp, vn)
+
+        def deq():
+            K.tq_dequant(kp, kn, krot, cent, bits, kd)
+            K.tq_dequant(vp, vn, vrot, cent, bits, vd)
+
+        nb = 2 * (N * H * hd * 2 + N * H * pd + N * H * 2)  # K and V: read fp16, write codes+norms
+        flops = 2 * 2 * N * H * hd * hd
+        for name, fn in (("compress", comp), ("dequant", deq)):
+            us = timer.time_us(fn, 20, warmup=3)
+            out[f"tq_{name}_kv_{bits}bit"] = {
+                "us": round(us, 2), "GB/s": round(gbs(nb, us), 1),
+                "frac_of_peak": round(gbs(nb, us) / PEAK_HBM_GBS, 4), "bytes": nb,
+                "rotation_TFLOP/s": round(flops / (us * 1e-6) / 1e12, 1),
+                "traffic": traffic_of(f"tq_{name}_{bits}bit")}
+    return {"workload": "TurboQuant KV compress / dequantize, one layer, [32768, 8, 128] K and V",
+            "kernels": out}
+
+
+def run_attention(args, torch, K, dev):
+    import numpy as np
+
+    from fracture_amd import turboquant as tq
+
+    rng = np.random.default_rng(5)
+    B, QH, KVH, HD, kb, vb = 64, 32, 8, 128, 4, 4
+    lens = rng.integers(1024, 32769, B).astype(np.int32)
+    nbs = (lens + 15) // 16
+    P = int(nbs.sum())
+    maxb = int(nbs.max())
+    perm = rng.permutation(P).astype(np.int32)
+    table = np.zeros((B, maxb), np.int32)
+    at = 0
+    for b in range(B):
+        table[b, :nbs[b]] = perm[at:at + nbs[b]]
+        at += nbs[b]
+    pdk, pdv = K.packed_dim(HD, kb), K.packed_dim(HD, vb)
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    kp = torch.randint(0, 256, (P, 16, KVH * pdk), generator=g, device=dev, dtype=torch.uint8)
+    vp = torch.randint(0, 256, (P, 16, KVH * pdv), generator=g, device=dev, dtype=torch.uint8)
+    kn = (torch.rand((P, 16, KVH), generator=g, device=dev) * 10 + 6).to(torch.float16)
+    vn = (torch.rand((P, 16, KVH), generator=g, device=dev) * 10 + 6).to(torch.float16)
+    q = torch.randn((B, QH, HD), generator=g, device=dev).to(torch.float16)
+    out = torch.empty_like(q)
+    krot = torch.from_numpy(tq.rotation_matrix(HD, 42)).to(dev)
+    vrot = torch.from_numpy(tq.rotation_matrix(HD, 542)).to(dev)
+    kc = torch.from_numpy(tq.codebook(HD, kb)[0]).to(dev)
+    vc = torch.from_numpy(tq.codebook(HD, vb)[0]).to(dev)
+    tb = torch.from_numpy(table).to(dev)
+    sl = torch.from_numpy(lens).to(dev)
+    ws = K.attention_workspace(B, QH, HD, maxb, dev)
+    fn = lambda: K.attention_tq_decode(out, q, tb, sl, kp, kn, vp, vn, krot, vrot, kc, vc, kb, vb,
+                                       KVH, ws)
+    us = Timer(torch).time_us(fn, 10, warmup=2)
+    tok = int(lens.sum())
+    nb = tok * KVH * (pdk + pdv + 4) + B * QH * HD * 4 + B * maxb * 4
+    return {"workload": "TurboQuant K4/V4 paged decode attention, B=64, 32/8 heads, hd 128",
+            "kernels": {"attention_tq_decode": {
+                "us": round(us, 1), "GB/s": round(gbs(nb, us), 1),
+                "frac_of_peak": round(gbs(nb, us) / PEAK_HBM_GBS, 4), "bytes": nb,
+                "context_tokens": tok, "mean_ctx": float(lens.mean()),
+                "traffic": traffic_of("attention_tq_decode")}}}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "fracture_amd benchmarks one GPU: this build has no "
+                                   "multi-GPU path; run with --gpus 1"}))
+        sys.exit(2)
+    import torch
+
+    from fracture_amd import kernels as K
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    wl = args.workload
+    if wl in ("decode", "all"):
+        print(json.dumps(run_decode(args, torch, K, dev)), flush=True)
+    if wl in ("prefill", "all"):
+        print(json.dumps(run_prefill(args, torch, K, dev)), flush=True)
+    if wl in ("tq", "all"):
+        print(json.dumps(run_tq(args, torch, K, dev)), flush=True)
+    if wl in ("attention", "all"):
+        print(json.dumps(run_attention(args, torch, K, dev)), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,948 @@
+// Handle runtime of libfracture_hip.so: the C-ABI mirror of Fracture's `Backend` trait
+// (crates/fracture-core/src/backend.rs:8-223) and of the inherent CudaBackend API
+// (backends/fracture-cuda/src/lib.rs:76-182, backend.rs:7-710).
+//
+// One HIP stream per backend, a mutex-guarded id -> device pointer registry, event timers,
+// roctx markers. Host-side arguments (positions, token ids, block tables, page pointer
+// tables) go through a ring of pinned staging slots copied with hipMemcpyAsync on the
+// backend's stream; each slot is reused only after the event recorded behind the kernel that
+// read it has completed, so no per-call hipMalloc/hipFree is needed (the reference mallocs
+// and frees them synchronously on every call, backend.rs:178-204, 387-410, 643-705).
+#include <hip/hip_runtime.h>
+#include <dlfcn.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "fracture_hip.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e) {
+    return fail(FHIP_ERR_BACKEND, "HIP error (%d): %s", (int)e, hipGetErrorString(e));
+}
+
+#define HIP_TRY(call)                                \
+    do {                                             \
+        hipError_t e_ = (call);                      \
+        if (e_ != hipSuccess) return hip_fail(e_);   \
+    } while (0)
+
+int launch_result(int e) {
+    if (e != hipSuccess) return hip_fail((hipError_t)e);
+    return FHIP_OK;
+}
+
+size_t dtype_size(int dt) {
+    switch (dt) {
+        case FHIP_FP16: return 2;
+        case FHIP_FP32: return 4;
+        case FHIP_BF16: return 2;
+        case FHIP_INT8: return 1;
+        case FHIP_INT4: return 1;
+        default: return 0;
+    }
+}
+const char* dtype_name(int dt) {
+    switch (dt) {
+        case FHIP_FP16: return "FP16";
+        case FHIP_FP32: return "FP32";
+        case FHIP_BF16: return "BF16";
+        case FHIP_INT8: return "INT8";
+        case FHIP_INT4: return "INT4";
+        default: return "?";
+    }
+}
+
+uint64_t numel(const fhip_tensor* t) {
+    uint64_t n = 1;
+    for (int i = 0; i < t->ndim; ++i) n *= t->shape[i];
+    return n;
+}
+// DeviceTensor::size_bytes (tensor.rs:53-60): INT4 packs two elements per byte.
+uint64_t size_bytes(const fhip_tensor* t) {
+    const uint64_t n = numel(t);
+    return t->dtype == FHIP_INT4 ? (n + 1) / 2 : n * dtype_size(t->dtype);
+}
+std::string shape_str(const fhip_tensor* t) {
+    std::string s = "[";
+    for (int i = 0; i < t->ndim; ++i) {
+        if (i) s += ", ";
+        s += std::to_string(t->shape[i]);
+    }
+    return s + "]";
+}
+bool same_shape(const fhip_tensor* a, const fhip_tensor* b) {
+    if (a->ndim != b->ndim) return false;
+    for (int i = 0; i < a->ndim; ++i)
+        if (a->shape[i] != b->shape[i]) return false;
+    return true;
+}
+bool valid_desc(const fhip_tensor* t) {
+    return t && t->ndim >= 0 && t->ndim <= FHIP_MAX_DIMS && dtype_size(t->dtype) != 0;
+}
+
+// roctx, loaded on first use; markers are no-ops without it.
+struct Roctx {
+    int (*push)(const char*) = nullptr;
+    int (*pop)() = nullptr;
+    std::once_flag once;
+    void load() {
+        std::call_once(once, [this] {
+            void* h = dlopen("libroctx64.so", RTLD_LAZY | RTLD_LOCAL);
+            if (!h) h = dlopen("/opt/rocm/lib/libroctx64.so", RTLD_LAZY | RTLD_LOCAL);
+            if (!h) return;
+            push = (int (*)(const char*))dlsym(h, "roctxRangePushA");
+            pop = (int (*)())dlsym(h, "roctxRangePop");
+        });
+    }
+} g_roctx;
+
+// Pinned host + device staging slot for small host-side arguments.
+struct StageSlot {
+    void* host = nullptr;
+    void* dev = nullptr;
+    size_t cap = 0;
+    hipEvent_t ev = nullptr;
+    bool pending = false;
+};
+
+}  // namespace
+
+struct fhip_backend {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string name;
+    size_t total_mem = 0;
+    std::mutex mu;  // registry, timers
+    std::unordered_map<uint64_t, void*> tensors;
+    uint64_t next_id = 1;
+    std::unordered_map<uint64_t, std::pair<hipEvent_t, hipEvent_t>> timers;
+    uint64_t next_timer = 1;
+    float* rope_freq = nullptr;
+    size_t rope_half = 0;
+    // launch lock: staging ring and workspace are per backend
+    std::mutex launch_mu;
+    static constexpr int kSlots = 16;
+    StageSlot slots[kSlots];
+    int next_slot = 0;
+    void* workspace = nullptr;
+    size_t ws_cap = 0;
+    hipEvent_t ws_ev = nullptr;
+    bool ws_pending = false;
+
+    int get_ptr(uint64_t id, void** out) {
+        std::lock_guard<std::mutex> g(mu);
+        auto it = tensors.find(id);
+        if (it == tensors.end())
+            return fail(FHIP_ERR_TENSOR_NOT_FOUND, "tensor id %llu",
+                        (unsigned long long)id);
+        *out = it->second;
+        return FHIP_OK;
+    }
+
+    // Copy `bytes` of host data to a device staging slot; returns the slot index. Callers
+    // hold launch_mu and call stage_done(slot) after enqueuing the consumer kernel.
+    int stage(const void* src, size_t bytes, void** dev_out, int* slot_out) {
+        const int si = next_slot;
+        next_slot = (next_slot + 1) % kSlots;
+        StageSlot& s = slots[si];
+        if (s.pending) {
+            HIP_TRY(hipEventSynchronize(s.ev));
+            s.pending = false;
+        }
+        if (!s.ev) HIP_TRY(hipEventCreateWithFlags(&s.ev, hipEventDisableTiming));
+        if (bytes > s.cap) {
+            if (s.host) HIP_TRY(hipHostFree(s.host));
+            if (s.dev) HIP_TRY(hipFree(s.dev));
+            s.host = s.dev = nullptr;
+            s.cap = 0;
+            size_t cap = 256;
+            while (cap < bytes) cap *= 2;
+            HIP_TRY(hipHostMalloc(&s.host, cap, hipHostMallocDefault));
+            HIP_TRY(hipMalloc(&s.dev, cap));
+            s.cap = cap;
+        }
+        if (bytes) {
+            memcpy(s.host, src, bytes);
+            HIP_TRY(hipMemcpyAsync(s.dev, s.host, bytes, hipMemcpyHostToDevice, stream));
+        }
+        *dev_out = s.dev;
+        *slot_out = si;
+        return FHIP_OK;
+    }
+    int stage_done(int si) {
+        HIP_TRY(hipEventRecord(slots[si].ev, stream));
+        slots[si].pending = true;
+        return FHIP_OK;
+    }
+    // Backend-owned scratch (softmax partials, attention split partials). Callers hold
+    // launch_mu and call ws_done() after enqueuing the kernels that use it.
+    int get_workspace(size_t bytes, void** out) {
+        if (ws_pending) {
+            HIP_TRY(hipEventSynchronize(ws_ev));
+            ws_pending = false;
+        }
+        if (!ws_ev) HIP_TRY(hipEventCreateWithFlags(&ws_ev, hipEventDisableTiming));
+        if (bytes > ws_cap) {
+            if (workspace) HIP_TRY(hipFree(workspace));
+            workspace = nullptr;
+            ws_cap = 0;
+            size_t cap = 1 << 20;
+            while (cap < bytes) cap *= 2;
+            HIP_TRY(hipMalloc(&workspace, cap));
+            ws_cap = cap;
+        }
+        *out = workspace;
+        return FHIP_OK;
+    }
+    int ws_done() {
+        HIP_TRY(hipEventRecord(ws_ev, stream));
+        ws_pending = true;
+        return FHIP_OK;
+    }
+};
+
+namespace {
+
+#define CHECK_B(b) \
+    if (!(b)) return fail(FHIP_ERR_BACKEND, "null backend handle")
+#define CHECK_T(t) \
+    if (!valid_desc(t)) return fail(FHIP_ERR_INVALID_SHAPE, "invalid tensor descriptor")
+#define GET_PTR(b, t, p)                         \
+    void* p = nullptr;                           \
+    {                                            \
+        int r_ = (b)->get_ptr((t)->id, &p);      \
+        if (r_ != FHIP_OK) return r_;            \
+    }
+
+int set_device(fhip_backend* b) {
+    HIP_TRY(hipSetDevice(b->device));
+    return FHIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* fhip_last_error(void) { return g_last_error.c_str(); }
+
+int fhip_backend_create(int device_id, fhip_backend** out) {
+    if (!out) return fail(FHIP_ERR_BACKEND, "null output handle");
+    *out = nullptr;
+    HIP_TRY(hipSetDevice(device_id));
+    hipDeviceProp_t props;
+    HIP_TRY(hipGetDeviceProperties(&props, device_id));
+    fhip_backend* b = new fhip_backend();
+    b->device = device_id;
+    hipError_t e = hipStreamCreateWithFlags(&b->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete b;
+        return hip_fail(e);
+    }
+    b->name = props.name;
+    b->total_mem = props.totalGlobalMem;
+    *out = b;
+    return FHIP_OK;
+}
+
+void fhip_backend_destroy(fhip_backend* b) {
+    if (!b) return;
+    (void)hipSetDevice(b->device);
+    (void)hipStreamSynchronize(b->stream);
+    for (auto& kv : b->tensors) (void)hipFree(kv.second);
+    for (auto& kv : b->timers) {
+        (void)hipEventDestroy(kv.second.first);
+        (void)hipEventDestroy(kv.second.second);
+    }
+    for (auto& s : b->slots) {
+        if (s.host) (void)hipHostFree(s.host);
+        if (s.dev) (void)hipFree(s.dev);
+        if (s.ev) (void)hipEventDestroy(s.ev);
+    }
+    if (b->workspace) (void)hipFree(b->workspace);
+    if (b->ws_ev) (void)hipEventDestroy(b->ws_ev);
+    if (b->rope_freq) (void)hipFree(b->rope_freq);
+    (void)hipStreamDestroy(b->stream);
+    delete b;
+}
+
+int fhip_get_ptr(fhip_backend* b, uint64_t id, void** out) {
+    CHECK_B(b);
+    if (!out) return fail(FHIP_ERR_BACKEND, "null output pointer");
+    return b->get_ptr(id, out);
+}
+
+fhip_stream_t fhip_stream(fhip_backend* b) { return b ? (fhip_stream_t)b->stream : nullptr; }
+
+int fhip_precompute_rope_freqs(fhip_backend* b, size_t head_dim, double theta) {
+    CHECK_B(b);
+    if (head_dim < 2 || head_dim % 2 != 0 || head_dim > 4096)
+        return fail(FHIP_ERR_INVALID_SHAPE, "rope head_dim must be even and in [2, 4096], got %zu",
+                    head_dim);
+    set_device(b);
+    const size_t half = head_dim / 2;
+    std::vector<float> f(half);
+    fhip_rope_freqs((int)head_dim, theta, f.data());
+    float* dev = nullptr;
+    HIP_TRY(hipMalloc(&dev, half * sizeof(float)));
+    hipError_t e = hipMemcpy(dev, f.data(), half * sizeof(float), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(dev);
+        return hip_fail(e);
+    }
+    std::lock_guard<std::mutex> g(b->launch_mu);
+    if (b->rope_freq) {
+        (void)hipStreamSynchronize(b->stream);
+        (void)hipFree(b->rope_freq);
+    }
+    b->rope_freq = dev;
+    b->rope_half = half;
+    return FHIP_OK;
+}
+
+int fhip_alloc(fhip_backend* b, const uint64_t* shape, int ndim, int dtype, fhip_tensor* out) {
+    CHECK_B(b);
+    if (!out || ndim < 0 || ndim > FHIP_MAX_DIMS || (ndim > 0 && !shape))
+        return fail(FHIP_ERR_INVALID_SHAPE, "invalid shape (ndim %d)", ndim);
+    if (dtype_size(dtype) == 0) return fail(FHIP_ERR_UNSUPPORTED_DTYPE, "dtype %d", dtype);
+    fhip_tensor t;
+    memset(&t, 0, sizeof t);
+    t.dtype = dtype;
+    t.ndim = ndim;
+    unsigned __int128 n = 1;
+    for (int i = 0; i < ndim; ++i) {
+        t.shape[i] = shape[i];
+        n *= shape[i];
+    }
+    if (n > ((unsigned __int128)1 << 62))
+        return fail(FHIP_ERR_BACKEND, "HIP error (%d): %s", (int)hipErrorOutOfMemory,
+                    hipGetErrorString(hipErrorOutOfMemory));
+    const uint64_t bytes = size_bytes(&t);
+    set_device(b);
+    void* p = nullptr;
+    // hipMalloc of zero bytes returns a null pointer; keep a 1-byte allocation so the id is
+    // still resolvable.
+    HIP_TRY(hipMalloc(&p, bytes ? bytes : 1));
+    std::lock_guard<std::mutex> g(b->mu);
+    t.id = b->next_id++;
+    b->tensors[t.id] = p;
+    *out = t;
+    return FHIP_OK;
+}
+
+int fhip_free(fhip_backend* b, const fhip_tensor* t) {
+    CHECK_B(b);
+    if (!t) return fail(FHIP_ERR_INVALID_SHAPE, "null tensor");
+    void* p = nullptr;
+    {
+        std::lock_guard<std::mutex> g(b->mu);
+        auto it = b->tensors.find(t->id);
+        if (it == b->tensors.end())
+            return fail(FHIP_ERR_TENSOR_NOT_FOUND, "tensor id %llu",
+                        (unsigned long long)t->id);
+        p = it->second;
+        b->tensors.erase(it);
+    }
+    set_device(b);
+    // Kernels on the backend's stream may still read the buffer.
+    HIP_TRY(hipStreamSynchronize(b->stream));
+    HIP_TRY(hipFree(p));
+    return FHIP_OK;
+}
+
+int fhip_copy_to_device(fhip_backend* b, const fhip_tensor* dst, const void* src, size_t src_len) {
+    CHECK_B(b);
+    CHECK_T(dst);
+    GET_PTR(b, dst, p);
+    const uint64_t size = size_bytes(dst);
+    if (src_len < size)
+        return fail(FHIP_ERR_INVALID_SHAPE, "source buffer too small: %zu < %llu",
+                    src_len, (unsigned long long)size);
+    if (size == 0) return FHIP_OK;
+    set_device(b);
+    HIP_TRY(hipMemcpyAsync(p, src, size, hipMemcpyHostToDevice, b->stream));
+    HIP_TRY(hipStreamSynchronize(b->stream));
+    return FHIP_OK;
+}
+
+int fhip_copy_to_host(fhip_backend* b, const fhip_tensor* src, void* dst, size_t dst_len) {
+    CHECK_B(b);
+    CHECK_T(src);
+    GET_PTR(b, src, p);
+    const uint64_t size = size_bytes(src);
+    if (dst_len < size)
+        return fail(FHIP_ERR_INVALID_SHAPE,
+                    "destination buffer too small: %zu < %llu", dst_len,
+                    (unsigned long long)size);
+    if (size == 0) return FHIP_OK;
+    set_device(b);
+    HIP_TRY(hipMemcpyAsync(dst, p, size, hipMemcpyDeviceToHost, b->stream));
+    HIP_TRY(hipStreamSynchronize(b->stream));
+    return FHIP_OK;
+}
+
+int fhip_rmsnorm(fhip_backend* b, const fhip_tensor* input, const fhip_tensor* weight, double eps,
+                 const fhip_tensor* out) {
+    CHECK_B(b);
+    CHECK_T(input);
+    CHECK_T(weight);
+    CHECK_T(out);
+    GET_PTR(b, input, pin);
+    GET_PTR(b, weight, pw);
+    GET_PTR(b, out, pout);
+    if (input->ndim < 1)
+        return fail(FHIP_ERR_INVALID_SHAPE, "rmsnorm input must be 2-D");
+    const uint64_t cols = input->shape[input->ndim - 1];
+    const uint64_t rows = cols ? numel(input) / cols : 0;
+    if (numel(weight) != cols || numel(out) != numel(input) || weight->dtype != input->dtype ||
+        out->dtype != input->dtype)
+        return fail(FHIP_ERR_INVALID_SHAPE,
+                    "rmsnorm: input %s %s, weight %s %s, out %s %s",
+                    shape_str(input).c_str(), dtype_name(input->dtype), shape_str(weight).c_str(),
+                    dtype_name(weight->dtype), shape_str(out).c_str(), dtype_name(out->dtype));
+    if (input->dtype != FHIP_FP16 && input->dtype != FHIP_BF16 && input->dtype != FHIP_FP32)
+        return fail(FHIP_ERR_UNSUPPORTED_DTYPE, "rmsnorm %s",
+                    dtype_name(input->dtype));
+    if (rows == 0) return FHIP_OK;
+    set_device(b);
+    g_roctx.load();
+    return launch_result(fhip_launch_rmsnorm_ex(pout, pin, pw, (float)eps, (int)rows, (int)cols,
+                                                input->dtype, b->stream));
+}
+
+int fhip_add_rmsnorm(fhip_backend* b, const fhip_tensor* residual, const fhip_tensor* delta,
+                     const fhip_tensor* weight, double eps, const fhip_tensor* normed_out) {
+    CHECK_B(b);
+    CHECK_T(residual);
+    CHECK_T(delta);
+    CHECK_T(weight);
+    CHECK_T(normed_out);
+    GET_PTR(b, residual, ph);
+    GET_PTR(b, delta, pd);
+    GET_PTR(b, weight, pw);
+    GET_PTR(b, normed_out, po);
+    if (residual->ndim < 1)
+        return fail(FHIP_ERR_INVALID_SHAPE, "add_rmsnorm needs 2-D input");
+    const uint64_t cols = residual->shape[residual->ndim - 1];
+    const uint64_t rows = cols ? numel(residual) / cols : 0;
+    if (!same_shape(residual, delta) || numel(normed_out) != numel(residual) ||
+        numel(weight) != cols || delta->dtype != residual->dtype ||
+        weight->dtype != residual->dtype || normed_out->dtype != residual->dtype)
+        return fail(FHIP_ERR_INVALID_SHAPE,
+                    "add_rmsnorm: residual %s, delta %s, weight %s, out %s",
+                    shape_str(residual).c_str(), shape_str(delta).c_str(),
+                    shape_str(weight).c_str(), shape_str(normed_out).c_str());
+    if (residual->dtype != FHIP_FP16 && residual->dtype != FHIP_BF16 &&
+        residual->dtype != FHIP_FP32)
+        return fail(FHIP_ERR_UNSUPPORTED_DTYPE, "add_rmsnorm %s",
+                    dtype_name(residual->dtype));
+    if (rows == 0) return FHIP_OK;
+    set_device(b);
+    return launch_result(fhip_launch_add_rmsnorm(ph, pd, pw, (float)eps, po, (int)rows, (int)cols,
+                                                 residual->dtype, b->stream));
+}
+
+int fhip_rope(fhip_backend* b, const fhip_tensor* q, const fhip_tensor* k,
+              const uint32_t* positions, size_t num_positions, double theta, size_t head_dim) {
+    (void)theta;  // the table from precompute_rope_freqs is used (backend.rs:166)
+    CHECK_B(b);
+    CHECK_T(q);
+    CHECK_T(k);
+    GET_PTR(b, q, pq);
+    GET_PTR(b, k, pk);
+    if (!b->rope_freq)
+        return fail(FHIP_ERR_BACKEND,
+                    "RoPE frequency table not initialized. Call precompute_rope_freqs() first.");
+    if (q->ndim < 2 || k->ndim < 2 || head_dim != 2 * b->rope_half)
+        return fail(FHIP_ERR_INVALID_SHAPE,
+                    "rope: q %s, k %s, head_dim %zu (table for %zu)",
+                    shape_str(q).c_str(), shape_str(k).c_str(), head_dim, 2 * b->rope_half);
+    const uint64_t qh = q->shape[1], kvh = k->shape[1];
+    const uint64_t T = num_positions;
+    if (numel(q) < T * qh * head_dim || numel(k) < T * kvh * head_dim || q->dtype != k->dtype)
+        return fail(FHIP_ERR_INVALID_SHAPE,
+                    "rope: %zu positions do not fit q %s / k %s",
+                    num_positions, shape_str(q).c_str(), shape_str(k).c_str());
+    if (q->dtype != FHIP_FP16 && q->dtype != FHIP_BF16 && q->dtype != FHIP_FP32)
+        return fail(FHIP_ERR_UNSUPPORTED_DTYPE, "rope %s", dtype_name(q->dtype));
+    if (T == 0) return FHIP_OK;
+    if (!positions) return fail(FHIP_ERR_INVALID_SHAPE, "null positions");
+    set_device(b);
+    std::lock_guard<std::mutex> g(b->launch_mu);
+    void* dpos;
+    int slot;
+    int r = b->stage(positions, T * sizeof(uint32_t), &dpos, &slot);
+    if (r != FHIP_OK) return r;
+    int e = fhip_launch_rope_ex(pq, pk, (const uint32_t*)dpos, b->rope_freq, (int)T, (int)qh,
+                                (int)kvh, (int)head_dim, q->dtype, b->stream);
+    r = b->stage_done(slot);
+    if (e != hipSuccess)
+        return fail(FHIP_ERR_BACKEND, "RoPE kernel error: %s", hipGetErrorString((hipError_t)e));
+    return r;
+}
+
+int fhip_silu_mul(fhip_backend* b, const fhip_tensor* gate, const fhip_tensor* up,
+                  const fhip_tensor* out) {
+    CHECK_B(b);
+    CHECK_T(gate);
+    CHECK_T(up);
+    CHECK_T(out);
+    if (!same_shape(gate, up))
+        return fail(FHIP_ERR_INVALID_SHAPE, "silu_mul: gate shape %s != up shape %s",
+                    shape_str(gate).c_str(), shape_str(up).c_str());
+    GET_PTR(b, gate, pg);
+    GET_PTR(b, up, pu);
+    GET_PTR(b, out, po);
+    if (numel(out) < numel(gate) || up->dtype != gate->dtype || out->dtype != gate->dtype)
+        return fail(FHIP_ERR_INVALID_SHAPE, "silu_mul: out %s too small",
+                    shape_str(out).c_str());
+    set_device(b);
+    return launch_result(
+        fhip_launch_silu_mul_ex(po, pg, pu, (int64_t)numel(gate), gate->dtype, b->stream));
+}
+
+int fhip_add(fhip_backend* b, const fhip_tensor* a, const fhip_tensor* bt, const fhip_tensor* out) {
+    CHECK_B(b);
+    CHECK_T(a);
+    CHECK_T(bt);
+    CHECK_T(out);
+    if (!same_shape(a, bt))
+        return fail(FHIP_ERR_INVALID_SHAPE, "add: a shape %s != b shape %s",
+                    shape_str(a).c_str(), shape_str(bt).c_str());
+    GET_PTR(b, a, pa);
+    GET_PTR(b, bt, pb);
+    GET_PTR(b, out, po);
+    if (numel(out) < numel(a) || bt->dtype != a->dtype || out->dtype != a->dtype)
+        return fail(FHIP_ERR_INVALID_SHAPE, "add: out %s too small",
+                    shape_str(out).c_str());
+    set_device(b);
+    return launch_result(fhip_launch_add_ex(po, pa, pb, (int64_t)numel(a), a->dtype, b->stream));
+}
+
+int fhip_embedding(fhip_backend* b, const uint32_t* token_ids, size_t num_tokens,
+                   const fhip_tensor* table, const fhip_tensor* out) {
+    CHECK_B(b);
+    CHECK_T(table);
+    CHECK_T(out);
+    GET_PTR(b, table, pt);
+    GET_PTR(b, out, po);
+    if (table->ndim != 2 || (dtype_size(table->dtype) != 2 && dtype_size(table->dtype) != 4))
+        return fail(FHIP_ERR_INVALID_SHAPE, "embedding table %s",
+                    shape_str(table).c_str());
+    const uint64_t vocab = table->shape[0], hidden = table->shape[1];
+    if (numel(out) < num_tokens * hidden || out->dtype != table->dtype)
+        return fail(FHIP_ERR_INVALID_SHAPE, "embedding out %s for %zu tokens",
+                    shape_str(out).c_str(), num_tokens);
+    if (num_tokens == 0) return FHIP_OK;
+    if (!token_ids) return fail(FHIP_ERR_INVALID_SHAPE, "null token ids");
+    set_device(b);
+    std::lock_guard<std::mutex> g(b->launch_mu);
+    void* dids;
+    int slot;
+    int r = b->stage(token_ids, num_tokens * sizeof(uint32_t), &dids, &slot);
+    if (r != FHIP_OK) return r;
+    int e = fhip_launch_embedding_ex(po, pt, (const uint32_t*)dids, (int)num_tokens, (int)hidden,
+                                     (int)(vocab > 0x7fffffffull ? 0x7fffffff : vocab),
+                                     (int)dtype_size(table->dtype), b->stream);
+    r = b->stage_done(slot);
+    if (e != hipSuccess)
+        return fail(FHIP_ERR_BACKEND, "embedding kernel error: %s", hipGetErrorString((hipError_t)e));
+    return r;
+}
+
+int fhip_copy_rows(fhip_backend* b, const fhip_tensor* src, const fhip_tensor* dst,
+                   size_t src_offset, size_t dst_offset, size_t count) {
+    CHECK_B(b);
+    CHECK_T(src);
+    CHECK_T(dst);
+    if (src->ndim < 1 || dst->ndim < 1)
+        return fail(FHIP_ERR_INVALID_SHAPE, "copy_rows needs >= 1-D tensors");
+    if (src_offset + count > src->shape[0])
+        return fail(FHIP_ERR_INVALID_SHAPE,
+                    "copy_rows: src_offset(%zu) + count(%zu) = %zu exceeds src rows(%llu)",
+                    src_offset, count, src_offset + count, (unsigned long long)src->shape[0]);
+    if (dst_offset + count > dst->shape[0])
+        return fail(FHIP_ERR_INVALID_SHAPE,
+                    "copy_rows: dst_offset(%zu) + count(%zu) = %zu exceeds dst rows(%llu)",
+                    dst_offset, count, dst_offset + count, (unsigned long long)dst->shape[0]);
+    bool tail_eq = src->ndim == dst->ndim;
+    for (int i = 1; tail_eq && i < src->ndim; ++i) tail_eq = src->shape[i] == dst->shape[i];
+    if (!tail_eq)
+        return fail(FHIP_ERR_INVALID_SHAPE, "copy_rows: src column shape != dst column shape (%s vs %s)",
+                    shape_str(src).c_str(), shape_str(dst).c_str());
+    if (src->dtype != dst->dtype)
+        return fail(FHIP_ERR_INVALID_SHAPE, "copy_rows: src dtype %s != dst dtype %s",
+                    dtype_name(src->dtype), dtype_name(dst->dtype));
+    GET_PTR(b, src, ps);
+    GET_PTR(b, dst, pdst);
+    uint64_t row_elems = 1;
+    for (int i = 1; i < src->ndim; ++i) row_elems *= src->shape[i];
+    const uint64_t row = row_elems * dtype_size(src->dtype);
+    if (count == 0 || row == 0) return FHIP_OK;
+    set_device(b);
+    HIP_TRY(hipMemcpyAsync((char*)pdst + dst_offset * row, (const char*)ps + src_offset * row,
+                           count * row, hipMemcpyDeviceToDevice, b->stream));
+    return FHIP_OK;
+}
+
+const char* fhip_device_name(fhip_backend* b) { return b ? b->name.c_str() : ""; }
+size_t fhip_total_memory(fhip_backend* b) { return b ? b->total_mem : 0; }
+size_t fhip_available_memory(fhip_backend* b) {
+    if (!b) return 0;
+    (void)hipSetDevice(b->device);
+    size_t free_b = 0, total_b = 0;
+    if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) return 0;
+    return free_b;
+}
+
+int fhip_synchronize(fhip_backend* b) {
+    CHECK_B(b);
+    set_device(b);
+    HIP_TRY(hipStreamSynchronize(b->stream));
+    return FHIP_OK;
+}
+
+int fhip_create_timer(fhip_backend* b, uint64_t* timer_id) {
+    CHECK_B(b);
+    if (!timer_id) return fail(FHIP_ERR_BACKEND, "null timer id");
+    set_device(b);
+    hipEvent_t s, e;
+    HIP_TRY(hipEventCreate(&s));
+    hipError_t r = hipEventCreate(&e);
+    if (r != hipSuccess) {
+        (void)hipEventDestroy(s);
+        return hip_fail(r);
+    }
+    std::lock_guard<std::mutex> g(b->mu);
+    *timer_id = b->next_timer++;
+    b->timers[*timer_id] = {s, e};
+    return FHIP_OK;
+}
+
+static int find_timer(fhip_backend* b, uint64_t id, hipEvent_t* s, hipEvent_t* e) {
+    std::lock_guard<std::mutex> g(b->mu);
+    auto it = b->timers.find(id);
+    if (it == b->timers.end()) return fail(FHIP_ERR_BACKEND, "timer %llu not found", (unsigned long long)id);
+    *s = it->second.first;
+    *e = it->second.second;
+    return FHIP_OK;
+}
+
+int fhip_start_timer(fhip_backend* b, uint64_t timer_id) {
+    CHECK_B(b);
+    hipEvent_t s, e;
+    int r = find_timer(b, timer_id, &s, &e);
+    if (r) return r;
+    HIP_TRY(hipEventRecord(s, b->stream));
+    return FHIP_OK;
+}
+
+int fhip_stop_timer(fhip_backend* b, uint64_t timer_id, float* ms_out) {
+    CHECK_B(b);
+    hipEvent_t s, e;
+    int r = find_timer(b, timer_id, &s, &e);
+    if (r) return r;
+    HIP_TRY(hipEventRecord(e, b->stream));
+    HIP_TRY(hipEventSynchronize(e));
+    float ms = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&ms, s, e));
+    if (ms_out) *ms_out = ms;
+    return FHIP_OK;
+}
+
+int fhip_destroy_timer(fhip_backend* b, uint64_t timer_id) {
+    CHECK_B(b);
+    std::pair<hipEvent_t, hipEvent_t> ev;
+    {
+        std::lock_guard<std::mutex> g(b->mu);
+        auto it = b->timers.find(timer_id);
+        if (it == b->timers.end())
+            return fail(FHIP_ERR_BACKEND, "timer %llu not found", (unsigned long long)timer_id);
+        ev = it->second;
+        b->timers.erase(it);
+    }
+    (void)hipEventDestroy(ev.first);
+    (void)hipEventDestroy(ev.second);
+    return FHIP_OK;
+}
+
+void fhip_marker_push(fhip_backend* b, const char* name) {
+    (void)b;
+    g_roctx.load();
+    if (g_roctx.push && name) g_roctx.push(name);
+}
+
+void fhip_marker_pop(fhip_backend* b) {
+    (void)b;
+    g_roctx.load();
+    if (g_roctx.pop) g_roctx.pop();
+}
+
+int fhip_turboquant_compress(fhip_backend* b, const fhip_tensor* input, const fhip_tensor* rotation,
+                             const fhip_tensor* centroids, uint8_t bits,
+                             const fhip_tensor* packed_out, const fhip_tensor* norms_out) {
+    CHECK_B(b);
+    CHECK_T(input);
+    CHECK_T(rotation);
+    CHECK_T(centroids);
+    CHECK_T(packed_out);
+    CHECK_T(norms_out);
+    GET_PTR(b, input, pin);
+    GET_PTR(b, rotation, prot);
+    GET_PTR(b, centroids, pc);
+    GET_PTR(b, packed_out, pp);
+    GET_PTR(b, norms_out, pn);
+    if (input->ndim != 3 || input->dtype != FHIP_FP16)
+        return fail(FHIP_ERR_INVALID_SHAPE,
+                    "turboquant_compress input must be [N, kv_heads, head_dim] FP16, got %s %s",
+                    shape_str(input).c_str(), dtype_name(input->dtype));
+    const uint64_t N = input->shape[0], H = input->shape[1], hd = input->shape[2];
+    const uint64_t L = numel(centroids);
+    if (bits < 1 || bits > 8 || L < 1 || L > (1ull << bits) || centroids->dtype != FHIP_FP32)
+        return fail(FHIP_ERR_INVALID_SHAPE,
+                    "turboquant_compress: %llu centroids for %u bits",
+                    (unsigned long long)L, (unsigned)bits);
+    const uint64_t pd = fhip_tq_packed_dim_per_head(hd, bits);
+    if (numel(rotation) != hd * hd || rotation->dtype != FHIP_FP32 ||
+        size_bytes(packed_out) < N * H * pd || numel(norms_out) < N * H ||
+        norms_out->dtype != FHIP_FP16)
+        return fail(FHIP_ERR_INVALID_SHAPE,
+                    "turboquant_compress: rotation %s, packed %s, norms %s",
+                    shape_str(rotation).c_str(), shape_str(packed_out).c_str(),
+                    shape_str(norms_out).c_str());
+    set_device(b);
+    return launch_result(fhip_launch_turboquant_compress(pin, (const float*)prot, (const float*)pc,
+                                                         pp, pn, (int)N, (int)H, (int)hd, (int)L,
+                                                         bits, (int)pd, b->stream));
+}
+
+int fhip_tq_quantize_pack(fhip_backend* b, const fhip_tensor* y, const fhip_tensor* centroids,
+                          uint8_t bits, const fhip_tensor* packed_out) {
+    CHECK_B(b);
+    CHECK_T(y);
+    CHECK_T(centroids);
+    CHECK_T(packed_out);
+    GET_PTR(b, y, py);
+    GET_PTR(b, centroids, pc);
+    GET_PTR(b, packed_out, pp);
+    if (y->ndim < 1 || y->dtype != FHIP_FP32)
+        return fail(FHIP_ERR_INVALID_SHAPE, "tq_quantize_pack y %s",
+                    shape_str(y).c_str());
+    const uint64_t hd = y->shape[y->ndim - 1];
+    const uint64_t rows = hd ? numel(y) / hd : 0;
+    const uint64_t L = numel(centroids);
+    if (bits < 1 || bits > 8 || L < 1 || L > (1ull << bits) || centroids->dtype != FHIP_FP32)
+        return fail(FHIP_ERR_INVALID_SHAPE, "%llu centroids for %u bits",
+                    (unsigned long long)L, (unsigned)bits);
+    const uint64_t pd = fhip_tq_packed_dim_per_head(hd, bits);
+    if (size_bytes(packed_out) < rows * pd)
+        return fail(FHIP_ERR_INVALID_SHAPE, "packed %s too small",
+                    shape_str(packed_out).c_str());
+    set_device(b);
+    return launch_result(fhip_launch_tq_quantize_pack((const float*)py, (const float*)pc, (int)L,
+                                                      bits, pp, (int)rows, (int)hd, (int)pd,
+                                                      b->stream));
+}
+
+int fhip_tq_dequantize(fhip_backend* b, const fhip_tensor* packed, const fhip_tensor* norms,
+                       const fhip_tensor* rotation, const fhip_tensor* centroids, uint8_t bits,
+                       const fhip_tensor* out) {
+    CHECK_B(b);
+    CHECK_T(packed);
+    CHECK_T(norms);
+    CHECK_T(rotation);
+    CHECK_T(centroids);
+    CHECK_T(out);
+    GET_PTR(b, packed, pp);
+    GET_PTR(b, norms, pn);
+    GET_PTR(b, rotation, prot);
+    GET_PTR(b, centroids, pc);
+    GET_PTR(b, out, po);
+    if (out->ndim != 3 || out->dtype != FHIP_FP16)
+        return fail(FHIP_ERR_INVALID_SHAPE, "dequantize out must be [N, kv_heads, head_dim] FP16");
+    const uint64_t N = out->shape[0], H = out->shape[1], hd = out->shape[2];
+    const uint64_t L = numel(centroids);
+    if (bits < 1 || bits > 8 || L < 1 || L > (1ull << bits) || centroids->dtype != FHIP_FP32)
+        return fail(FHIP_ERR_INVALID_SHAPE, "%llu centroids for %u bits",
+                    (unsigned long long)L, (unsigned)bits);
+    const uint64_t pd = fhip_tq_packed_dim_per_head(hd, bits);
+    if (size_bytes(packed) < N * H * pd || numel(norms) < N * H || norms->dtype != FHIP_FP16 ||
+        numel(rotation) != hd * hd || rotation->dtype != FHIP_FP32)
+        return fail(FHIP_ERR_INVALID_SHAPE, "dequantize packed %s norms %s",
+                    shape_str(packed).c_str(), shape_str(norms).c_str());
+    set_device(b);
+    return launch_result(fhip_launch_tq_dequant(pp, pn, (const float*)prot, (const float*)pc,
+                                                (int)L, po, (int)N, (int)H, (int)hd, bits,
+                                                (int)pd, b->stream));
+}
+
+int fhip_softmax_rows(fhip_backend* b, const fhip_tensor* logits, float temperature,
+                      const fhip_tensor* probs) {
+    CHECK_B(b);
+    CHECK_T(logits);
+    CHECK_T(probs);
+    GET_PTR(b, logits, pl);
+    GET_PTR(b, probs, pp);
+    if (logits->ndim < 1 || logits->dtype != FHIP_FP32 || probs->dtype != FHIP_FP32 ||
+        numel(probs) != numel(logits))
+        return fail(FHIP_ERR_INVALID_SHAPE, "softmax logits %s probs %s",
+                    shape_str(logits).c_str(), shape_str(probs).c_str());
+    const uint64_t cols = logits->shape[logits->ndim - 1];
+    if (cols == 0) return fail(FHIP_ERR_GENERATION, "empty logits");
+    const uint64_t rows = numel(logits) / cols;
+    if (rows == 0) return FHIP_OK;
+    set_device(b);
+    std::lock_guard<std::mutex> g(b->launch_mu);
+    void* ws;
+    int r = b->get_workspace(fhip_rows_workspace_bytes((int)rows, (int)cols), &ws);
+    if (r) return r;
+    int e = fhip_launch_softmax_rows((const float*)pl, (float*)pp, (int)rows, (int)cols,
+                                     temperature, ws, b->stream);
+    r = b->ws_done();
+    if (e != hipSuccess) return hip_fail((hipError_t)e);
+    return r;
+}
+
+int fhip_argmax_rows(fhip_backend* b, const fhip_tensor* logits, uint32_t* tokens_out,
+                     size_t rows_out) {
+    CHECK_B(b);
+    CHECK_T(logits);
+    GET_PTR(b, logits, pl);
+    if (logits->ndim < 1 || logits->dtype != FHIP_FP32)
+        return fail(FHIP_ERR_INVALID_SHAPE, "argmax logits %s",
+                    shape_str(logits).c_str());
+    const uint64_t cols = logits->shape[logits->ndim - 1];
+    if (cols == 0) return fail(FHIP_ERR_GENERATION, "empty logits");
+    const uint64_t rows = numel(logits) / cols;
+    if (rows_out < rows || (rows && !tokens_out))
+        return fail(FHIP_ERR_INVALID_SHAPE, "%zu outputs for %llu rows",
+                    rows_out, (unsigned long long)rows);
+    if (rows == 0) return FHIP_OK;
+    set_device(b);
+    std::vector<int32_t> idx(rows);
+    std::vector<uint32_t> flags(rows);
+    {
+        std::lock_guard<std::mutex> g(b->launch_mu);
+        const size_t part = fhip_rows_workspace_bytes((int)rows, (int)cols);
+        const size_t off = (part + 255) & ~(size_t)255;
+        void* ws;
+        int r = b->get_workspace(off + rows * 8, &ws);
+        if (r) return r;
+        int32_t* didx = (int32_t*)((char*)ws + off);
+        uint32_t* dfl = (uint32_t*)(didx + rows);
+        int e = fhip_launch_argmax_rows((const float*)pl, didx, dfl, (int)rows, (int)cols, ws,
+                                        b->stream);
+        if (e != hipSuccess) return hip_fail((hipError_t)e);
+        HIP_TRY(hipMemcpyAsync(idx.data(), didx, rows * 4, hipMemcpyDeviceToHost, b->stream));
+        HIP_TRY(hipMemcpyAsync(flags.data(), dfl, rows * 4, hipMemcpyDeviceToHost, b->stream));
+        HIP_TRY(hipStreamSynchronize(b->stream));
+    }
+    // The sampler rejects any NaN first, then any infinity (sampling.rs:51-56).
+    for (uint64_t r = 0; r < rows; ++r)
+        if (flags[r] & FHIP_ROW_HAS_NAN) return fail(FHIP_ERR_GENERATION, "NaN in logits");
+    for (uint64_t r = 0; r < rows; ++r)
+        if (flags[r] & FHIP_ROW_HAS_INF) return fail(FHIP_ERR_GENERATION, "Inf in logits");
+    for (uint64_t r = 0; r < rows; ++r) tokens_out[r] = (uint32_t)idx[r];
+    return FHIP_OK;
+}
+
+int fhip_attention_paged_tq(fhip_backend* b, const fhip_tensor* q, const int32_t* block_table,
+                            size_t num_blocks, const fhip_tensor* k_packed,
+                            const fhip_tensor* k_norms, const fhip_tensor* v_packed,
+                            const fhip_tensor* v_norms, size_t pool_len,
+                            const fhip_tensor* k_rotation, const fhip_tensor* v_rotation,
+                            const fhip_tensor* k_centroids, const fhip_tensor* v_centroids,
+                            uint8_t key_bits, uint8_t value_bits, size_t num_kv_heads,
+                            size_t kv_len, size_t start_pos, const fhip_tensor* out) {
+    CHECK_B(b);
+    CHECK_T(q);
+    CHECK_T(k_rotation);
+    CHECK_T(v_rotation);
+    CHECK_T(k_centroids);
+    CHECK_T(v_centroids);
+    CHECK_T(out);
+    GET_PTR(b, q, pq);
+    GET_PTR(b, out, po);
+    GET_PTR(b, k_rotation, pkr);
+    GET_PTR(b, v_rotation, pvr);
+    GET_PTR(b, k_centroids, pkc);
+    GET_PTR(b, v_centroids, pvc);
+    if (q->ndim != 3 || q->dtype != FHIP_FP16 || out->dtype != FHIP_FP16 ||
+        numel(out) != numel(q))
+        return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged_tq q %s out %s",
+                    shape_str(q).c_str(), shape_str(out).c_str());
+    const uint64_t T = q->shape[0], qh = q->shape[1], hd = q->shape[2];
+    if (num_kv_heads == 0 || qh % num_kv_heads != 0 || key_bits < 1 || key_bits > 8 ||
+        value_bits < 1 || value_bits > 8 || numel(k_rotation) != hd * hd ||
+        numel(v_rotation) != hd * hd || numel(k_centroids) < (1ull << key_bits) ||
+        numel(v_centroids) < (1ull << value_bits))
+        return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged_tq arguments");
+    const uint64_t needed_blocks = (kv_len + FHIP_PAGE_TOKENS - 1) / FHIP_PAGE_TOKENS;
+    if (num_blocks < needed_blocks)
+        return fail(FHIP_ERR_INVALID_SHAPE,
+                    "block table has %zu blocks for kv_len %zu", num_blocks,
+                    kv_len);
+    const uint64_t kpd = fhip_tq_packed_dim_per_head(hd, key_bits);
+    const uint64_t vpd = fhip_tq_packed_dim_per_head(hd, value_bits);
+    // Resolve the per-block tensors the table uses (all pool entries, as the reference does).
+    std::vector<const void*> ptrs(4 * pool_len > 0 ? 4 * pool_len : 1, nullptr);
+    for (size_t i = 0; i < pool_len; ++i) {
+        const fhip_tensor* ts[4] = {&k_packed[i], &k_norms[i], &v_packed[i], &v_norms[i]};
+        const uint64_t need[4] = {FHIP_PAGE_TOKENS * num_kv_heads * kpd,
+                                  FHIP_PAGE_TOKENS * num_kv_heads * 2,
+                                  FHIP_PAGE_TOKENS * num_kv_heads * vpd,
+                                  FHIP_PAGE_TOKENS * num_kv_heads * 2};
+        for (int k = 0; k < 4; ++k) {
+            void* p;
+            int r = b->get_ptr(ts[k]->id, &p);
+            if (r) return r;
+            if (size_bytes(ts[k]) < need[k])
+                return fail(FHIP_ERR_INVALID_SHAPE, "page tensor %s too small",
+                            shape_str(ts[k]).c_str());
+            ptrs[(size_t)k * pool_len + i] = p;
+        }
+    }
+    for (uint64_t i = 0; i < needed_blocks; ++i)
+        if (block_table[i] < 0 || (uint64_t)block_table[i] >= pool_len)
+            return fail(FHIP_ERR_INVALID_SHAPE, "block id %d outside the pool of %zu",
+                        block_table[i], pool_len);
+    if (T == 0) return FHIP_OK;
+    set_device(b);
+    std::lock_guard<std::mutex> g(b->launch_mu);
+    void *dbt, *dptr;
+    int s1, s2;
+    int r = b->stage(block_table, (needed_blocks ? needed_blocks : 1) * sizeof(int32_t), &dbt, &s1);
+    if (r) return r;
+    r = b->stage(ptrs.data(), ptrs.size() * sizeof(void*), &dptr, &s2);
+    if (r) return r;
+    const void** dp = (const void**)dptr;
+    int e = fhip_launch_attention_paged_tq(
+        po, pq, (const int*)dbt, dp, dp + pool_len, dp + 2 * pool_len, dp + 3 * pool_len,
+        (const float*)pkr, (const float*)pvr, (const float*)pkc, (const float*)pvc, (int)T, (int)qh,
+        (int)num_kv_heads, (int)hd, (int)kv_len, (int)start_pos, key_bits, value_bits, (int)kpd,
+        (int)vpd, b->stream);
+    b->stage_done(s1);
+    b->stage_done(s2);
+    if (e != hipSuccess) return hip_fail((hipError_t)e);
+    return FHIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,334 @@
+/*
+ * fracture_hip.h — C ABI of libfracture_hip.so, an MI355X (gfx950) implementation of the
+ * elementwise / reduction / TurboQuant hot path behind Fracture's `Backend` trait.
+ *
+ * Three groups of entry points:
+ *
+ *   1. Raw launchers `fhip_launch_*`: device pointers, int32 dims, asynchronous on the
+ *      given stream, no allocation, return 0 (hipSuccess) or a HIP error code. The first
+ *      eight replace, one for one, the `launch_*` symbols that the reference's Rust code
+ *      binds in backends/fracture-cuda/src/ffi.rs:141-274.
+ *   2. A handle runtime `fhip_*` that mirrors the `Backend` trait
+ *      (crates/fracture-core/src/backend.rs:8-223) over opaque tensor ids, plus the
+ *      inherent `CudaBackend` API (backends/fracture-cuda/src/lib.rs:76-161). Calls return
+ *      an FHIP_* status; `fhip_last_error()` gives the message of the calling thread's last
+ *      failure, worded like the reference's `FractureError` strings.
+ *   3. Host-only helpers (no GPU) for the TurboQuant tables the reference builds on the CPU
+ *      (crates/fracture-core/src/turboquant.rs:99-438) and the RoPE frequency table
+ *      (backends/fracture-cuda/src/lib.rs:133-155).
+ *
+ * Entry points marked "additive" have no counterpart in the reference's FFI; they cover the
+ * ops the reference runs on the CPU (softmax/argmax in crates/fracture-generate/src/
+ * sampling.rs:45-99), as two launches (add then rmsnorm, crates/fracture-engine/src/
+ * engine.rs:692-697) or only from tests (dequantize).
+ */
+#ifndef FRACTURE_HIP_H
+#define FRACTURE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* A hipStream_t; NULL means the default (null) stream. */
+typedef void* fhip_stream_t;
+
+/* Status codes of the handle runtime; the names follow fracture_core::FractureError
+ * (crates/fracture-core/src/error.rs:6-51). */
+enum {
+    FHIP_OK = 0,
+    FHIP_ERR_BACKEND = 1,           /* FractureError::Backend          */
+    FHIP_ERR_INVALID_SHAPE = 2,     /* FractureError::InvalidShape     */
+    FHIP_ERR_TENSOR_NOT_FOUND = 3,  /* FractureError::TensorNotFound   */
+    FHIP_ERR_OUT_OF_MEMORY = 4,     /* FractureError::OutOfMemory      */
+    FHIP_ERR_UNSUPPORTED_DTYPE = 5, /* FractureError::UnsupportedDType */
+    FHIP_ERR_GENERATION = 6         /* FractureError::Generation       */
+};
+
+/* Element types, in the order of fracture_core::DType (crates/fracture-core/src/dtype.rs:5-11). */
+enum { FHIP_FP16 = 0, FHIP_FP32 = 1, FHIP_BF16 = 2, FHIP_INT8 = 3, FHIP_INT4 = 4 };
+
+/* Flags written by the row argmax kernels (the sampler's NaN / Inf rejection,
+ * crates/fracture-generate/src/sampling.rs:51-56). */
+enum { FHIP_ROW_HAS_NAN = 1u, FHIP_ROW_HAS_INF = 2u };
+
+/* Tokens per KV page (block) of the paged caches
+ * (crates/fracture-engine/src/paged_kv_cache.rs:7, attention_paged_tq.cu:35). */
+#define FHIP_PAGE_TOKENS 16
+
+/* =====================================================================================
+ * 1. Raw launchers
+ * ===================================================================================== */
+
+/* ffi.rs:142-150 `launch_rmsnorm`: out[r,:] = fp16(x * rsqrt(mean(x^2) + eps) * w), fp16. */
+int fhip_launch_rmsnorm(void* output, const void* input, const void* weight, float eps, int rows,
+                        int cols, fhip_stream_t stream);
+
+/* ffi.rs:152-162 `launch_rope`: split-half rotary embedding in place on q [T,qh,hd] and
+ * k [T,kvh,hd] (fp16); positions u32[T] and freq_table f32[hd/2] in device memory. */
+int fhip_launch_rope(void* q, void* k, const uint32_t* positions, const float* freq_table,
+                     int num_tokens, int num_q_heads, int num_kv_heads, int head_dim,
+                     fhip_stream_t stream);
+
+/* ffi.rs:164-170 `launch_silu_mul`: out = fp16(silu(gate) * up), n elements. */
+int fhip_launch_silu_mul(void* output, const void* gate, const void* up, int n,
+                         fhip_stream_t stream);
+
+/* ffi.rs:202-210 `launch_embedding`: out[t,:] = table[ids[t],:]; ids >= vocab give zeros. */
+int fhip_launch_embedding(void* output, const void* table, const uint32_t* token_ids,
+                          int num_tokens, int hidden_dim, int vocab_size, fhip_stream_t stream);
+
+/* ffi.rs:212-218 `launch_add`: out = a + b, fp16 (round to nearest even). */
+int fhip_launch_add(void* output, const void* a, const void* b, int n, fhip_stream_t stream);
+
+/* ffi.rs:222-235 `launch_turboquant_compress`: per vector of input [N, kvh, hd] fp16:
+ * norm -> normalize -> y = rotation @ x_hat -> nearest centroid (first minimum) -> MSB-first
+ * bit-pack into packed_out [N, kvh*packed_dim_per_head]; norms_out [N, kvh] fp16.
+ * bits in 1..8 (the reference accepts 2, 4, 8; 3 is the MSB-first bitstream generalization). */
+int fhip_launch_turboquant_compress(const void* input, const float* rotation,
+                                    const float* centroids, void* packed_out, void* norms_out,
+                                    int num_tokens, int num_kv_heads, int head_dim, int n_levels,
+                                    int bits, int packed_dim_per_head, fhip_stream_t stream);
+
+/* ffi.rs:237-249 `launch_turboquant_decompress`: unpack -> centroid -> rotation^T @ y_hat ->
+ * fp16(x_hat * norm). */
+int fhip_launch_turboquant_decompress(const void* packed_in, const void* norms_in,
+                                      const float* rotation, const float* centroids,
+                                      void* output, int num_tokens, int num_kv_heads,
+                                      int head_dim, int bits, int packed_dim_per_head,
+                                      fhip_stream_t stream);
+
+/* ffi.rs:251-274 `launch_attention_paged_tq`: causal GQA attention of q [T, qh, hd] fp16 over
+ * TurboQuant pages given as per-block pointer arrays (device memory), with the query
+ * pre-rotated by k_rotation and the output unrotated by v_rotation^T. Unlike the reference
+ * kernel it keeps no kv_len-sized score row, so kv_len is bounded only by the block table. */
+int fhip_launch_attention_paged_tq(void* output, const void* q, const int* block_table,
+                                   const void** k_packed_ptrs, const void** k_norms_ptrs,
+                                   const void** v_packed_ptrs, const void** v_norms_ptrs,
+                                   const float* k_rotation, const float* v_rotation,
+                                   const float* k_centroids, const float* v_centroids,
+                                   int num_tokens, int num_q_heads, int num_kv_heads,
+                                   int head_dim, int kv_len, int start_pos, int key_bits,
+                                   int value_bits, int k_packed_dim_per_head,
+                                   int v_packed_dim_per_head, fhip_stream_t stream);
+
+/* --- additive raw launchers ---------------------------------------------------------- */
+
+/* dtype-generic forms of rmsnorm / add / silu_mul (FHIP_FP16, FHIP_BF16, FHIP_FP32). */
+int fhip_launch_rmsnorm_ex(void* output, const void* input, const void* weight, float eps,
+                           int rows, int cols, int dtype, fhip_stream_t stream);
+int fhip_launch_add_ex(void* output, const void* a, const void* b, int64_t n, int dtype,
+                       fhip_stream_t stream);
+int fhip_launch_silu_mul_ex(void* output, const void* gate, const void* up, int64_t n,
+                            int dtype, fhip_stream_t stream);
+/* rope for FHIP_FP16 / FHIP_BF16 / FHIP_FP32 q and k. */
+int fhip_launch_rope_ex(void* q, void* k, const uint32_t* positions, const float* freq_table,
+                        int num_tokens, int num_q_heads, int num_kv_heads, int head_dim,
+                        int dtype, fhip_stream_t stream);
+/* embedding of rows of elem_bytes-sized elements (2 for fp16/bf16, 4 for fp32). */
+int fhip_launch_embedding_ex(void* output, const void* table, const uint32_t* token_ids,
+                             int num_tokens, int hidden_dim, int vocab_size, int elem_bytes,
+                             fhip_stream_t stream);
+
+/* Fused residual add + RMSNorm, one HBM pass: residual = dtype(residual + delta) (in place,
+ * rounded before the norm reads it, as add.cu:13 then rmsnorm.cu:27 do), then
+ * normed_out = dtype(residual * rsqrt(mean(residual^2) + eps) * weight). */
+int fhip_launch_add_rmsnorm(void* residual, const void* delta, const void* weight, float eps,
+                            void* normed_out, int rows, int cols, int dtype,
+                            fhip_stream_t stream);
+
+/* Row softmax / argmax over fp32 logits [rows, cols] (the sampler's greedy and softmax paths,
+ * sampling.rs:45-82). argmax ties resolve to the LAST index (Iterator::max_by); flags_out
+ * gets FHIP_ROW_HAS_NAN / FHIP_ROW_HAS_INF per row. probs = exp(l/T - max) / sum.
+ * The workspace holds per-chunk partials; size it with fhip_rows_workspace_bytes. */
+size_t fhip_rows_workspace_bytes(int rows, int cols);
+int fhip_launch_softmax_rows(const float* logits, float* probs, int rows, int cols,
+                             float temperature, void* workspace, fhip_stream_t stream);
+int fhip_launch_argmax_rows(const float* logits, int32_t* index_out, uint32_t* flags_out,
+                            int rows, int cols, void* workspace, fhip_stream_t stream);
+int fhip_launch_softmax_argmax_rows(const float* logits, float* probs, int32_t* index_out,
+                                    uint32_t* flags_out, int rows, int cols, float temperature,
+                                    void* workspace, fhip_stream_t stream);
+
+/* TurboQuant quantize + pack of given fp32 rotated vectors y [rows, head_dim]: the code of
+ * each coordinate is the first index minimising |y - c| in fp32 (turboquant_compress.cu:
+ * 120-130), packed MSB-first. Bit-exact with the reference for any y and any centroids. */
+int fhip_launch_tq_quantize_pack(const float* y, const float* centroids, int n_levels, int bits,
+                                 void* packed_out, int rows, int head_dim,
+                                 int packed_dim_per_head, fhip_stream_t stream);
+
+/* The fp32 rotated unit vectors y and fp16 norms that fhip_launch_turboquant_compress
+ * quantizes, for the same input (identical arithmetic). */
+int fhip_launch_tq_rotate(const void* input, const float* rotation, float* y_out,
+                          void* norms_out, int rows, int head_dim, fhip_stream_t stream);
+
+/* Compress [N, kvh, hd] fp16 straight into 16-token pages of a contiguous pool:
+ * token t goes to page page_ids[(first_pos + t) / 16], slot (first_pos + t) % 16, in the
+ * layout of quantized_paged_kv_cache.rs:86-128 (packed [16, kvh*pd] u8, norms [16, kvh]
+ * fp16) with pool strides page_packed_bytes / page_norm_bytes (bytes between pages). */
+int fhip_launch_tq_compress_pages(const void* input, const float* rotation,
+                                  const float* centroids, int n_levels, int bits,
+                                  void* packed_pool, void* norms_pool, int64_t page_packed_bytes,
+                                  int64_t page_norm_bytes, const int32_t* page_ids, int num_pages,
+                                  int first_pos, int num_tokens, int num_kv_heads, int head_dim,
+                                  fhip_stream_t stream);
+
+/* launch_turboquant_decompress with an explicit codebook size (codes index only the first
+ * n_levels centroids; the reference form assumes 2^bits). */
+int fhip_launch_tq_dequant(const void* packed_in, const void* norms_in, const float* rotation,
+                           const float* centroids, int n_levels, void* output, int num_tokens,
+                           int num_kv_heads, int head_dim, int bits, int packed_dim_per_head,
+                           fhip_stream_t stream);
+
+/* Batched decode attention over a TurboQuant page pool: one query token per sequence,
+ * q [B, qh, hd] fp16, block_table [B, max_blocks] int32 (physical page ids), seq_lens [B]
+ * int32; pages in contiguous pools (strides in bytes between pages); positions whose page
+ * id is outside [0, num_pages) are masked out. Output [B, qh, hd] fp16; centroid tables
+ * hold 2^bits entries.
+ * The workspace holds split-K partials; size it with fhip_attention_tq_workspace_bytes. */
+size_t fhip_attention_tq_workspace_bytes(int batch, int num_q_heads, int head_dim,
+                                         int max_blocks);
+int fhip_launch_attention_tq_decode(void* output, const void* q, const int32_t* block_table,
+                                    const int32_t* seq_lens, int batch, int max_blocks,
+                                    int num_pages, const void* k_packed_pool, const void* k_norms_pool,
+                                    const void* v_packed_pool, const void* v_norms_pool,
+                                    int64_t page_k_packed_bytes, int64_t page_k_norm_bytes,
+                                    int64_t page_v_packed_bytes, int64_t page_v_norm_bytes,
+                                    const float* k_rotation, const float* v_rotation,
+                                    const float* k_centroids, const float* v_centroids,
+                                    int num_q_heads, int num_kv_heads, int head_dim,
+                                    int key_bits, int value_bits, void* workspace,
+                                    fhip_stream_t stream);
+
+/* =====================================================================================
+ * 2. Handle runtime (mirror of the Backend trait)
+ * ===================================================================================== */
+
+typedef struct fhip_backend fhip_backend;
+
+/* fracture_core::DeviceTensor (crates/fracture-core/src/tensor.rs:13-18) by value:
+ * an id, a row-major shape and a dtype. The backend resolves the id; callers never see
+ * device pointers. */
+#define FHIP_MAX_DIMS 8
+typedef struct {
+    uint64_t id;
+    int32_t dtype;
+    int32_t ndim;
+    uint64_t shape[FHIP_MAX_DIMS];
+} fhip_tensor;
+
+/* Message of the calling thread's most recent failing call (empty if none). */
+const char* fhip_last_error(void);
+
+/* CudaBackend::new (lib.rs:76-114) / Drop (lib.rs:164-182). */
+int fhip_backend_create(int device_id, fhip_backend** out);
+void fhip_backend_destroy(fhip_backend* b);
+
+/* CudaBackend::get_ptr (lib.rs:117-125) and ::stream (lib.rs:127-129). */
+int fhip_get_ptr(fhip_backend* b, uint64_t id, void** out);
+fhip_stream_t fhip_stream(fhip_backend* b);
+
+/* CudaBackend::precompute_rope_freqs (lib.rs:133-155). */
+int fhip_precompute_rope_freqs(fhip_backend* b, size_t head_dim, double theta);
+
+/* Backend::alloc / free / copy_to_device / copy_to_host (backend.rs:11-20). */
+int fhip_alloc(fhip_backend* b, const uint64_t* shape, int ndim, int dtype, fhip_tensor* out);
+int fhip_free(fhip_backend* b, const fhip_tensor* t);
+int fhip_copy_to_device(fhip_backend* b, const fhip_tensor* dst, const void* src, size_t src_len);
+int fhip_copy_to_host(fhip_backend* b, const fhip_tensor* src, void* dst, size_t dst_len);
+
+/* Backend::rmsnorm / rope / silu_mul / embedding / add / copy_rows (backend.rs:30-121). */
+int fhip_rmsnorm(fhip_backend* b, const fhip_tensor* input, const fhip_tensor* weight, double eps,
+                 const fhip_tensor* out);
+int fhip_rope(fhip_backend* b, const fhip_tensor* q, const fhip_tensor* k,
+              const uint32_t* positions, size_t num_positions, double theta, size_t head_dim);
+int fhip_silu_mul(fhip_backend* b, const fhip_tensor* gate, const fhip_tensor* up,
+                  const fhip_tensor* out);
+int fhip_embedding(fhip_backend* b, const uint32_t* token_ids, size_t num_tokens,
+                   const fhip_tensor* table, const fhip_tensor* out);
+int fhip_add(fhip_backend* b, const fhip_tensor* a, const fhip_tensor* bt, const fhip_tensor* out);
+int fhip_copy_rows(fhip_backend* b, const fhip_tensor* src, const fhip_tensor* dst,
+                   size_t src_offset, size_t dst_offset, size_t count);
+
+/* Backend::device_name / total_memory / available_memory / synchronize (backend.rs:126-135). */
+const char* fhip_device_name(fhip_backend* b);
+size_t fhip_total_memory(fhip_backend* b);
+size_t fhip_available_memory(fhip_backend* b);
+int fhip_synchronize(fhip_backend* b);
+
+/* Backend::create_timer / start_timer / stop_timer / destroy_timer (backend.rs:138-147);
+ * stop_timer synchronizes and returns elapsed milliseconds. */
+int fhip_create_timer(fhip_backend* b, uint64_t* timer_id);
+int fhip_start_timer(fhip_backend* b, uint64_t timer_id);
+int fhip_stop_timer(fhip_backend* b, uint64_t timer_id, float* ms_out);
+int fhip_destroy_timer(fhip_backend* b, uint64_t timer_id);
+
+/* Backend::marker_push / marker_pop (backend.rs:150-153): roctx ranges when libroctx64 is
+ * present, otherwise no-ops. */
+void fhip_marker_push(fhip_backend* b, const char* name);
+void fhip_marker_pop(fhip_backend* b);
+
+/* Backend::turboquant_compress (backend.rs:166-178). */
+int fhip_turboquant_compress(fhip_backend* b, const fhip_tensor* input, const fhip_tensor* rotation,
+                             const fhip_tensor* centroids, uint8_t bits,
+                             const fhip_tensor* packed_out, const fhip_tensor* norms_out);
+
+/* Backend::attention_paged_tq (backend.rs:200-222); the four per-block tensor lists are
+ * arrays of pool_len tensors indexed by physical block id. */
+int fhip_attention_paged_tq(fhip_backend* b, const fhip_tensor* q, const int32_t* block_table,
+                            size_t num_blocks, const fhip_tensor* k_packed,
+                            const fhip_tensor* k_norms, const fhip_tensor* v_packed,
+                            const fhip_tensor* v_norms, size_t pool_len,
+                            const fhip_tensor* k_rotation, const fhip_tensor* v_rotation,
+                            const fhip_tensor* k_centroids, const fhip_tensor* v_centroids,
+                            uint8_t key_bits, uint8_t value_bits, size_t num_kv_heads,
+                            size_t kv_len, size_t start_pos, const fhip_tensor* out);
+
+/* --- additive handle ops --------------------------------------------------------------- */
+
+/* Fused residual add + RMSNorm: residual += delta (in place), normed_out = rmsnorm(residual). */
+int fhip_add_rmsnorm(fhip_backend* b, const fhip_tensor* residual, const fhip_tensor* delta,
+                     const fhip_tensor* weight, double eps, const fhip_tensor* normed_out);
+/* probs [rows, vocab] fp32 from logits [rows, vocab] fp32. */
+int fhip_softmax_rows(fhip_backend* b, const fhip_tensor* logits, float temperature,
+                      const fhip_tensor* probs);
+/* Greedy tokens for each row, written to tokens_out (host, rows entries). Empty rows,
+ * NaN and Inf give FHIP_ERR_GENERATION with the sampler's messages. */
+int fhip_argmax_rows(fhip_backend* b, const fhip_tensor* logits, uint32_t* tokens_out,
+                     size_t rows);
+/* launch_turboquant_decompress through tensors: packed [N, kvh*pd] + norms [N, kvh] ->
+ * out [N, kvh, hd] fp16. */
+int fhip_tq_dequantize(fhip_backend* b, const fhip_tensor* packed, const fhip_tensor* norms,
+                       const fhip_tensor* rotation, const fhip_tensor* centroids, uint8_t bits,
+                       const fhip_tensor* out);
+/* quantize + pack of fp32 y [N, kvh, hd] (or [rows, hd]) into packed [N, kvh*pd]. */
+int fhip_tq_quantize_pack(fhip_backend* b, const fhip_tensor* y, const fhip_tensor* centroids,
+                          uint8_t bits, const fhip_tensor* packed_out);
+
+/* =====================================================================================
+ * 3. Host-only helpers (no GPU)
+ * ===================================================================================== */
+
+/* TurboQuantConfig::packed_dim_per_head (turboquant.rs:99-101): ceil(head_dim * bits / 8). */
+size_t fhip_tq_packed_dim_per_head(size_t head_dim, int bits);
+/* LloydMaxCodebook::compute (turboquant.rs:186-250): 2^bits centroids and 2^bits - 1
+ * boundaries for N(0, 1/dim). bits in 1..8. */
+int fhip_tq_codebook(int dim, int bits, float* centroids_out, float* boundaries_out);
+/* generate_rotation_matrix (turboquant.rs:306-338): d x d row-major Haar rotation. */
+int fhip_tq_rotation_matrix(int d, uint64_t seed, float* out);
+/* rotation_seeds (turboquant.rs:341-345). */
+void fhip_tq_rotation_seeds(uint64_t base_seed, uint64_t layer, uint64_t* k_seed,
+                            uint64_t* v_seed);
+/* The RoPE inverse-frequency table of precompute_rope_freqs (lib.rs:133-139), hd/2 floats. */
+void fhip_rope_freqs(int head_dim, double theta, float* out);
+
+/* Library version string. */
+const char* fhip_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FRACTURE_HIP_H */

@@ -1,0 +1,305 @@
+"""GPU parity of add, SwiGLU, RMSNorm, fused add+RMSNorm, RoPE and embedding against the
+oracle and the reference's fixture dumps.
+
+Tolerances (the reference's rule |a - e| <= atol + rtol*|e|):
+  fp16 outputs: rtol = atol = 1e-3; fp32: rtol = atol = 1e-5;
+  bf16 outputs: one bf16 unit in the last place (rtol 2^-7), since 1e-3 is finer than bf16
+  resolution, with at least 99.9% of elements bit-identical;
+  fixture dumps: the reference's own tolerances (5e-3 norms, 1e-3 silu, 0.01/0.025 rope).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import assert_close
+from fracture_amd import kernels as K
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float16: (1e-3, 1e-3), torch.float32: (1e-5, 1e-5)}
+NP = {torch.float16: np.float16, torch.float32: np.float32}
+
+
+def to_dev(a, dev, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    return t if dtype is None else t.to(dtype)
+
+
+def host(t):
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.uint16).cpu().numpy()
+    return t.cpu().numpy()
+
+
+def rand(shape, dtype, rng, scale=1.0):
+    x = (rng.standard_normal(shape) * scale).astype(np.float32)
+    if dtype == torch.bfloat16:
+        return oracle.f32_to_bf16_bits(x)
+    return x.astype(NP[dtype])
+
+
+def dev_tensor(a, dtype, dev):
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    return t.view(torch.bfloat16) if dtype == torch.bfloat16 else t
+
+
+def check(got, want, dtype, what):
+    if dtype == torch.bfloat16:
+        g, w = oracle.bf16_bits_to_f32(got), oracle.bf16_bits_to_f32(want)
+        assert_close(g, w, 2.0 ** -7, 1e-6, what)
+        assert np.mean(got == want) >= 0.999, f"{what}: bit-exact fraction {np.mean(got == want)}"
+    else:
+        rtol, atol = TOL[dtype]
+        assert_close(np.asarray(got, np.float32), np.asarray(want, np.float32), rtol, atol, what)
+
+
+DTYPES = [torch.float16, torch.bfloat16, torch.float32]
+
+
+# ---------------------------------------------------------------------------------------
+# add: bit-exact (one rounding of the exact sum)
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("n", [1, 7, 4096, 262147])
+def test_add_bit_exact(dev, dtype, n):
+    rng = np.random.default_rng(n)
+    a, b = rand(n, dtype, rng, 3.0), rand(n, dtype, rng, 3.0)
+    ta, tb = dev_tensor(a, dtype, dev), dev_tensor(b, dtype, dev)
+    out = torch.empty_like(ta)
+    K.add(out, ta, tb)
+    torch.cuda.synchronize()
+    got = host(out)
+    want = oracle.add(a, b)
+    assert np.array_equal(got.view(np.uint8), want.view(np.uint8))
+
+
+def test_add_unaligned_views(dev):
+    rng = np.random.default_rng(1)
+    a = rand(1001, torch.float16, rng)
+    b = rand(1001, torch.float16, rng)
+    ta, tb = to_dev(a, dev), to_dev(b, dev)
+    out = torch.zeros(1001, dtype=torch.float16, device=dev)
+    K.add(out[1:], ta[1:], tb[1:])  # 2-byte offsets: the scalar path
+    torch.cuda.synchronize()
+    assert np.array_equal(host(out)[1:].view(np.uint16), oracle.add(a[1:], b[1:]).view(np.uint16))
+
+
+# ---------------------------------------------------------------------------------------
+# SwiGLU
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(1, 5), (64, 14336), (8192, 1400)])
+def test_silu_mul(dev, dtype, shape):
+    rng = np.random.default_rng(sum(shape))
+    g, u = rand(shape, dtype, rng), rand(shape, dtype, rng)
+    tg, tu = dev_tensor(g, dtype, dev), dev_tensor(u, dtype, dev)
+    out = torch.empty_like(tg)
+    K.silu_mul(out, tg, tu)
+    torch.cuda.synchronize()
+    check(host(out), oracle.silu_mul(g, u), dtype, "silu_mul")
+
+
+def test_silu_mul_prefill_shape(dev):
+    # config 3 SwiGLU [8192, 14336] fp16, full size against the oracle
+    rng = np.random.default_rng(3)
+    g = rng.standard_normal((8192, 14336), dtype=np.float32).astype(np.float16)
+    u = rng.standard_normal((8192, 14336), dtype=np.float32).astype(np.float16)
+    tg, tu = to_dev(g, dev), to_dev(u, dev)
+    out = torch.empty_like(tg)
+    K.silu_mul(out, tg, tu)
+    torch.cuda.synchronize()
+    check(host(out), oracle.silu_mul(g, u), torch.float16, "silu_mul [8192,14336]")
+
+
+@pytest.mark.parametrize("case", ["prompt_0", "prompt_1", "decode_step_0"])
+def test_silu_mul_fixture(dev, golden, case):
+    for layer in range(4):
+        L = f"{case}/layer_{layer:02d}"
+        g = golden[f"{L}/gate"].reshape(-1, 256).astype(np.float16)
+        u = golden[f"{L}/up"].reshape(-1, 256).astype(np.float16)
+        tg, tu = to_dev(g, dev), to_dev(u, dev)
+        out = torch.empty_like(tg)
+        K.silu_mul(out, tg, tu)
+        torch.cuda.synchronize()
+        assert_close(host(out).astype(np.float32), golden[f"{L}/silu_mul"].reshape(-1, 256),
+                     1e-3, 1e-3, f"fixture silu_mul {L}")
+
+
+# ---------------------------------------------------------------------------------------
+# RMSNorm and fused add + RMSNorm
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(1, 4), (32, 4096), (64, 4096), (7, 4095), (3, 128),
+                                   (2, 16384), (5, 65536)])
+def test_rmsnorm(dev, dtype, shape):
+    rng = np.random.default_rng(shape[1])
+    x = rand(shape, dtype, rng)
+    wf = rng.uniform(0.5, 1.5, shape[1]).astype(np.float32)
+    w = oracle.f32_to_bf16_bits(wf) if dtype == torch.bfloat16 else wf.astype(NP[dtype])
+    tx, tw = dev_tensor(x, dtype, dev), dev_tensor(w, dtype, dev)
+    out = torch.empty_like(tx)
+    K.rmsnorm(out, tx, tw, 1e-5)
+    torch.cuda.synchronize()
+    check(host(out), oracle.rmsnorm(x, w, 1e-5), dtype, f"rmsnorm {shape}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(64, 4096), (32, 4096), (9, 1000), (1, 128)])
+def test_add_rmsnorm(dev, dtype, shape):
+    rng = np.random.default_rng(7 + shape[0])
+    h, d = rand(shape, dtype, rng), rand(shape, dtype, rng)
+    wf = rng.uniform(0.5, 1.5, shape[1]).astype(np.float32)
+    w = oracle.f32_to_bf16_bits(wf) if dtype == torch.bfloat16 else wf.astype(NP[dtype])
+    th, td, tw = dev_tensor(h, dtype, dev), dev_tensor(d, dtype, dev), dev_tensor(w, dtype, dev)
+    out = torch.empty_like(th)
+    K.add_rmsnorm(th, td, tw, 1e-5, out)
+    torch.cuda.synchronize()
+    h2, n2 = oracle.add_rmsnorm(h, d, w, 1e-5)
+    assert np.array_equal(host(th).view(np.uint8), h2.view(np.uint8)), "residual not bit-exact"
+    check(host(out), n2, dtype, "add_rmsnorm normed")
+
+
+def test_add_rmsnorm_prefill_shape(dev):
+    rng = np.random.default_rng(11)
+    h = rng.standard_normal((8192, 4096), dtype=np.float32).astype(np.float16)
+    d = rng.standard_normal((8192, 4096), dtype=np.float32).astype(np.float16)
+    w = rng.uniform(0.5, 1.5, 4096).astype(np.float16)
+    th, td, tw = to_dev(h, dev), to_dev(d, dev), to_dev(w, dev)
+    out = torch.empty_like(th)
+    K.add_rmsnorm(th, td, tw, 1e-5, out)
+    torch.cuda.synchronize()
+    h2, n2 = oracle.add_rmsnorm(h, d, w, 1e-5)
+    assert np.array_equal(host(th).view(np.uint16), h2.view(np.uint16))
+    check(host(out), n2, torch.float16, "add_rmsnorm [8192,4096]")
+
+
+def test_rmsnorm_known_answers(dev):
+    x = torch.tensor([[1.0, 2.0, 3.0, 4.0]], dtype=torch.float16, device=dev)
+    w = torch.ones(4, dtype=torch.float16, device=dev)
+    out = torch.empty_like(x)
+    K.rmsnorm(out, x, w, 1e-5)
+    want = np.array([1, 2, 3, 4]) / np.sqrt(7.5 + 1e-5)
+    assert np.abs(out.cpu().float().numpy()[0] - want).max() < 2e-3
+    z = torch.zeros((1, 4), dtype=torch.float16, device=dev)
+    K.rmsnorm(out, z, w, 1e-5)
+    assert not out.cpu().float().numpy().any()
+    big = torch.full((2, 64), 60000.0, dtype=torch.float16, device=dev)
+    o2 = torch.empty_like(big)
+    K.rmsnorm(o2, big, torch.ones(64, dtype=torch.float16, device=dev), 1e-5)
+    assert np.abs(o2.cpu().float().numpy() - 1.0).max() < 2e-3
+
+
+@pytest.mark.parametrize("case", ["prompt_0", "prompt_1", "decode_step_0"])
+def test_rmsnorm_fixture(dev, golden, case):
+    for layer in range(4):
+        L = f"{case}/layer_{layer:02d}"
+        for src, wname, dst in [("input_hidden", "attn_norm", "post_attn_norm"),
+                                ("post_attn_residual", "ffn_norm", "post_ffn_norm")]:
+            x = golden[f"{L}/{src}"].reshape(-1, 128).astype(np.float16)
+            w = golden[f"weights/blk.{layer}.{wname}.weight"]
+            tx, tw = to_dev(x, dev), to_dev(w, dev)
+            out = torch.empty_like(tx)
+            K.rmsnorm(out, tx, tw, 1e-5)
+            torch.cuda.synchronize()
+            assert_close(host(out).astype(np.float32), golden[f"{L}/{dst}"].reshape(-1, 128),
+                         5e-3, 5e-3, f"fixture {dst} {L}")
+
+
+# ---------------------------------------------------------------------------------------
+# RoPE
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("case", ["prompt_0", "prompt_1", "decode_step_0"])
+def test_rope_fixture(dev, golden, case):
+    cfg = golden["config"]
+    hd = cfg["head_dim"]
+    freqs = to_dev(oracle.rope_freqs(hd, cfg["rope_theta"]), dev)
+    for layer in range(4):
+        L = f"{case}/layer_{layer:02d}"
+        q = golden[f"{L}/q"].reshape(-1, cfg["num_q_heads"], hd).astype(np.float16)
+        k = golden[f"{L}/k"].reshape(-1, cfg["num_kv_heads"], hd).astype(np.float16)
+        T = q.shape[0]
+        pos = (golden[f"{case}/position_index"] if case.startswith("decode")
+               else np.arange(T)).astype(np.int32)
+        tq_, tk = to_dev(q, dev), to_dev(k, dev)
+        K.rope(tq_, tk, to_dev(pos, dev), freqs)
+        torch.cuda.synchronize()
+        assert_close(host(tq_).astype(np.float32), golden[f"{L}/q_rope"].reshape(q.shape), 0.01,
+                     0.025, "fixture q_rope")
+        assert_close(host(tk).astype(np.float32), golden[f"{L}/k_rope"].reshape(k.shape), 0.01,
+                     0.025, "fixture k_rope")
+        # and against the oracle at the 1e-3 rule
+        fr = oracle.rope_freqs(hd, cfg["rope_theta"])
+        assert_close(host(tq_).astype(np.float32), oracle.rope(q, pos, fr).astype(np.float32),
+                     1e-3, 1e-3, "q vs oracle")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("T,qh,kvh,hd", [(64, 32, 8, 128), (5, 4, 2, 32), (3, 2, 1, 20),
+                                          (17, 8, 0, 64)])
+def test_rope_vs_oracle(dev, dtype, T, qh, kvh, hd):
+    rng = np.random.default_rng(T * 100 + hd)
+    q = rand((T, qh, hd), dtype, rng)
+    k = rand((T, max(kvh, 1), hd), dtype, rng)[:, :kvh]
+    pos = rng.integers(0, 8192, T).astype(np.int32)
+    fr = oracle.rope_freqs(hd, 500000.0)
+    tq_, tk = dev_tensor(q, dtype, dev), dev_tensor(np.ascontiguousarray(k), dtype, dev)
+    K.rope(tq_, tk, to_dev(pos, dev), to_dev(fr, dev))
+    torch.cuda.synchronize()
+    check(host(tq_), oracle.rope(q, pos.astype(np.uint32), fr), dtype, "rope q")
+    if kvh:
+        check(host(tk), oracle.rope(np.ascontiguousarray(k), pos.astype(np.uint32), fr), dtype,
+              "rope k")
+
+
+def test_rope_position_zero_is_identity(dev):
+    rng = np.random.default_rng(2)
+    q = rng.standard_normal((4, 8, 128)).astype(np.float16)
+    tq_ = to_dev(q, dev)
+    tk = torch.empty((4, 0, 128), dtype=torch.float16, device=dev)
+    K.rope(tq_, tk, torch.zeros(4, dtype=torch.int32, device=dev),
+           to_dev(oracle.rope_freqs(128, 500000.0), dev))
+    assert np.array_equal(host(tq_).view(np.uint16), q.view(np.uint16))
+
+
+# ---------------------------------------------------------------------------------------
+# embedding gather: bit-exact
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("case", ["prompt_0", "prompt_1", "decode_step_0"])
+def test_embedding_fixture(dev, golden, case):
+    table = to_dev(golden["weights/token_embd.weight"], dev)
+    ids = golden[f"{case}/token_ids"].astype(np.int32)
+    out = torch.empty((ids.size, table.shape[1]), dtype=torch.float16, device=dev)
+    K.embedding(out, table, to_dev(ids, dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(host(out).astype(np.float32), golden[f"{case}/embeddings"].reshape(-1, 128))
+
+
+def test_embedding_llama_table(dev):
+    # [128256, 4096] fp16 (1.05 GB) with entries given by a closed form of (row, col)
+    V, H = 128256, 4096
+    rows = torch.arange(V, device=dev, dtype=torch.int64)[:, None]
+    cols = torch.arange(H, device=dev, dtype=torch.int64)[None, :]
+    bits = ((rows * 2654435761 + cols * 40503) % 30000).to(torch.int16)
+    table = bits.view(torch.float16)
+    rng = np.random.default_rng(9)
+    ids = np.concatenate([rng.integers(0, V, 60), [0, V - 1, V, 4000000000]]).astype(np.uint32)
+    out = torch.empty((ids.size, H), dtype=torch.float16, device=dev)
+    K.embedding(out, table, torch.from_numpy(ids.view(np.int32)).to(dev))
+    torch.cuda.synchronize()
+    got = out.view(torch.int16).cpu().numpy()
+    c = np.arange(H, dtype=np.int64)[None, :]
+    want = ((ids.astype(np.int64)[:, None] * 2654435761 + c * 40503) % 30000).astype(np.int16)
+    want[ids >= V] = 0
+    assert np.array_equal(got, want)
+
+
+def test_embedding_odd_width_scalar_path(dev):
+    rng = np.random.default_rng(3)
+    table = rng.standard_normal((50, 13)).astype(np.float16)
+    ids = np.array([3, 49, 50, 0, 7], np.int32)
+    out = torch.empty((5, 13), dtype=torch.float16, device=dev)
+    K.embedding(out, to_dev(table, dev), to_dev(ids, dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(host(out).view(np.uint16),
+                          oracle.embedding(table, ids.astype(np.uint32)).view(np.uint16))

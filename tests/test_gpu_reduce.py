@@ -1,0 +1,130 @@
+"""GPU parity of row softmax and argmax against the oracle's restatement of the sampler
+(crates/fracture-generate/src/sampling.rs:45-82).
+
+argmax: bit-exact index (ties -> last index) and NaN / Inf flags.
+softmax (fp32): the GPU sums each row with a tree, the sampler sequentially; at 128,256
+columns the sequential f32 sum carries up to ~3e-4 relative error in the row normaliser,
+so parity is checked as (a) every probability within rtol 1e-5 of the sampler's
+exp(x - max) divided by its row total, (b) rows sum to 1 within 1e-5, and (c) the plain
+|a-e| <= 1e-5 + 1e-5|e| rule wherever the sampler's own accumulation error is below 1e-6.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import assert_close
+from fracture_amd import kernels as K
+
+pytestmark = pytest.mark.gpu
+
+
+def spiky_logits(rows, cols, seed):
+    rng = np.random.default_rng(seed)
+    l = (rng.standard_normal((rows, cols)) * 3).astype(np.float32)
+    spikes = rng.integers(0, cols, rows)
+    l[np.arange(rows), spikes] += 20.0
+    return l, spikes
+
+
+def run_softmax(l, dev, T=1.0):
+    tl = torch.from_numpy(l).to(dev)
+    p = torch.empty_like(tl)
+    idx = torch.empty(l.shape[0], dtype=torch.int32, device=dev)
+    fl = torch.empty(l.shape[0], dtype=torch.int32, device=dev)
+    K.softmax_argmax_rows(tl, p, idx, fl, T)
+    torch.cuda.synchronize()
+    return p.cpu().numpy(), idx.cpu().numpy(), fl.cpu().numpy()
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 128256), (3, 1000), (1, 1), (5, 4097), (2, 7)])
+def test_softmax_vs_sampler(dev, rows, cols):
+    l, _ = spiky_logits(rows, cols, cols)
+    p, _, _ = run_softmax(l, dev)
+    ref = oracle.softmax_rows(l)
+    ref_norm = ref / ref.sum(1, dtype=np.float64, keepdims=True)
+    np.testing.assert_allclose(p, ref_norm, rtol=1e-5, atol=0)
+    np.testing.assert_allclose(p.sum(1, dtype=np.float64), 1.0, atol=1e-5)
+    if cols <= 4097:
+        assert_close(p, ref, 1e-5, 1e-5, "softmax")
+
+
+def test_softmax_temperature(dev):
+    l, _ = spiky_logits(4, 3000, 1)
+    p, _, _ = run_softmax(l, dev, 0.7)
+    ref = oracle.softmax_rows(l, 0.7)
+    np.testing.assert_allclose(p, ref / ref.sum(1, dtype=np.float64, keepdims=True), rtol=1e-5)
+
+
+def test_softmax_unaligned_width(dev):
+    l, _ = spiky_logits(3, 1001, 2)
+    tl = torch.from_numpy(l).to(dev)
+    p = torch.empty_like(tl)
+    K.softmax_rows(tl, p)
+    torch.cuda.synchronize()
+    ref = oracle.softmax_rows(l)
+    np.testing.assert_allclose(p.cpu().numpy(), ref / ref.sum(1, dtype=np.float64, keepdims=True),
+                               rtol=1e-5)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 128256), (7, 33), (1, 1), (2, 4096), (3, 4097)])
+def test_argmax_bit_exact_with_ties(dev, rows, cols):
+    rng = np.random.default_rng(rows * cols)
+    l = rng.integers(-50, 50, (rows, cols)).astype(np.float32)  # many equal maxima
+    if cols > 10:
+        for r in range(rows):  # three equal planted maxima per row
+            at = rng.choice(cols, 3, replace=False)
+            l[r, at] = 1000.0
+    tl = torch.from_numpy(l).to(dev)
+    idx = torch.empty(rows, dtype=torch.int32, device=dev)
+    fl = torch.empty(rows, dtype=torch.int32, device=dev)
+    K.argmax_rows(tl, idx, fl)
+    torch.cuda.synchronize()
+    want, status = oracle.argmax_rows(l)
+    assert (status == 0).all()
+    assert np.array_equal(idx.cpu().numpy(), want.astype(np.int32))
+    assert not fl.cpu().numpy().any()
+
+
+def test_argmax_signed_zero_ties(dev):
+    l = np.array([[-1.0, 0.0, -0.0, -2.0], [-1.0, -0.0, 0.0, -3.0]], np.float32)
+    tl = torch.from_numpy(l).to(dev)
+    idx = torch.empty(2, dtype=torch.int32, device=dev)
+    fl = torch.empty(2, dtype=torch.int32, device=dev)
+    K.argmax_rows(tl, idx, fl)
+    assert list(idx.cpu().numpy()) == [2, 2]
+
+
+def test_argmax_flags(dev):
+    l = np.zeros((4, 9000), np.float32)
+    l[0, 5000] = np.nan
+    l[1, 8999] = np.inf
+    l[2, 3] = -np.inf
+    l[3, 100] = 5.0
+    tl = torch.from_numpy(l).to(dev)
+    idx = torch.empty(4, dtype=torch.int32, device=dev)
+    fl = torch.empty(4, dtype=torch.int32, device=dev)
+    K.argmax_rows(tl, idx, fl)
+    torch.cuda.synchronize()
+    assert list(fl.cpu().numpy()) == [1, 2, 2, 0]
+    assert idx.cpu().numpy()[3] == 100
+
+
+def test_fused_softmax_argmax_matches_greedy(dev):
+    l, spikes = spiky_logits(64, 128256, 5)
+    _, idx, fl = run_softmax(l, dev)
+    want, _ = oracle.argmax_rows(l)
+    assert np.array_equal(idx, want.astype(np.int32)) and np.array_equal(idx, spikes)
+    assert not fl.any()
+
+
+@pytest.mark.parametrize("case", ["prompt_0", "prompt_1", "decode_step_0"])
+def test_fixture_greedy_tokens(dev, golden, case):
+    l = np.ascontiguousarray(golden[f"{case}/logits"].reshape(-1, 256))
+    tl = torch.from_numpy(l).to(dev)
+    idx = torch.empty(l.shape[0], dtype=torch.int32, device=dev)
+    fl = torch.empty(l.shape[0], dtype=torch.int32, device=dev)
+    K.argmax_rows(tl, idx, fl)
+    torch.cuda.synchronize()
+    assert int(idx.cpu().numpy()[-1]) == int(golden[f"{case}/greedy_token"][0])
+    assert np.array_equal(idx.cpu().numpy(), oracle.argmax_rows(l)[0].astype(np.int32))

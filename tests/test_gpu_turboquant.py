@@ -1,0 +1,264 @@
+"""GPU parity of the TurboQuant pipeline against the oracle.
+
+* quantize + pack of given fp32 y: bit-exact codes and bytes, any y (adversarial values at
+  centroids, midpoints and their neighbours, NaN, +-inf, huge), any bit width 1..8, any
+  head_dim, sorted or unsorted centroids;
+* compress: bit-exact bytes given the kernel's own fp32 rotated vectors (the rotate entry
+  runs the identical arithmetic), and against the oracle's own rotation only rounding-level
+  code flips at decision boundaries;
+* rotate: fp32 y within 3e-6 absolute of the oracle (|y| <= 1), norms within one fp16 ulp;
+* dequantize: fp16 output within the 1e-3 rule of the oracle on identical packed input;
+* round trips at the reference GPU tests' cosine thresholds (turboquant_gpu.rs:157-160,
+  236-239, 418-421) and the page writer against the flat compress.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import assert_close
+from fracture_amd import kernels as K
+from fracture_amd import turboquant as tq
+
+pytestmark = pytest.mark.gpu
+
+SIG = 1.0 / np.sqrt(128.0)
+
+
+def dev_t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def adversarial_y(c, rng, n):
+    c = c.astype(np.float32)
+    mids = ((c[:-1].astype(np.float64) + c[1:]) / 2).astype(np.float32)
+    up = np.nextafter(mids, np.float32(np.inf))
+    dn = np.nextafter(mids, np.float32(-np.inf))
+    special = np.array([0.0, -0.0, np.nan, -np.nan, np.inf, -np.inf, 1e30, -1e30, 3.0e38,
+                        1e-40, -1e-40, 1e4, -1e4], np.float32)
+    return np.concatenate([rng.standard_normal(n).astype(np.float32) * SIG,
+                           rng.standard_normal(n // 8).astype(np.float32), c, mids, up, dn,
+                           special]).astype(np.float32)
+
+
+def run_qp(y, cent, bits, dev):
+    hd = y.shape[-1]
+    rows = y.shape[0]
+    pd = K.packed_dim(hd, bits)
+    ty, tc = dev_t(y, dev), dev_t(cent, dev)
+    packed = torch.zeros((rows, pd), dtype=torch.uint8, device=dev)
+    K.tq_quantize_pack(ty, tc, bits, packed)
+    torch.cuda.synchronize()
+    return packed.cpu().numpy()
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4, 8])
+@pytest.mark.parametrize("hd", [128, 96, 5])
+def test_quantize_pack_bit_exact(dev, bits, hd):
+    rng = np.random.default_rng(bits * 1000 + hd)
+    cent = tq.codebook(128, bits)[0]
+    vals = adversarial_y(cent, rng, 6000)
+    rows = (vals.size + hd - 1) // hd
+    y = np.resize(vals, rows * hd).reshape(rows, hd)
+    rng.shuffle(y.reshape(-1))
+    got = run_qp(y, cent, bits, dev)
+    want = oracle.tq_quantize_pack(y, cent, bits)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("kind", ["shuffled", "duplicates", "tiny_gaps", "nan", "short"])
+def test_quantize_pack_unusual_codebooks(dev, kind):
+    rng = np.random.default_rng(17)
+    bits = 4
+    cent = tq.codebook(128, bits)[0].copy()
+    if kind == "shuffled":
+        rng.shuffle(cent)
+    elif kind == "duplicates":
+        cent[5] = cent[6]
+    elif kind == "tiny_gaps":
+        cent = (np.arange(16, dtype=np.float32) - 8) * np.float32(1e-30)
+    elif kind == "nan":
+        cent[3] = np.nan
+    elif kind == "short":
+        cent = cent[:11]  # fewer levels than 2^bits
+    y = adversarial_y(np.sort(cent[np.isfinite(cent)]), rng, 2000)
+    y = np.resize(y, (y.size // 128 + 1) * 128).reshape(-1, 128)
+    assert np.array_equal(run_qp(y, cent, bits, dev), oracle.tq_quantize_pack(y, cent, bits))
+
+
+def rotate(x, rot, dev):
+    tx, tr = dev_t(x, dev), dev_t(rot, dev)
+    rows, hd = x.size // x.shape[-1], x.shape[-1]
+    y = torch.empty((rows, hd), dtype=torch.float32, device=dev)
+    n = torch.empty(rows, dtype=torch.float16, device=dev)
+    K.tq_rotate(tx, tr, y, n)
+    torch.cuda.synchronize()
+    return y.cpu().numpy(), n.cpu().numpy()
+
+
+def compress(x, rot, cent, bits, dev):
+    N, H, hd = x.shape
+    tx, tr, tc = dev_t(x, dev), dev_t(rot, dev), dev_t(cent, dev)
+    packed = torch.empty((N, H * K.packed_dim(hd, bits)), dtype=torch.uint8, device=dev)
+    norms = torch.empty((N, H), dtype=torch.float16, device=dev)
+    K.tq_compress(tx, tr, tc, bits, packed, norms)
+    torch.cuda.synchronize()
+    return packed.cpu().numpy(), norms.cpu().numpy()
+
+
+def kv(rng, N, H, hd):
+    return (rng.standard_normal((N, H, hd)) * np.exp(rng.normal(0, 0.5, (N, 1, 1)))).astype(np.float16)
+
+
+@pytest.mark.parametrize("hd", [128, 16, 64])
+def test_rotate_vs_oracle(dev, hd):
+    rng = np.random.default_rng(hd)
+    x = kv(rng, 257, 3, hd)
+    rot = tq.rotation_matrix(hd, 42)
+    y, n = rotate(x, rot, dev)
+    yo, no = oracle.tq_rotate(x, rot)
+    assert np.abs(y - yo).max() < 3e-6
+    ulp = np.abs(n.view(np.uint16).astype(np.int32) - no.view(np.uint16).astype(np.int32))
+    assert ulp.max() <= 1
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
+@pytest.mark.parametrize("hd", [128, 16])
+def test_compress_bit_exact_given_kernel_y(dev, bits, hd):
+    rng = np.random.default_rng(bits + hd)
+    x = kv(rng, 301, 8, hd)
+    rot = tq.rotation_matrix(hd, 542)
+    cent = tq.codebook(hd, bits)[0]
+    packed, norms = compress(x, rot, cent, bits, dev)
+    y, n = rotate(x, rot, dev)
+    assert np.array_equal(norms.reshape(-1).view(np.uint16), n.view(np.uint16))
+    assert np.array_equal(packed.reshape(-1, K.packed_dim(hd, bits)),
+                          oracle.tq_quantize_pack(y, cent, bits))
+
+
+@pytest.mark.parametrize("bits", [3, 4])
+def test_compress_vs_oracle_rotation(dev, bits):
+    rng = np.random.default_rng(99)
+    hd = 128
+    x = kv(rng, 512, 8, hd)
+    rot = tq.rotation_matrix(hd, 42)
+    cent = tq.codebook(hd, bits)[0]
+    packed, norms = compress(x, rot, cent, bits, dev)
+    po, no, yo = oracle.tq_compress(x, rot, cent, bits)
+    got = oracle.tq_unpack_rows(packed.reshape(-1, K.packed_dim(hd, bits))[:64], hd, bits)
+    want = oracle.tq_unpack_rows(po[:64], hd, bits)
+    diff = got != want
+    # Codes differ only where the two fp32 rotations round y across a decision boundary.
+    assert diff.mean() < 1e-3
+    if diff.any():
+        r, d = np.nonzero(diff)
+        a, b = np.minimum(got[r, d], want[r, d]), np.maximum(got[r, d], want[r, d])
+        assert (b - a == 1).all()
+        mid = (cent[a].astype(np.float64) + cent[b]) / 2
+        assert np.abs(yo[r, d] - mid).max() < 3e-6
+    ulp = np.abs(norms.reshape(-1).view(np.uint16).astype(np.int32) - no.view(np.uint16).astype(np.int32))
+    assert ulp.max() <= 1
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
+@pytest.mark.parametrize("hd", [128, 16])
+def test_dequant_vs_oracle(dev, bits, hd):
+    rng = np.random.default_rng(bits * 7 + hd)
+    x = kv(rng, 200, 8, hd)
+    rot = tq.rotation_matrix(hd, 42)
+    cent = tq.codebook(hd, bits)[0]
+    po, no, _ = oracle.tq_compress(x, rot, cent, bits)
+    out = torch.empty((200, 8, hd), dtype=torch.float16, device=dev)
+    K.tq_dequant(dev_t(po, dev), dev_t(no, dev), dev_t(rot, dev), dev_t(cent, dev), bits, out)
+    torch.cuda.synchronize()
+    want = oracle.tq_dequant(po, no, rot, cent, bits, hd)
+    assert_close(out.cpu().numpy().reshape(-1, hd).astype(np.float32), want.astype(np.float32),
+                 1e-3, 1e-3, "dequant")
+
+
+def cos(a, b):
+    a = a.astype(np.float64).reshape(-1, a.shape[-1])
+    b = b.astype(np.float64).reshape(-1, b.shape[-1])
+    return (a * b).sum(1) / (np.linalg.norm(a, axis=1) * np.linalg.norm(b, axis=1))
+
+
+@pytest.mark.parametrize("bits,thr", [(8, 0.999), (4, 0.95), (3, 0.93), (2, 0.80)])
+@pytest.mark.parametrize("hd", [128, 16])
+def test_roundtrip_cosine(dev, bits, thr, hd):
+    rng = np.random.default_rng(bits)
+    x = kv(rng, 128, 8, hd)
+    rot = tq.rotation_matrix(hd, 42)
+    cent = tq.codebook(hd, bits)[0]
+    packed, norms = compress(x, rot, cent, bits, dev)
+    out = torch.empty((128, 8, hd), dtype=torch.float16, device=dev)
+    K.tq_dequant(dev_t(packed, dev), dev_t(norms, dev), dev_t(rot, dev), dev_t(cent, dev), bits,
+                 out)
+    torch.cuda.synchronize()
+    c = cos(out.cpu().numpy(), x)
+    assert c.min() > thr
+    nrm = np.linalg.norm(x.astype(np.float64).reshape(-1, hd), axis=1)
+    assert np.abs(norms.reshape(-1).astype(np.float64) / nrm - 1).max() < 0.02
+
+
+def test_zero_vectors(dev):
+    x = np.zeros((4, 2, 128), np.float16)
+    rot = tq.rotation_matrix(128, 42)
+    cent = tq.codebook(128, 4)[0]
+    packed, norms = compress(x, rot, cent, 4, dev)
+    assert np.array_equal(packed.reshape(-1, 64), oracle.tq_compress(x, rot, cent, 4)[0])
+    out = torch.empty((4, 2, 128), dtype=torch.float16, device=dev)
+    K.tq_dequant(dev_t(packed, dev), dev_t(norms, dev), dev_t(rot, dev), dev_t(cent, dev), 4, out)
+    o = out.cpu().numpy().astype(np.float32)
+    assert not np.isnan(o).any() and not o.any()
+
+
+@pytest.mark.parametrize("bits", [4, 3])
+def test_layer_scale_kv_compress(dev, bits):
+    """One layer of Llama-3.1-8B K at 32768 tokens x 8 kv heads: bytes bit-exact given the
+    kernel's rotation, every vector's round-trip cosine above the threshold."""
+    rng = np.random.default_rng(12345)
+    N, H, hd = 32768, 8, 128
+    x = (rng.standard_normal((N, H, hd), dtype=np.float32) *
+         np.exp(rng.normal(0, 0.5, (N, 1, 1))).astype(np.float32)).astype(np.float16)
+    rot = tq.rotation_matrix(hd, 42)
+    cent = tq.codebook(hd, bits)[0]
+    packed, norms = compress(x, rot, cent, bits, dev)
+    y, n = rotate(x, rot, dev)
+    assert np.array_equal(packed.reshape(N * H, -1), oracle.tq_quantize_pack(y, cent, bits))
+    assert np.array_equal(norms.reshape(-1).view(np.uint16), n.view(np.uint16))
+    out = torch.empty((N, H, hd), dtype=torch.float16, device=dev)
+    K.tq_dequant(dev_t(packed, dev), dev_t(norms, dev), dev_t(rot, dev), dev_t(cent, dev), bits,
+                 out)
+    torch.cuda.synchronize()
+    assert cos(out.cpu().numpy(), x).min() > (0.95 if bits == 4 else 0.93)
+
+
+@pytest.mark.parametrize("first_pos", [0, 5, 16])
+def test_page_writer_equals_flat_compress(dev, first_pos):
+    rng = np.random.default_rng(first_pos)
+    T, H, hd, bits = 70, 8, 128, 4
+    pd = K.packed_dim(hd, bits)
+    x = kv(rng, T, H, hd)
+    rot = tq.rotation_matrix(hd, 42)
+    cent = tq.codebook(hd, bits)[0]
+    npages = 12
+    nblocks = (first_pos + T + 15) // 16
+    page_ids = rng.permutation(npages)[:nblocks].astype(np.int32)
+    page_ids[-1] = npages + 5  # out of range: those tokens are skipped
+    kp = torch.full((npages, 16, H * pd), 0xAB, dtype=torch.uint8, device=dev)
+    kn = torch.full((npages, 16, H), 7.0, dtype=torch.float16, device=dev)
+    K.tq_compress_pages(dev_t(x, dev), dev_t(rot, dev), dev_t(cent, dev), bits, kp, kn,
+                        dev_t(page_ids, dev), first_pos)
+    torch.cuda.synchronize()
+    flat_p, flat_n = compress(x, rot, cent, bits, dev)
+    KP, KN = kp.cpu().numpy(), kn.cpu().numpy()
+    written = np.zeros((npages, 16), bool)
+    for t in range(T):
+        pos = first_pos + t
+        page, slot = page_ids[pos // 16], pos % 16
+        if page >= npages:
+            continue
+        written[page, slot] = True
+        assert np.array_equal(KP[page, slot], flat_p[t])
+        assert np.array_equal(KN[page, slot].view(np.uint16), flat_n[t].view(np.uint16))
+    assert (KP[~written] == 0xAB).all() and (KN[~written] == 7.0).all()
