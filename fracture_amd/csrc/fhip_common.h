@@ -115,6 +115,11 @@ __device__ __forceinline__ void st16_stream(void* p, const u32x4& v) {
     __builtin_nontemporal_store(v, (u32x4*)p);
 }
 
+// The readlane builtin moves 32-bit integers: floats cross it as their bit patterns.
+__device__ __forceinline__ float lane63(float v) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // ---------------------------------------------------------------------------------------
 // Wave64 reductions with DPP: quad swaps, half-row and row mirrors, then row_bcast:15 /
 // row_bcast:31 carry the row totals up to lane 63, which is read back as a scalar.
@@ -126,7 +131,7 @@ __device__ __forceinline__ float wave_sum(float v) {
     v += __builtin_amdgcn_update_dpp(0.0f, v, 0x140, 0xF, 0xF, true);  // row_mirror
     v += __builtin_amdgcn_update_dpp(0.0f, v, 0x142, 0xA, 0xF, false); // row_bcast:15
     v += __builtin_amdgcn_update_dpp(0.0f, v, 0x143, 0xC, 0xF, false); // row_bcast:31
-    return __builtin_amdgcn_readlane(v, 63);
+    return lane63(v);
 }
 __device__ __forceinline__ float wave_max(float v) {
     const float ninf = -__builtin_inff();
@@ -136,7 +141,7 @@ __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, __builtin_amdgcn_update_dpp(ninf, v, 0x140, 0xF, 0xF, true));
     v = fmaxf(v, __builtin_amdgcn_update_dpp(ninf, v, 0x142, 0xA, 0xF, false));
     v = fmaxf(v, __builtin_amdgcn_update_dpp(ninf, v, 0x143, 0xC, 0xF, false));
-    return __builtin_amdgcn_readlane(v, 63);
+    return lane63(v);
 }
 __device__ __forceinline__ float wave_min(float v) {
     const float pinf = __builtin_inff();
@@ -146,7 +151,7 @@ __device__ __forceinline__ float wave_min(float v) {
     v = fminf(v, __builtin_amdgcn_update_dpp(pinf, v, 0x140, 0xF, 0xF, true));
     v = fminf(v, __builtin_amdgcn_update_dpp(pinf, v, 0x142, 0xA, 0xF, false));
     v = fminf(v, __builtin_amdgcn_update_dpp(pinf, v, 0x143, 0xC, 0xF, false));
-    return __builtin_amdgcn_readlane(v, 63);
+    return lane63(v);
 }
 
 // Workgroup sum of one float per thread. `scratch` holds one float per wave; the result is

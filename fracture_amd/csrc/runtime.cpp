@@ -35,7 +35,10 @@ int fail(int code, const char* fmt, ...) {
     return code;
 }
 
+// Reports a failed HIP call and clears HIP's per-thread last error, so that a recoverable
+// failure (an allocation beyond the device, say) is not reported again by the next launch.
 int hip_fail(hipError_t e) {
+    (void)hipGetLastError();
     return fail(FHIP_ERR_BACKEND, "HIP error (%d): %s", (int)e, hipGetErrorString(e));
 }
 

@@ -114,7 +114,9 @@ def test_fused_softmax_argmax_matches_greedy(dev):
     l, spikes = spiky_logits(64, 128256, 5)
     _, idx, fl = run_softmax(l, dev)
     want, _ = oracle.argmax_rows(l)
-    assert np.array_equal(idx, want.astype(np.int32)) and np.array_equal(idx, spikes)
+    assert np.array_equal(idx, want.astype(np.int32))
+    # the +20 spike is the maximum of its row unless another N(0, 3) draw beats it
+    assert np.mean(idx == spikes) > 0.9
     assert not fl.any()
 
 
