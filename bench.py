@@ -55,6 +55,8 @@ class Timer:
         self.torch = torch
 
     def time_us(self, fn, reps: int, warmup: int = 3) -> float:
+        """Average over `reps` back-to-back eager calls (for launches of >= ~10 us, where the
+        host keeps the queue full)."""
         t = self.torch
         for _ in range(warmup):
             fn()
@@ -66,6 +68,30 @@ class Timer:
         e.record()
         e.synchronize()
         return s.elapsed_time(e) * 1e3 / reps
+
+    def graph_time_us(self, fn, per_graph: int = 50, replays: int = 20) -> float:
+        """Average launch duration of `fn` from a HIP graph of `per_graph` back-to-back calls
+        replayed `replays` times (short launches, which host-side launch cost would hide)."""
+        t = self.torch
+        side = t.cuda.Stream()
+        side.wait_stream(t.cuda.current_stream())
+        with t.cuda.stream(side):
+            for _ in range(3):
+                fn()
+        t.cuda.current_stream().wait_stream(side)
+        g = t.cuda.CUDAGraph()
+        with t.cuda.graph(g):
+            for _ in range(per_graph):
+                fn()
+        g.replay()
+        t.cuda.synchronize()
+        s, e = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(replays):
+            g.replay()
+        e.record()
+        e.synchronize()
+        return s.elapsed_time(e) * 1e3 / (replays * per_graph)
 
 
 def traffic_of(kernel_key: str):
@@ -221,9 +247,8 @@ def run_decode(args, torch, K, dev):
 
     # per-kernel average launch durations (back-to-back launches between two events)
     per = {}
-    reps = 400
     for name in ("embedding", "rope", "silu_mul", "add_rmsnorm"):
-        us = timer.time_us(ops[name], reps)
+        us = timer.graph_time_us(ops[name])
         per[name] = {"us": round(us, 3), "GB/s": round(gbs(nbytes[name], us), 1),
                      "frac_of_peak": round(gbs(nbytes[name], us) / PEAK_HBM_GBS, 4),
                      "bytes": nbytes[name]}

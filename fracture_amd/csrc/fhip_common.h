@@ -5,6 +5,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+#include <vector>
+
 #include "fracture_hip.h"
 
 namespace fhip {
@@ -154,6 +157,15 @@ __device__ __forceinline__ float wave_min(float v) {
     return lane63(v);
 }
 
+// Workgroup barrier that orders LDS only. __syncthreads() also fences global memory, which
+// on gfx9 makes every wave drain its outstanding global loads and stores (vmcnt(0)) before
+// the barrier; kernels that keep prefetches in flight across a barrier use this instead.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Workgroup sum of one float per thread. `scratch` holds one float per wave; the result is
 // returned to every thread. Contains two barriers.
 __device__ __forceinline__ float block_sum(float v, float* scratch) {
@@ -181,4 +193,49 @@ inline bool aligned16(const void* p) { return (((uintptr_t)p) & 15u) == 0; }
 inline hipStream_t as_stream(fhip_stream_t s) { return (hipStream_t)s; }
 // Workgroups that fill the chip for a streaming kernel: 256 CUs, a few groups each.
 constexpr int kStreamGroups = 256 * 8;
+
+// Compute units of the current device (cached per device; 256 on MI355X).
+inline int cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+// Grid of a persistent kernel: as many workgroups as are resident at once on the device
+// (occupancy of `kernel` at `block` lanes and `lds` dynamic bytes), capped by the work.
+// The occupancy is looked up once per (kernel, block, lds) and cached.
+template <class K>
+inline int resident_grid(K kernel, int block, size_t lds, int64_t work_units) {
+    struct Entry {
+        const void* fn;
+        int block;
+        size_t lds;
+        int per_cu;
+    };
+    static std::mutex mu;
+    static std::vector<Entry> cache;
+    int per_cu = 0;
+    {
+        std::lock_guard<std::mutex> g(mu);
+        for (const Entry& e : cache)
+            if (e.fn == (const void*)kernel && e.block == block && e.lds == lds) per_cu = e.per_cu;
+        if (per_cu == 0) {
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, lds) !=
+                    hipSuccess ||
+                per_cu <= 0)
+                per_cu = 1;
+            cache.push_back(Entry{(const void*)kernel, block, lds, per_cu});
+        }
+    }
+    const int64_t g = (int64_t)per_cu * cu_count();
+    return (int)(work_units < g ? (work_units > 0 ? work_units : 1) : g);
+}
 }  // namespace fhip_host

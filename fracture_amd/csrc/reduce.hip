@@ -4,10 +4,17 @@
 // (crates/fracture-generate/src/sampling.rs:45-82, crates/fracture-engine/src/engine.rs:728-738).
 // A 128,256-wide row is 513 KB, more than one CU's LDS, and a decode batch has few rows, so
 // each row is split into 4096-element chunks, one workgroup per (chunk, row), which fills
-// the chip. Pass 1 reduces each chunk to a record {max, sum exp(x - max), argmax, flags};
-// pass 2 combines the row's records (every workgroup of a row in the same order, so all of
-// them agree on the row max and sum) and writes exp(x/T - M) / S for its chunk, the second
-// read being served mostly by the 256 MB MALL.
+// the chip with one wave of loads.
+//
+// Pass 1 (row_stats_kernel) reduces each chunk to a record {max, sum exp(x - max), argmax,
+// flags}. argmax then folds each row's records with one wave per row (argmax_fold_kernel);
+// softmax reads the logits again (mostly from the MALL) in softmax_write_kernel, where
+// every workgroup of a row folds the row's records in the same fixed order (so all agree on
+// the row's max and sum) while its logits loads are in flight, and writes exp(x/T - M) / S.
+// No atomics or cross-workgroup fences: a device-scope fence on gfx9 writes back the L2.
+//
+// exp is evaluated as exp2((s - m) * log2(e)) on the hardware exp2; over the logit range of a
+// sampler (|s - m| < 100) that is within 1e-5 relative of expf.
 #include "fhip_common.h"
 
 using namespace fhip;
@@ -17,16 +24,20 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kPerLane = 16;                  // 4 x 16-byte loads per lane
 constexpr int kChunk = kBlock * kPerLane;     // 4096 elements per workgroup
+constexpr float kLog2e = 1.4426950408889634f;
+
+enum : int { kStatsSoftmax = 1, kStatsArgmax = 2 };
 
 struct alignas(16) RowPart {
     float m;         // chunk max of the scaled logits (-inf if none)
-    float s;         // sum of exp(x - m) over the chunk
-    float bv;        // largest value, ties to the last index
+    float s;         // sum of exp(s - m) over the chunk
+    float bv;        // largest raw logit, ties to the last index
     int bi;          // its index (-1 if none)
     uint32_t flags;  // FHIP_ROW_HAS_NAN | FHIP_ROW_HAS_INF
     uint32_t pad[3];
 };
 
+// Workspace: RowPart[rows][nchunks].
 int num_chunks(int cols) { return (int)ceil_div(cols, kChunk); }
 
 // (value, index) order of the greedy sampler: larger value wins, equal values go to the
@@ -47,9 +58,22 @@ __device__ __forceinline__ void wave_argmax(float& bv, int& bi) {
     }
 }
 
+// exp(s - m) for the softmax; s == m gives exactly 1.
+__device__ __forceinline__ float exp_diff(float s, float m) {
+    return __builtin_amdgcn_exp2f((s - m) * kLog2e);
+}
+
+// Wave combine of per-lane (max, sum-of-exp) pairs.
+__device__ __forceinline__ void wave_softmax_pair(float& m, float& s) {
+    const float mw = wave_max(m);
+    const float part = (m == -__builtin_inff()) ? 0.0f : s * exp_diff(m, mw);
+    s = wave_sum(part);
+    m = mw;
+}
+
 template <bool kVec>
-__device__ __forceinline__ void load_chunk(const float* row, int cols, int base, float T,
-                                           float (&v)[kPerLane], bool (&ok)[kPerLane]) {
+__device__ __forceinline__ void load_chunk(const float* row, int cols, int base,
+                                           float (&v)[kPerLane]) {
 #pragma unroll
     for (int u = 0; u < kPerLane / 4; ++u) {
         const int e0 = base + u * (kBlock * 4) + threadIdx.x * 4;
@@ -57,71 +81,80 @@ __device__ __forceinline__ void load_chunk(const float* row, int cols, int base,
             if (e0 + 3 < cols) {
                 const u32x4 w = ld16(row + e0);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    v[4 * u + i] = __uint_as_float(w[i]) / T;
-                    ok[4 * u + i] = true;
-                }
+                for (int i = 0; i < 4; ++i) v[4 * u + i] = __uint_as_float(w[i]);
                 continue;
             }
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int e = e0 + i;
-            ok[4 * u + i] = e < cols;
-            v[4 * u + i] = e < cols ? row[e] / T : 0.0f;
+            v[4 * u + i] = e < cols ? row[e] : 0.0f;
         }
     }
 }
 
-// Pass 1: one RowPart per (chunk, row).
-template <bool kVec>
-__global__ __launch_bounds__(kBlock) void row_partials_kernel(const float* __restrict__ logits,
-                                                              int cols, float T,
-                                                              RowPart* __restrict__ parts) {
+__device__ __forceinline__ int elem_index(int base, int j) {
+    return base + (j / 4) * (kBlock * 4) + threadIdx.x * 4 + (j & 3);
+}
+
+// Pass 1. kMode: kStatsSoftmax and/or kStatsArgmax.
+template <int kMode, bool kVec>
+__global__ __launch_bounds__(kBlock) void row_stats_kernel(const float* __restrict__ logits,
+                                                           int cols, float inv_t,
+                                                           RowPart* __restrict__ parts) {
     __shared__ float sm[4], ss[4], sbv[4];
     __shared__ int sbi[4];
     __shared__ uint32_t sfl[4];
-    const int chunk = blockIdx.x, row = blockIdx.y;
+    const int chunk = blockIdx.x, row = blockIdx.y, nchunks = gridDim.x;
     const int base = chunk * kChunk;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const float* r = logits + (int64_t)row * cols;
     float v[kPerLane];
-    bool ok[kPerLane];
-    load_chunk<kVec>(r, cols, base, T, v, ok);
+    load_chunk<kVec>(r, cols, base, v);
+    const int nvalid = cols - base;  // elements of this chunk: indices base .. base + nvalid-1
 
-    float m = -__builtin_inff(), bv = -__builtin_inff();
+    // Non-finite screen: x * 0 is NaN exactly for NaN and +-inf.
+    float nf = 0.0f;
+    float m = -__builtin_inff(), s = 0.0f, bv = -__builtin_inff();
     int bi = -1;
-    uint32_t fl = 0;
 #pragma unroll
     for (int j = 0; j < kPerLane; ++j) {
-        if (!ok[j]) continue;
+        const int idx = elem_index(base, j);
+        if (idx - base >= nvalid) continue;
         const float x = v[j];
-        const int idx = base + (j / 4) * (kBlock * 4) + threadIdx.x * 4 + (j & 3);
-        m = fmaxf(m, x);
-        if (x != x) fl |= FHIP_ROW_HAS_NAN;
-        if (__builtin_isinf(x)) fl |= FHIP_ROW_HAS_INF;
-        if (better(x, idx, bv, bi)) {
-            bv = x;
-            bi = idx;
+        nf = fmaf(x, 0.0f, nf);
+        if constexpr (kMode & kStatsArgmax) {
+            if (x >= bv) {  // lane visits its indices in increasing order: last max wins
+                bv = x;
+                bi = idx;
+            }
+        }
+        if constexpr (kMode & kStatsSoftmax) m = fmaxf(m, x * inv_t);
+    }
+    if constexpr (kMode & kStatsSoftmax) {
+        if (m != -__builtin_inff()) {
+#pragma unroll
+            for (int j = 0; j < kPerLane; ++j)
+                if (elem_index(base, j) - base < nvalid) s += exp_diff(v[j] * inv_t, m);
         }
     }
-    float s = 0.0f;
-    if (m != -__builtin_inff()) {
+    uint32_t fl = 0;
+    if (nf != nf) {  // rare: classify exactly
 #pragma unroll
-        for (int j = 0; j < kPerLane; ++j)
-            if (ok[j]) s += expf(v[j] - m);
+        for (int j = 0; j < kPerLane; ++j) {
+            if (elem_index(base, j) - base >= nvalid) continue;
+            const float x = v[j];
+            if (x != x) fl |= FHIP_ROW_HAS_NAN;
+            if (__builtin_isinf(x)) fl |= FHIP_ROW_HAS_INF;
+        }
     }
-    // wave combine
-    const float mw = wave_max(m);
-    const float sw = wave_sum(mw == -__builtin_inff() || m == -__builtin_inff()
-                                  ? 0.0f
-                                  : s * expf(m - mw));
-    wave_argmax(bv, bi);
+    if constexpr (kMode & kStatsSoftmax) wave_softmax_pair(m, s);
+    if constexpr (kMode & kStatsArgmax) wave_argmax(bv, bi);
     const uint32_t any_nan = __ballot(fl & FHIP_ROW_HAS_NAN) != 0 ? FHIP_ROW_HAS_NAN : 0u;
     const uint32_t any_inf = __ballot(fl & FHIP_ROW_HAS_INF) != 0 ? FHIP_ROW_HAS_INF : 0u;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (lane == 0) {
-        sm[wave] = mw;
-        ss[wave] = sw;
+        sm[wave] = m;
+        ss[wave] = s;
         sbv[wave] = bv;
         sbi[wave] = bi;
         sfl[wave] = any_nan | any_inf;
@@ -134,7 +167,7 @@ __global__ __launch_bounds__(kBlock) void row_partials_kernel(const float* __res
         int BI = sbi[0];
         uint32_t F = sfl[0];
         for (int w = 0; w < kBlock / 64; ++w) {
-            if (sm[w] != -__builtin_inff()) S += ss[w] * expf(sm[w] - M);
+            if (sm[w] != -__builtin_inff()) S += ss[w] * exp_diff(sm[w], M);
             if (w > 0) {
                 if (better(sbv[w], sbi[w], BV, BI)) {
                     BV = sbv[w];
@@ -150,59 +183,93 @@ __global__ __launch_bounds__(kBlock) void row_partials_kernel(const float* __res
         p.bi = BI;
         p.flags = F;
         p.pad[0] = p.pad[1] = p.pad[2] = 0;
-        parts[(int64_t)row * gridDim.x + chunk] = p;
+        parts[(int64_t)row * nchunks + chunk] = p;
     }
 }
 
-// Combine a row's records in chunk order (identical in every workgroup of the row).
-__device__ __forceinline__ void combine_row(const RowPart* __restrict__ parts, int nchunks,
-                                            float& M, float& S) {
+// Fold one row's records on one wave (chunk c on lane c mod 64, a fixed order, so every
+// caller of the same row gets the same M and S).
+template <int kMode>
+__device__ __forceinline__ void fold_row(const RowPart* __restrict__ rp, int nchunks, float& M,
+                                         float& S, float& BV, int& BI, uint32_t& F) {
+    const int lane = threadIdx.x & 63;
     M = -__builtin_inff();
-    for (int c = 0; c < nchunks; ++c) M = fmaxf(M, parts[c].m);
     S = 0.0f;
-    for (int c = 0; c < nchunks; ++c)
-        if (parts[c].m != -__builtin_inff()) S += parts[c].s * expf(parts[c].m - M);
+    BV = -__builtin_inff();
+    BI = -1;
+    uint32_t fl = 0;
+    for (int c = lane; c < nchunks; c += 64) {
+        const RowPart p = rp[c];
+        fl |= p.flags;
+        if constexpr (kMode & kStatsArgmax) {
+            if (better(p.bv, p.bi, BV, BI)) {
+                BV = p.bv;
+                BI = p.bi;
+            }
+        }
+        if constexpr (kMode & kStatsSoftmax) {
+            if (p.m != -__builtin_inff()) {
+                const float mn = fmaxf(M, p.m);
+                S = (M == -__builtin_inff() ? 0.0f : S * exp_diff(M, mn)) +
+                    p.s * exp_diff(p.m, mn);
+                M = mn;
+            }
+        }
+    }
+    if constexpr (kMode & kStatsSoftmax) wave_softmax_pair(M, S);
+    if constexpr (kMode & kStatsArgmax) wave_argmax(BV, BI);
+    const uint32_t fn = __ballot(fl & FHIP_ROW_HAS_NAN) != 0 ? FHIP_ROW_HAS_NAN : 0u;
+    const uint32_t fi = __ballot(fl & FHIP_ROW_HAS_INF) != 0 ? FHIP_ROW_HAS_INF : 0u;
+    F = fn | fi;
 }
 
-__device__ __forceinline__ void argmax_row(const RowPart* __restrict__ parts, int nchunks,
-                                           int32_t* index_out, uint32_t* flags_out) {
-    float BV = parts[0].bv;
-    int BI = parts[0].bi;
-    uint32_t F = parts[0].flags;
-    for (int c = 1; c < nchunks; ++c) {
-        if (better(parts[c].bv, parts[c].bi, BV, BI)) {
-            BV = parts[c].bv;
-            BI = parts[c].bi;
-        }
-        F |= parts[c].flags;
+// argmax pass 2: one wave per row.
+__global__ __launch_bounds__(kBlock) void argmax_fold_kernel(const RowPart* __restrict__ parts,
+                                                             int rows, int nchunks,
+                                                             int32_t* __restrict__ index_out,
+                                                             uint32_t* __restrict__ flags_out) {
+    const int row = blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    float M, S, BV;
+    int BI;
+    uint32_t F;
+    fold_row<kStatsArgmax>(parts + (int64_t)row * nchunks, nchunks, M, S, BV, BI, F);
+    if ((threadIdx.x & 63) == 0) {
+        index_out[row] = BI;
+        flags_out[row] = F;
     }
-    *index_out = BI;
-    *flags_out = F;
 }
 
 // Pass 2: probabilities for one (chunk, row); chunk 0 also writes the row's argmax.
-template <bool kVec>
+template <int kMode, bool kVec>
 __global__ __launch_bounds__(kBlock) void softmax_write_kernel(
-    const float* __restrict__ logits, float* __restrict__ probs, int cols, float T,
+    const float* __restrict__ logits, float* __restrict__ probs, int cols, float inv_t,
     const RowPart* __restrict__ parts, int32_t* __restrict__ index_out,
     uint32_t* __restrict__ flags_out) {
     __shared__ float sMS[2];
-    const int chunk = blockIdx.x, row = blockIdx.y;
-    const RowPart* rp = parts + (int64_t)row * gridDim.x;
-    if (threadIdx.x == 0) {
-        float M, S;
-        combine_row(rp, gridDim.x, M, S);
-        sMS[0] = M;
-        sMS[1] = S;
-        if (chunk == 0 && index_out) argmax_row(rp, gridDim.x, index_out + row, flags_out + row);
-    }
+    const int chunk = blockIdx.x, row = blockIdx.y, nchunks = gridDim.x;
     const int base = chunk * kChunk;
     const float* r = logits + (int64_t)row * cols;
     float v[kPerLane];
-    bool ok[kPerLane];
-    load_chunk<kVec>(r, cols, base, T, v, ok);
+    load_chunk<kVec>(r, cols, base, v);
+    if (threadIdx.x < 64) {
+        float M, S, BV;
+        int BI;
+        uint32_t F;
+        fold_row<kMode>(parts + (int64_t)row * nchunks, nchunks, M, S, BV, BI, F);
+        if (threadIdx.x == 0) {
+            sMS[0] = M;
+            sMS[1] = 1.0f / S;
+            if constexpr (kMode & kStatsArgmax) {
+                if (chunk == 0) {
+                    index_out[row] = BI;
+                    flags_out[row] = F;
+                }
+            }
+        }
+    }
     __syncthreads();
-    const float M = sMS[0], S = sMS[1];
+    const float M = sMS[0], invS = sMS[1];
     float* o = probs + (int64_t)row * cols;
 #pragma unroll
     for (int u = 0; u < kPerLane / 4; ++u) {
@@ -210,24 +277,15 @@ __global__ __launch_bounds__(kBlock) void softmax_write_kernel(
         if (kVec && e0 + 3 < cols) {
             u32x4 w;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) w[i] = __float_as_uint(expf(v[4 * u + i] - M) / S);
+            for (int i = 0; i < 4; ++i)
+                w[i] = __float_as_uint(exp_diff(v[4 * u + i] * inv_t, M) * invS);
             st16_stream(o + e0, w);
         } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                if (ok[4 * u + i]) o[e0 + i] = expf(v[4 * u + i] - M) / S;
+                if (e0 + i < cols) o[e0 + i] = exp_diff(v[4 * u + i] * inv_t, M) * invS;
         }
     }
-}
-
-// Argmax only: one lane per row folds the row's records.
-__global__ __launch_bounds__(kBlock) void argmax_finalize_kernel(const RowPart* __restrict__ parts,
-                                                                 int rows, int nchunks,
-                                                                 int32_t* __restrict__ index_out,
-                                                                 uint32_t* __restrict__ flags_out) {
-    const int row = blockIdx.x * kBlock + threadIdx.x;
-    if (row < rows)
-        argmax_row(parts + (int64_t)row * nchunks, nchunks, index_out + row, flags_out + row);
 }
 
 int check_rows(const float* logits, int rows, int cols, void* ws) {
@@ -236,17 +294,31 @@ int check_rows(const float* logits, int rows, int cols, void* ws) {
     return hipSuccess;
 }
 
-int launch_partials(const float* logits, int rows, int cols, float T, RowPart* parts,
-                    hipStream_t s, bool& vec) {
-    vec = cols % 4 == 0 && fhip_host::aligned16(logits);
+template <int kMode>
+int launch_stats(const float* logits, int rows, int cols, float inv_t, RowPart* parts,
+                 hipStream_t s) {
+    const bool vec = cols % 4 == 0 && fhip_host::aligned16(logits);
     dim3 grid(num_chunks(cols), rows);
     if (vec)
-        hipLaunchKernelGGL(row_partials_kernel<true>, grid, dim3(kBlock), 0, s, logits, cols, T,
-                           parts);
+        hipLaunchKernelGGL((row_stats_kernel<kMode, true>), grid, dim3(kBlock), 0, s, logits, cols,
+                           inv_t, parts);
     else
-        hipLaunchKernelGGL(row_partials_kernel<false>, grid, dim3(kBlock), 0, s, logits, cols, T,
-                           parts);
+        hipLaunchKernelGGL((row_stats_kernel<kMode, false>), grid, dim3(kBlock), 0, s, logits,
+                           cols, inv_t, parts);
     return hipGetLastError();
+}
+
+template <int kMode>
+void launch_write(const float* logits, float* probs, int rows, int cols, float inv_t,
+                  const RowPart* parts, int32_t* index_out, uint32_t* flags_out, hipStream_t s) {
+    const bool vec = cols % 4 == 0 && fhip_host::aligned16(logits) && fhip_host::aligned16(probs);
+    dim3 grid(num_chunks(cols), rows);
+    if (vec)
+        hipLaunchKernelGGL((softmax_write_kernel<kMode, true>), grid, dim3(kBlock), 0, s, logits,
+                           probs, cols, inv_t, parts, index_out, flags_out);
+    else
+        hipLaunchKernelGGL((softmax_write_kernel<kMode, false>), grid, dim3(kBlock), 0, s, logits,
+                           probs, cols, inv_t, parts, index_out, flags_out);
 }
 
 }  // namespace
@@ -268,17 +340,17 @@ int fhip_launch_softmax_argmax_rows(const float* logits, float* probs, int32_t* 
     if (rows == 0) return hipSuccess;
     hipStream_t s = fhip_host::as_stream(stream);
     RowPart* parts = (RowPart*)workspace;
-    bool vec;
-    e = launch_partials(logits, rows, cols, temperature, parts, s, vec);
-    if (e != hipSuccess) return e;
-    vec = vec && fhip_host::aligned16(probs);
-    dim3 grid(num_chunks(cols), rows);
-    if (vec)
-        hipLaunchKernelGGL(softmax_write_kernel<true>, grid, dim3(kBlock), 0, s, logits, probs,
-                           cols, temperature, parts, index_out, flags_out);
-    else
-        hipLaunchKernelGGL(softmax_write_kernel<false>, grid, dim3(kBlock), 0, s, logits, probs,
-                           cols, temperature, parts, index_out, flags_out);
+    const float inv_t = 1.0f / temperature;
+    if (index_out) {
+        e = launch_stats<kStatsSoftmax | kStatsArgmax>(logits, rows, cols, inv_t, parts, s);
+        if (e != hipSuccess) return e;
+        launch_write<kStatsSoftmax | kStatsArgmax>(logits, probs, rows, cols, inv_t, parts,
+                                                   index_out, flags_out, s);
+    } else {
+        e = launch_stats<kStatsSoftmax>(logits, rows, cols, inv_t, parts, s);
+        if (e != hipSuccess) return e;
+        launch_write<kStatsSoftmax>(logits, probs, rows, cols, inv_t, parts, nullptr, nullptr, s);
+    }
     return hipGetLastError();
 }
 
@@ -296,10 +368,9 @@ int fhip_launch_argmax_rows(const float* logits, int32_t* index_out, uint32_t* f
     if (rows == 0) return hipSuccess;
     hipStream_t s = fhip_host::as_stream(stream);
     RowPart* parts = (RowPart*)workspace;
-    bool vec;
-    e = launch_partials(logits, rows, cols, 1.0f, parts, s, vec);
+    e = launch_stats<kStatsArgmax>(logits, rows, cols, 1.0f, parts, s);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(argmax_finalize_kernel, dim3((unsigned)ceil_div(rows, kBlock)),
+    hipLaunchKernelGGL(argmax_fold_kernel, dim3((unsigned)ceil_div(rows, kBlock / 64)),
                        dim3(kBlock), 0, s, parts, rows, num_chunks(cols), index_out, flags_out);
     return hipGetLastError();
 }

@@ -34,6 +34,7 @@ struct Quantizer {
     float2 ent[kMaxBuckets];         // {threshold in bucket or +inf, base count (int bits)}
     float ybound, scale, offset, jmax;
     int L, J;
+    int unit_fast;  // quantize_unit is exact for every |y| <= 4 and for NaN
     float red_f[2][16];
     int red_i[16];
 };
@@ -60,9 +61,33 @@ __device__ inline float exact_threshold(float c0, float c1) {
     return ofloat(lo);
 }
 
+// Monotone bucket map, clamped to [0, J-1]; NaN maps to bucket 0 (med3 of NaN, 0, jmax
+// returns 0 on gfx9, like fminf(fmaxf(NaN, 0), jmax)).
+// The same threshold, found by walking from the fp32 midpoint (the boundary is within a few
+// ulps of it); falls back to the bisection when the walk does not end within 16 steps.
+__device__ inline float exact_threshold_walk(float c0, float c1) {
+    const float m = c0 + 0.5f * (c1 - c0);
+    if (!(m > c0 && m < c1)) return exact_threshold(c0, c1);
+    uint32_t k = okey(m);
+    const bool up = fabsf(m - c0) <= fabsf(m - c1);
+#pragma unroll 1
+    for (int it = 0; it < 16; ++it) {
+        if (up) {  // P(k) holds: advance while P(k + 1) holds
+            const float n = ofloat(k + 1u);
+            if (!(n < c1) || fabsf(n - c0) > fabsf(n - c1)) return ofloat(k);
+            ++k;
+        } else {  // P(k) fails: step down until it holds
+            --k;
+            const float n = ofloat(k);
+            if (!(n > c0) || fabsf(n - c0) <= fabsf(n - c1)) return n > c0 ? n : c0;
+        }
+    }
+    return exact_threshold(c0, c1);
+}
+
 __device__ __forceinline__ int bucket_of(const Quantizer& q, float y) {
     const float jf = fmaf(y, q.scale, q.offset);
-    return (int)fminf(fmaxf(jf, 0.0f), q.jmax);
+    return (int)__builtin_amdgcn_fmed3f(jf, 0.0f, q.jmax);
 }
 
 // The reference's linear scan.
@@ -77,6 +102,15 @@ __device__ inline int slow_code(float y, const float* c, int L) {
         }
     }
     return idx;
+}
+
+// Fast path for the rotated unit vectors of TurboQuant (|y| <= 1 up to rounding, or NaN when
+// the input held NaN/inf): valid when q.unit_fast is set, i.e. ybound >= 4 and no bucket
+// holds two thresholds. NaN clamps to bucket 0 and takes its base, code 0, which is what the
+// reference's scan returns for NaN (no distance compares below the first).
+__device__ __forceinline__ int quantize_unit(const Quantizer& q, float y) {
+    const float2 e = q.ent[bucket_of(q, y)];
+    return __float_as_int(e.y) + (y > e.x ? 1 : 0);
 }
 
 __device__ __forceinline__ int quantize(const Quantizer& q, float y) {
@@ -142,7 +176,7 @@ __device__ inline void quantizer_build(Quantizer& q, const float* __restrict__ c
     __syncthreads();
     const bool fast = q.ybound > 0.0f;
     if (fast)
-        for (int i = tid; i < L - 1; i += bs) q.t[i] = exact_threshold(q.c[i], q.c[i + 1]);
+        for (int i = tid; i < L - 1; i += bs) q.t[i] = exact_threshold_walk(q.c[i], q.c[i + 1]);
     __syncthreads();
     if (tid == 0 && fast) {
         const int J = q.J;
@@ -164,6 +198,7 @@ __device__ inline void quantizer_build(Quantizer& q, const float* __restrict__ c
         q.offset = o;
     }
     __syncthreads();
+    int crowded = 0;
     if (q.ybound > 0.0f) {
         for (int i = tid; i < L - 1; i += bs) q.jt[i] = bucket_of(q, q.t[i]);
         __syncthreads();
@@ -190,10 +225,13 @@ __device__ inline void quantizer_build(Quantizer& q, const float* __restrict__ c
             } else {
                 e.x = 0.0f;
                 e.y = __int_as_float(-1);
+                crowded = 1;
             }
             q.ent[j] = e;
         }
     }
+    crowded = __syncthreads_or(crowded);
+    if (tid == 0) q.unit_fast = (q.ybound >= 4.0f && !crowded) ? 1 : 0;
     __syncthreads();
 }
 

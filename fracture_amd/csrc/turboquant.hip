@@ -12,11 +12,17 @@
 //   dequantize: x_hat = Pi^T yhat = Pi_hi^T c_hi + 2^-12 (Pi_lo'^T c_hi + Pi_hi^T c_lo')
 // Each representation error is ~2^-22 relative, the level of the fp32 sums themselves.
 //
-// Work mapping (head_dim 128): a 256-lane workgroup (4 waves) takes tiles of 32 vectors;
-// wave w owns rotated coordinates [32w, 32w+32) and keeps its 32x128 slice of the rotation
-// (hi and lo) in registers for the workgroup's lifetime. The tile is staged once in LDS and
-// shared by the four waves. Other head dims use a per-vector VALU path that follows the
-// reference kernel's arithmetic.
+// Work mapping (head_dim 128, 2/3/4/8 bits): one workgroup of 8 (compress) or 12
+// (dequantize) waves per CU holds the rotation's hi/lo MFMA fragments in LDS (64 KB, staged
+// once). Every wave then owns whole
+// tiles of 32 vectors: it loads its tile's input straight into MFMA operand registers
+// (prefetching the next tile while it computes), runs 4 blocks of 32 output coordinates x
+// 8 K-steps of MFMA against the LDS fragments, and quantizes / packs / stores its own
+// results. Waves never wait for one another after the staging barrier, and each keeps one
+// tile of loads in flight, which is what hides HBM latency. The two lanes that hold the two
+// halves of a 16-byte group exchange them with v_permlane32_swap.
+// Other head dims and bit widths use a per-vector VALU path that follows the reference
+// kernel's arithmetic.
 #include "tq_quant.h"
 
 using namespace fhip;
@@ -25,8 +31,8 @@ namespace {
 
 constexpr int kTile = 32;        // vectors per MFMA tile
 constexpr int kHd = 128;         // head_dim of the MFMA path
-constexpr int kXStride = 136;    // fp16 elements per LDS row (128 + 8 pad, conflict-free)
-constexpr int kCStride = 132;    // bytes per LDS code row (128 + 4 pad)
+constexpr int kWavesC = 8;       // waves per workgroup of the MFMA compress (one group per CU)
+constexpr int kWavesD = 12;      // waves per workgroup of the MFMA dequantize
 constexpr float kLoScale = 4096.0f;
 constexpr float kLoInv = 1.0f / 4096.0f;
 
@@ -73,147 +79,237 @@ struct PageDst {
     }
 };
 
-struct CompressLds {
-    uint16_t x[kTile * kXStride];
-    float ssp[4][kTile];
-    uint8_t codes[kTile * kCStride];
+// ---------------------------------------------------------------------------------------
+// Rotation fragments in LDS. MFMA step s of a 32-coordinate block takes K = 16 coordinates,
+// ordered so that lane half h, element e of step s is coordinate 64h + 8s + e: a lane's B
+// operand over the 8 steps is then one contiguous half of its vector (128 bytes of fp16
+// input, or 8 consecutive code groups), which it loads with wide loads.
+//   compress   (y = Pi x):      A[i][k] = Pi[32c + i][k]
+//   dequantize (x = Pi^T y):    A[i][k] = Pi[k][32c + i]
+// frag[c][s][0|1][lane] = 8 fp16 of the hi / lo' part, lane = (i = lane & 31, h = lane >> 5).
+// ---------------------------------------------------------------------------------------
+struct RotLds {
+    u32x4 frag[4][8][2][64];  // 64 KB
 };
 
-// Load the rotation slice of wave `wave` as MFMA A fragments, split hi/lo.
-// kTranspose = false: A[i][k] = Pi[32w + i][k]   (compress: y = Pi x)
-// kTranspose = true : A[i][k] = Pi[k][32w + i]   (dequantize: x = Pi^T y)
 template <bool kTranspose>
-__device__ __forceinline__ void load_rotation(const float* __restrict__ rot, int wave, int r,
-                                              int h, f16x8 (&ahi)[8], f16x8 (&alo)[8]) {
+__device__ __forceinline__ void stage_rotation(const float* __restrict__ rot, RotLds& L) {
+    for (int idx = threadIdx.x; idx < 4 * 8 * 64; idx += blockDim.x) {
+        const int lane = idx & 63, s = (idx >> 6) & 7, c = idx >> 9;
+        const int i = lane & 31, h = lane >> 5;
+        const int row = 32 * c + i;
+        const int k0 = 64 * h + 8 * s;
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+            uint32_t hb[2], lb[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int k = k0 + 2 * e2 + t;
+                const float v = kTranspose ? rot[k * kHd + row] : rot[row * kHd + k];
+                const _Float16 hi = (_Float16)v;
+                hb[t] = __builtin_bit_cast(uint16_t, hi);
+                lb[t] = __builtin_bit_cast(uint16_t, (_Float16)((v - (float)hi) * kLoScale));
+            }
+            hw[e2] = hb[0] | (hb[1] << 16);
+            lw[e2] = lb[0] | (lb[1] << 16);
+        }
+        L.frag[c][s][0][lane] = u32x4{hw[0], hw[1], hw[2], hw[3]};
+        L.frag[c][s][1][lane] = u32x4{lw[0], lw[1], lw[2], lw[3]};
+    }
+}
+
+__device__ __forceinline__ f16x8 frag(const RotLds& L, int c, int s, int hl, int lane) {
+    return __builtin_bit_cast(f16x8, L.frag[c][s][hl][lane]);
+}
+
+// Lanes l and l^32: after swap_halves(v, w), lanes 0-31 hold (own v, partner's v) and lanes
+// 32-63 hold (partner's w, own w) in (v, w) (v_permlane32_swap).
+__device__ __forceinline__ void swap_halves(uint32_t& v, uint32_t& w) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, w, false, false);
+    v = r[0];
+    w = r[1];
+}
+__device__ __forceinline__ float partner_f(float x) {
+    uint32_t v = __float_as_uint(x), w = v;
+    swap_halves(v, w);  // lanes < 32: partner in w; lanes >= 32: partner in v
+    return __uint_as_float((threadIdx.x & 32) ? v : w);
+}
+
+// Sum of squares of 8 fp16 values with fp32 accumulation (products of fp16 are exact).
+__device__ __forceinline__ float sumsq8(const f16x8& b, float acc) {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const f16x2 p = {b[2 * e], b[2 * e + 1]};
+        acc = __builtin_amdgcn_fdot2(p, p, acc, false);
+    }
+    return acc;
+}
+
+// Store n (2..64) bytes at dst, using the widest aligned stores the address allows.
+template <int n>
+__device__ __forceinline__ void store_bytes(uint8_t* dst, const uint32_t (&w)[16]) {
+    const uintptr_t a = (uintptr_t)dst;
+    if constexpr (n % 16 == 0) {
+        if ((a & 15u) == 0) {
+#pragma unroll
+            for (int i = 0; i < n / 16; ++i)
+                *(u32x4*)(dst + 16 * i) = u32x4{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]};
+            return;
+        }
+    }
+    if constexpr (n % 8 == 0) {
+        if ((a & 7u) == 0) {
+#pragma unroll
+            for (int i = 0; i < n / 8; ++i) *(u32x2*)(dst + 8 * i) = u32x2{w[2 * i], w[2 * i + 1]};
+            return;
+        }
+    }
+    if ((a & 3u) == 0) {
+#pragma unroll
+        for (int i = 0; i < n / 4; ++i) *(uint32_t*)(dst + 4 * i) = w[i];
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < n; ++i) dst[i] = (uint8_t)(w[i >> 2] >> (8 * (i & 3)));
+}
+
+// One lane's half of a 32 x 128 fp16 input tile: row r = lane & 31, coordinates
+// [64h, 64h + 64) as 8 MFMA B fragments (zeros past the end).
+__device__ __forceinline__ void load_x_half(const uint16_t* __restrict__ in, int64_t tile,
+                                            int64_t ntiles, int64_t rows, f16x8 (&x)[8]) {
+    const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
+    const int64_t m0 = tile * kTile;
+    const bool ok = tile < ntiles && r < rows - m0;
+    const uint16_t* src = in + m0 * kHd + (r * kHd + 64 * h);
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-        float v[8];
-        if constexpr (!kTranspose) {
-            const float* p = rot + (32 * wave + r) * kHd + 16 * s + 8 * h;
-            const f32x4 p0 = *(const f32x4*)p;
-            const f32x4 p1 = *(const f32x4*)(p + 4);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                v[e] = p0[e];
-                v[4 + e] = p1[e];
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = rot[(16 * s + 8 * h + e) * kHd + 32 * wave + r];
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const _Float16 hi = (_Float16)v[e];
-            ahi[s][e] = hi;
-            alo[s][e] = (_Float16)((v[e] - (float)hi) * kLoScale);
-        }
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (ok) v = ld16(src + 8 * s);
+        x[s] = __builtin_bit_cast(f16x8, v);
     }
 }
 
 // ---------------------------------------------------------------------------------------
-// MFMA compress / rotate, head_dim 128.
-//   kMode 0: quantize + pack to Dst;  kMode 1: write fp32 y (and norms) for verification.
+// MFMA compress / rotate of one tile by one wave (head_dim 128).
+//   kMode 0: quantize + pack to Dst (kBits 2, 3, 4, 8);  kMode 1: fp32 y (and norms).
+// Lane (r, h) ends block c holding coordinates 32c + 8g + 4h + e (g, e = 0..3) of vector r;
+// it quantizes them into half-groups (4 codes, 4*kBits bits, MSB first). After the 4 blocks
+// lane h owns groups [8h, 8h+8) of row r: 8*kBits contiguous bytes at byte 8*kBits*h.
 // ---------------------------------------------------------------------------------------
-template <int kMode, class Dst>
-__global__ __launch_bounds__(256) void tq_compress_mfma_kernel(
-    const uint16_t* __restrict__ in, const float* __restrict__ rot,
-    const float* __restrict__ cent, int L, int bits, Dst dst, float* __restrict__ y_out,
-    int64_t rows) {
-    __shared__ Quantizer qz;
-    __shared__ CompressLds sh;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int r = lane & 31, h = lane >> 5;
-
-    f16x8 ahi[8], alo[8];
-    load_rotation<false>(rot, wave, r, h, ahi, alo);
-    if constexpr (kMode == 0) quantizer_build(qz, cent, L);
-
-    const int64_t ntiles = ceil_div(rows, kTile);
-    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-        const int64_t m0 = tile * kTile;
-        const int nvalid = (int)(rows - m0 < kTile ? rows - m0 : kTile);
-        // Stage the 32 x 128 fp16 tile (8 KB): 16 lanes per row, 16 bytes each.
+template <int kMode, int kBits, bool kUnitFast, class Dst>
+__device__ __forceinline__ void compress_tile(const Quantizer& qz, const RotLds& L,
+                                              const f16x8 (&x)[8], const Dst& dst,
+                                              float* __restrict__ y_out, int64_t m0, int nvalid) {
+    const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
+    float ssq = 0.0f;  // this lane's half of vector r
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int idx = tid + 256 * i;
-            const int row = idx >> 4, c16 = idx & 15;
-            u32x4 v = {0u, 0u, 0u, 0u};
-            if (row < nvalid) v = ld16(in + (m0 + row) * kHd + c16 * 8);
-            *(u32x4*)&sh.x[row * kXStride + c16 * 8] = v;
-        }
-        __syncthreads();
-
+    for (int s = 0; s < 8; ++s) ssq = sumsq8(x[s], ssq);
+    const float nrm = sqrtf(ssq + partner_f(ssq));
+    const float inv = 1.0f / (nrm + 1e-8f);
+    const bool row_ok = r < nvalid;
+    if (h == 0 && row_ok) {
+        uint16_t* np = dst.nptr(m0 + r);
+        if (np) *np = (uint16_t)f2h(nrm);
+    }
+    uint32_t half[16];  // kMode 0: half-group of group 4c + g held by this lane
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        __builtin_amdgcn_sched_barrier(0);  // keep each block's fragment loads within it
         f32x16 acc_hi = {}, acc_lo = {};
-        float ssq = 0.0f;
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-            const f16x8 b = *(const f16x8*)&sh.x[r * kXStride + 16 * s + 8 * h];
-            acc_hi = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi[s], b, acc_hi, 0, 0, 0);
-            acc_lo = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo[s], b, acc_lo, 0, 0, 0);
-            if ((s >> 1) == wave) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float xe = (float)b[e];
-                    ssq += xe * xe;
-                }
-            }
+            acc_hi = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag(L, c, s, 0, lane), x[s], acc_hi,
+                                                            0, 0, 0);
+            acc_lo = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag(L, c, s, 1, lane), x[s], acc_lo,
+                                                            0, 0, 0);
         }
-        ssq += __shfl_xor(ssq, 32);
-        if (h == 0) sh.ssp[wave][r] = ssq;
-        __syncthreads();
-        const float ss = sh.ssp[0][r] + sh.ssp[1][r] + sh.ssp[2][r] + sh.ssp[3][r];
-        const float nrm = sqrtf(ss);
-        const float inv = 1.0f / (nrm + 1e-8f);
-        if (wave == 0 && h == 0 && r < nvalid) {
-            uint16_t* np = dst.nptr(m0 + r);
-            if (np) *np = (uint16_t)f2h(nrm);
-        }
-        // Lane (r, h) holds coordinates 32*wave + 8g + 4h + e of vector r.
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             float y[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                y[e] = (acc_hi[4 * g + e] + acc_lo[4 * g + e] * kLoInv) * inv;
-            const int i0 = 32 * wave + 8 * g + 4 * h;
+                y[e] = fmaf(acc_lo[4 * g + e], kLoInv, acc_hi[4 * g + e]) * inv;
             if constexpr (kMode == 1) {
-                if (r < nvalid) {
-                    f32x4 yv = {y[0], y[1], y[2], y[3]};
-                    *(f32x4*)&y_out[(m0 + r) * kHd + i0] = yv;
-                }
+                if (row_ok)
+                    *(f32x4*)&y_out[(m0 + r) * kHd + 32 * c + 8 * g + 4 * h] =
+                        f32x4{y[0], y[1], y[2], y[3]};
             } else {
-                uint32_t word = 0;
+                uint32_t hw = 0;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) word |= (uint32_t)quantize(qz, y[e]) << (8 * e);
-                *(uint32_t*)&sh.codes[r * kCStride + i0] = word;
+                for (int e = 0; e < 4; ++e)
+                    hw = (hw << kBits) |
+                         (uint32_t)(kUnitFast ? quantize_unit(qz, y[e]) : quantize(qz, y[e]));
+                half[4 * c + g] = hw;
             }
         }
-        if constexpr (kMode == 0) {
-            __syncthreads();
-            // Pack: 32 rows x 16 groups of 8 codes, 2 groups per lane; consecutive lanes
-            // write consecutive bytes of the tile's packed rows.
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int idx = tid + 256 * i;
-                const int row = idx >> 4, g = idx & 15;
-                if (row < nvalid) {
-                    uint8_t* prow = dst.prow(m0 + row);
-                    if (prow) {
-                        const uint32_t* cp = (const uint32_t*)&sh.codes[row * kCStride + 8 * g];
-                        const uint32_t w0 = cp[0], w1 = cp[1];
-                        int codes[8];
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            codes[e] = (w0 >> (8 * e)) & 0xff;
-                            codes[4 + e] = (w1 >> (8 * e)) & 0xff;
-                        }
-                        store_group(prow + g * bits, group_word(codes, bits), bits, bits);
-                    }
-                }
-            }
-        }
-        __syncthreads();
     }
+    if constexpr (kMode == 0) {
+        // Group j (< 8) and group j + 8: lane h = 0 gets both halves of group j, lane h = 1
+        // both halves of group j + 8, as (first half, second half) in (half[j], half[j+8]).
+        uint32_t w[16] = {};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint32_t v = half[j], u = half[j + 8];
+            swap_halves(v, u);
+            const uint64_t G = ((uint64_t)v << (4 * kBits)) | u;  // 8*kBits bits, MSB first
+#pragma unroll
+            for (int k = 0; k < kBits; ++k) {
+                const int byte = j * kBits + k;
+                w[byte >> 2] |= (uint32_t)((G >> (8 * (kBits - 1 - k))) & 0xffu) << (8 * (byte & 3));
+            }
+        }
+        if (row_ok) {
+            uint8_t* prow = dst.prow(m0 + r);
+            if (prow) store_bytes<8 * kBits>(prow + 8 * kBits * h, w);
+        }
+    }
+}
+
+// xa holds the wave's first tile (loaded before the workgroup's set-up).
+template <int kMode, int kBits, bool kUnitFast, class Dst>
+__device__ __forceinline__ void compress_waves(const Quantizer& qz, const RotLds& L,
+                                               const uint16_t* __restrict__ in, const Dst& dst,
+                                               float* __restrict__ y_out, int64_t rows,
+                                               f16x8 (&xa)[8]) {
+    const int64_t ntiles = ceil_div(rows, kTile);
+    const int64_t stride = (int64_t)gridDim.x * kWavesC;
+    int64_t tile = (int64_t)blockIdx.x * kWavesC + (threadIdx.x >> 6);
+    f16x8 xb[8];
+    // Two tiles per trip, ping-ponging the register buffers: each tile's successor is in
+    // flight while it computes.
+    while (tile < ntiles) {
+        load_x_half(in, tile + stride, ntiles, rows, xb);
+        compress_tile<kMode, kBits, kUnitFast>(qz, L, xa, dst, y_out, tile * kTile,
+                                               (int)min<int64_t>(kTile, rows - tile * kTile));
+        tile += stride;
+        if (tile >= ntiles) break;
+        load_x_half(in, tile + stride, ntiles, rows, xa);
+        compress_tile<kMode, kBits, kUnitFast>(qz, L, xb, dst, y_out, tile * kTile,
+                                               (int)min<int64_t>(kTile, rows - tile * kTile));
+        tile += stride;
+    }
+}
+
+template <int kMode, int kBits, class Dst>
+__global__ __launch_bounds__(64 * kWavesC) __attribute__((amdgpu_waves_per_eu(2))) void
+tq_compress_mfma_kernel(const uint16_t* __restrict__ in, const float* __restrict__ rot,
+                        const float* __restrict__ cent, int L, Dst dst,
+                        float* __restrict__ y_out, int64_t rows) {
+    __shared__ Quantizer qz;
+    __shared__ RotLds rl;
+    if constexpr (kMode == 0) quantizer_build(qz, cent, L);  // has barriers
+    // The first tile's loads go out before the rotation is staged, which overlaps them.
+    f16x8 xa[8];
+    load_x_half(in, (int64_t)blockIdx.x * kWavesC + (threadIdx.x >> 6), ceil_div(rows, kTile),
+                rows, xa);
+    stage_rotation<false>(rot, rl);
+    __syncthreads();
+    if (kMode == 0 && qz.unit_fast)
+        compress_waves<kMode, kBits, true>(qz, rl, in, dst, y_out, rows, xa);
+    else
+        compress_waves<kMode, kBits, false>(qz, rl, in, dst, y_out, rows, xa);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -319,80 +415,176 @@ __global__ __launch_bounds__(256) void tq_quantize_pack_kernel(const float* __re
 //   unpack -> c[idx] -> x_hat = Pi^T y_hat -> fp16(x_hat * float(norm)).
 // ---------------------------------------------------------------------------------------
 struct DequantLds {
-    uint16_t chi[kMaxLevels], clo[kMaxLevels];
-    uint16_t yhi[kTile * kXStride], ylo[kTile * kXStride];
+    uint32_t tab[kMaxLevels];  // c -> fp16 bits of (c_hi | c_lo << 16), c = c_hi + c_lo*2^-12
+    u32x2 pair[256];           // 4-bit: byte -> {hi(c[b>>4]) | hi(c[b&15])<<16, same for lo}
 };
 
-__global__ __launch_bounds__(256) void tq_dequant_mfma_kernel(const uint8_t* __restrict__ packed,
-                                                              const uint16_t* __restrict__ norms,
-                                                              const float* __restrict__ rot,
-                                                              const float* __restrict__ cent,
-                                                              int L, int bits,
-                                                              uint16_t* __restrict__ out,
-                                                              int64_t rows, int64_t pd) {
-    __shared__ DequantLds sh;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int r = lane & 31, h = lane >> 5;
-    for (int i = tid; i < kMaxLevels; i += 256) {
-        const float c = i < L ? cent[i] : 0.0f;
-        const _Float16 hi = (_Float16)c;
-        sh.chi[i] = __builtin_bit_cast(uint16_t, hi);
-        sh.clo[i] = __builtin_bit_cast(uint16_t, (_Float16)((c - (float)hi) * kLoScale));
-    }
-    f16x8 ahi[8], alo[8];
-    load_rotation<true>(rot, wave, r, h, ahi, alo);
-    __syncthreads();
-    const int64_t ntiles = ceil_div(rows, kTile);
-    for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-        const int64_t m0 = tile * kTile;
-        const int nvalid = (int)(rows - m0 < kTile ? rows - m0 : kTile);
-        // Decode 32 rows x 16 groups into fp16 hi/lo operand tiles, 2 groups per lane.
+// fp16 hi and lo operand halves of two codes' table entries.
+__device__ __forceinline__ void split_pair(uint32_t t0, uint32_t t1, uint32_t& vh, uint32_t& vl) {
+    vh = __builtin_amdgcn_perm(t1, t0, 0x05040100u);
+    vl = __builtin_amdgcn_perm(t1, t0, 0x07060302u);
+}
+
+// One lane's codes of a tile: row r = lane & 31, groups [8h, 8h+8) (8*kBits bytes at byte
+// 8*kBits*h of the row), and the row's norm.
+template <int kBits>
+struct CodeHalf {
+    uint32_t w[2 * kBits];
+    uint16_t norm;
+};
+
+template <int kBits>
+__device__ __forceinline__ void load_code_half(const uint8_t* __restrict__ packed,
+                                               const uint16_t* __restrict__ norms, int64_t tile,
+                                               int64_t ntiles, int64_t rows, CodeHalf<kBits>& cw) {
+    constexpr int pd = 16 * kBits;
+    const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
+    const int64_t m0 = tile * kTile;
+    const bool ok = tile < ntiles && r < rows - m0;
+    const uint8_t* src = packed + m0 * pd + (r * pd + 8 * kBits * h);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int idx = tid + 256 * i;
-            const int row = idx >> 4, g = idx & 15;
-            uint32_t whi[4] = {0u, 0u, 0u, 0u}, wlo[4] = {0u, 0u, 0u, 0u};
-            if (row < nvalid) {
-                int codes[8];
-                load_group(packed + (m0 + row) * pd + (int64_t)g * bits, bits, bits, codes);
+    for (int i = 0; i < 2 * kBits; ++i) cw.w[i] = 0u;
+    if (ok) {
+        if constexpr (kBits % 2 == 0) {  // 16, 32 or 64 bytes at a 16-byte aligned offset
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    whi[e] = (uint32_t)sh.chi[codes[2 * e]] | ((uint32_t)sh.chi[codes[2 * e + 1]] << 16);
-                    wlo[e] = (uint32_t)sh.clo[codes[2 * e]] | ((uint32_t)sh.clo[codes[2 * e + 1]] << 16);
-                }
+            for (int i = 0; i < kBits / 2; ++i) {
+                const u32x4 v = ld16(src + 16 * i);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) cw.w[4 * i + t] = v[t];
             }
-            u32x4 vh = {whi[0], whi[1], whi[2], whi[3]}, vl = {wlo[0], wlo[1], wlo[2], wlo[3]};
-            *(u32x4*)&sh.yhi[row * kXStride + 8 * g] = vh;
-            *(u32x4*)&sh.ylo[row * kXStride + 8 * g] = vl;
+        } else {  // 24 bytes at an 8-byte aligned offset
+#pragma unroll
+            for (int i = 0; i < kBits; ++i) {
+                const u32x2 v = *(const u32x2*)(src + 8 * i);
+                cw.w[2 * i] = v[0];
+                cw.w[2 * i + 1] = v[1];
+            }
         }
-        __syncthreads();
+    }
+    cw.norm = ok ? norms[m0 + r] : (uint16_t)0;
+}
+
+// The 8 codes of group s of this lane's half as fp16 hi / lo B fragments.
+template <int kBits>
+__device__ __forceinline__ void decode_group(const DequantLds& t, const CodeHalf<kBits>& cw,
+                                             int s, f16x8& bh, f16x8& bl) {
+    uint32_t vh[4], vl[4];
+    if constexpr (kBits == 4) {
+        const uint32_t g = cw.w[s];  // byte p: coordinates (2p, 2p+1) in (high, low) nibbles
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const u32x2 e = t.pair[(g >> (8 * p)) & 0xffu];
+            vh[p] = e[0];
+            vl[p] = e[1];
+        }
+    } else {
+        uint64_t word = 0;  // big-endian group word of kBits bytes
+#pragma unroll
+        for (int k = 0; k < kBits; ++k) {
+            const int byte = s * kBits + k;
+            word = (word << 8) | ((cw.w[byte >> 2] >> (8 * (byte & 3))) & 0xffu);
+        }
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint32_t c0 = (uint32_t)(word >> (kBits * (7 - 2 * p))) & ((1u << kBits) - 1u);
+            const uint32_t c1 = (uint32_t)(word >> (kBits * (6 - 2 * p))) & ((1u << kBits) - 1u);
+            split_pair(t.tab[c0], t.tab[c1], vh[p], vl[p]);
+        }
+    }
+    bh = __builtin_bit_cast(f16x8, u32x4{vh[0], vh[1], vh[2], vh[3]});
+    bl = __builtin_bit_cast(f16x8, u32x4{vl[0], vl[1], vl[2], vl[3]});
+}
+
+// ---------------------------------------------------------------------------------------
+// MFMA dequantize of one tile by one wave, head_dim 128 (turboquant_decompress.cu:21-94):
+//   unpack -> c[idx] -> x_hat = Pi^T y_hat -> fp16(x_hat * float(norm)).
+// Lane (r, h) ends block c holding coordinates 32c + 8g + 4h + e of row r; neighbouring
+// chunks are exchanged with the partner lane so every lane stores 16 contiguous bytes.
+// ---------------------------------------------------------------------------------------
+template <int kBits>
+__device__ __forceinline__ void dequant_tile(const DequantLds& t, const RotLds& L,
+                                             const CodeHalf<kBits>& cw,
+                                             uint16_t* __restrict__ out, int64_t m0, int nvalid) {
+    const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
+    f16x8 bh[8], bl[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) decode_group<kBits>(t, cw, s, bh[s], bl[s]);
+    const float nrm = h2f(cw.norm);
+    uint16_t* orow = out + m0 * kHd + (r * kHd + 8 * h);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        __builtin_amdgcn_sched_barrier(0);  // keep each block's fragment loads within it
         f32x16 acc1 = {}, acc2 = {};
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-            const f16x8 bh = *(const f16x8*)&sh.yhi[r * kXStride + 16 * s + 8 * h];
-            const f16x8 bl = *(const f16x8*)&sh.ylo[r * kXStride + 16 * s + 8 * h];
-            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi[s], bh, acc1, 0, 0, 0);
-            acc2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo[s], bh, acc2, 0, 0, 0);
-            acc2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi[s], bl, acc2, 0, 0, 0);
+            const f16x8 ah = frag(L, c, s, 0, lane), al = frag(L, c, s, 1, lane);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bh[s], acc1, 0, 0, 0);
+            acc2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh[s], acc2, 0, 0, 0);
+            acc2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bl[s], acc2, 0, 0, 0);
         }
-        if (r < nvalid) {
-            const float nrm = h2f(norms[m0 + r]);
-            uint16_t* orow = out + (m0 + r) * kHd;
+        uint32_t ch[4][2];  // chunk g: coordinates 32c + 8g + 4h + 0..3 as fp16 pairs
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                uint32_t w[2];
+        for (int g = 0; g < 4; ++g) {
 #pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const float x0 = (acc1[4 * g + 2 * e] + acc2[4 * g + 2 * e] * kLoInv) * nrm;
-                    const float x1 =
-                        (acc1[4 * g + 2 * e + 1] + acc2[4 * g + 2 * e + 1] * kLoInv) * nrm;
-                    w[e] = f2h(x0) | (f2h(x1) << 16);
-                }
-                u32x2 wv = {w[0], w[1]};
-                *(u32x2*)&orow[32 * wave + 8 * g + 4 * h] = wv;
+            for (int e = 0; e < 2; ++e) {
+                const float x0 = fmaf(acc2[4 * g + 2 * e], kLoInv, acc1[4 * g + 2 * e]) * nrm;
+                const float x1 =
+                    fmaf(acc2[4 * g + 2 * e + 1], kLoInv, acc1[4 * g + 2 * e + 1]) * nrm;
+                ch[g][e] = f2h(x0) | (f2h(x1) << 16);
             }
         }
+        // chunks (2m, 2m+1): lane h = 0 takes coordinates 16m + 0..7, lane h = 1 16m + 8..15
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) swap_halves(ch[2 * m][e], ch[2 * m + 1][e]);
+            if (r < nvalid)
+                *(u32x4*)&orow[32 * c + 16 * m] =
+                    u32x4{ch[2 * m][0], ch[2 * m][1], ch[2 * m + 1][0], ch[2 * m + 1][1]};
+        }
+    }
+}
+
+template <int kBits>
+__global__ __launch_bounds__(64 * kWavesD) __attribute__((amdgpu_waves_per_eu(3))) void
+tq_dequant_mfma_kernel(const uint8_t* __restrict__ packed, const uint16_t* __restrict__ norms,
+                       const float* __restrict__ rot, const float* __restrict__ cent, int L,
+                       uint16_t* __restrict__ out, int64_t rows) {
+    __shared__ DequantLds t;
+    __shared__ RotLds rl;
+    const int64_t ntiles = ceil_div(rows, kTile);
+    const int64_t stride = (int64_t)gridDim.x * kWavesD;
+    int64_t tile = (int64_t)blockIdx.x * kWavesD + (threadIdx.x >> 6);
+    // The first tile's loads go out before the set-up, which then overlaps their latency.
+    CodeHalf<kBits> ca, cb;
+    load_code_half<kBits>(packed, norms, tile, ntiles, rows, ca);
+    for (int i = threadIdx.x; i < kMaxLevels; i += blockDim.x) {
+        const float c = i < L ? cent[i] : 0.0f;
+        const _Float16 hi = (_Float16)c;
+        const uint32_t hb = __builtin_bit_cast(uint16_t, hi);
+        const uint32_t lb = __builtin_bit_cast(uint16_t, (_Float16)((c - (float)hi) * kLoScale));
+        t.tab[i] = hb | (lb << 16);
+    }
+    stage_rotation<true>(rot, rl);
+    __syncthreads();
+    if constexpr (kBits == 4) {
+        for (int b = threadIdx.x; b < 256; b += blockDim.x) {
+            uint32_t vh, vl;
+            split_pair(t.tab[b >> 4], t.tab[b & 15], vh, vl);
+            t.pair[b] = u32x2{vh, vl};
+        }
         __syncthreads();
+    }
+    while (tile < ntiles) {
+        load_code_half<kBits>(packed, norms, tile + stride, ntiles, rows, cb);
+        dequant_tile<kBits>(t, rl, ca, out, tile * kTile,
+                            (int)min<int64_t>(kTile, rows - tile * kTile));
+        tile += stride;
+        if (tile >= ntiles) break;
+        load_code_half<kBits>(packed, norms, tile + stride, ntiles, rows, ca);
+        dequant_tile<kBits>(t, rl, cb, out, tile * kTile,
+                            (int)min<int64_t>(kTile, rows - tile * kTile));
+        tile += stride;
     }
 }
 
@@ -436,15 +628,33 @@ bool tq_args_ok(int n_levels, int bits) {
            n_levels <= kMaxLevels;
 }
 
+// Grid of the MFMA kernels: one workgroup per CU (each stages the rotation once), never
+// more workgroups than needed to give every wave a tile.
+int mfma_grid(int64_t ntiles, int waves) {
+    const int64_t need = ceil_div(ntiles, waves);
+    const int64_t cus = fhip_host::cu_count();
+    return (int)(need < cus ? (need > 0 ? need : 1) : cus);
+}
+
 template <int kMode, class Dst>
 int launch_compress(const void* input, const float* rot, const float* cent, int L, int bits,
                     Dst dst, float* y_out, int64_t rows, int hd, hipStream_t s) {
     if (rows == 0) return hipSuccess;
-    if (hd == kHd && fhip_host::aligned16(input) && fhip_host::aligned16(rot) &&
+    const bool mfma_bits = kMode == 1 || bits == 2 || bits == 3 || bits == 4 || bits == 8;
+    if (hd == kHd && mfma_bits && fhip_host::aligned16(input) &&
         (kMode == 0 || fhip_host::aligned16(y_out))) {
-        const int grid = tq_grid(ceil_div(rows, kTile), 1024);
-        hipLaunchKernelGGL((tq_compress_mfma_kernel<kMode, Dst>), dim3(grid), dim3(256), 0, s,
-                           (const uint16_t*)input, rot, cent, L, bits, dst, y_out, rows);
+        auto kern = tq_compress_mfma_kernel<kMode, 4, Dst>;
+        if constexpr (kMode == 0) {
+            switch (bits) {
+                case 2: kern = tq_compress_mfma_kernel<kMode, 2, Dst>; break;
+                case 3: kern = tq_compress_mfma_kernel<kMode, 3, Dst>; break;
+                case 8: kern = tq_compress_mfma_kernel<kMode, 8, Dst>; break;
+                default: break;
+            }
+        }
+        hipLaunchKernelGGL(kern, dim3(mfma_grid(ceil_div(rows, kTile), kWavesC)),
+                           dim3(64 * kWavesC), 0, s, (const uint16_t*)input, rot, cent, L, dst,
+                           y_out, rows);
     } else {
         const int grid = tq_grid(rows, 2048);
         const size_t lds = 2 * (size_t)hd * sizeof(float);
@@ -538,12 +748,20 @@ int fhip_launch_tq_dequant(const void* packed_in, const void* norms_in, const fl
         return hipErrorInvalidValue;
     hipStream_t s = fhip_host::as_stream(stream);
     const int L = n_levels;
-    if (head_dim == kHd && fhip_host::aligned16(output) && fhip_host::aligned16(rotation)) {
-        const int grid = tq_grid(ceil_div(rows, kTile), 1024);
-        hipLaunchKernelGGL(tq_dequant_mfma_kernel, dim3(grid), dim3(256), 0, s,
-                           (const uint8_t*)packed_in, (const uint16_t*)norms_in, rotation,
-                           centroids, L, bits, (uint16_t*)output, rows,
-                           (int64_t)packed_dim_per_head);
+    const bool mfma_bits = bits == 2 || bits == 3 || bits == 4 || bits == 8;
+    if (head_dim == kHd && mfma_bits && packed_dim_per_head == 16 * bits &&
+        fhip_host::aligned16(output) && fhip_host::aligned16(packed_in) &&
+        (((uintptr_t)norms_in) & 1u) == 0) {
+        auto kern = tq_dequant_mfma_kernel<4>;
+        switch (bits) {
+            case 2: kern = tq_dequant_mfma_kernel<2>; break;
+            case 3: kern = tq_dequant_mfma_kernel<3>; break;
+            case 8: kern = tq_dequant_mfma_kernel<8>; break;
+            default: break;
+        }
+        hipLaunchKernelGGL(kern, dim3(mfma_grid(ceil_div(rows, kTile), kWavesD)),
+                           dim3(64 * kWavesD), 0, s, (const uint8_t*)packed_in, (const uint16_t*)norms_in, rotation,
+                           centroids, L, (uint16_t*)output, rows);
     } else {
         const int grid = tq_grid(rows, 2048);
         hipLaunchKernelGGL(tq_dequant_generic_kernel, dim3(grid), dim3(256),

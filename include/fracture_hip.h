@@ -142,7 +142,8 @@ int fhip_launch_add_rmsnorm(void* residual, const void* delta, const void* weigh
 /* Row softmax / argmax over fp32 logits [rows, cols] (the sampler's greedy and softmax paths,
  * sampling.rs:45-82). argmax ties resolve to the LAST index (Iterator::max_by); flags_out
  * gets FHIP_ROW_HAS_NAN / FHIP_ROW_HAS_INF per row. probs = exp(l/T - max) / sum.
- * The workspace holds per-chunk partials; size it with fhip_rows_workspace_bytes. */
+ * The workspace holds per-chunk partials; size it with fhip_rows_workspace_bytes. Calls
+ * sharing a workspace must be ordered on one stream. Each op is two launches. */
 size_t fhip_rows_workspace_bytes(int rows, int cols);
 int fhip_launch_softmax_rows(const float* logits, float* probs, int rows, int cols,
                              float temperature, void* workspace, fhip_stream_t stream);
