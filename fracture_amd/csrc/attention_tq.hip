@@ -38,6 +38,25 @@ struct PtrPages {
     __device__ const uint8_t* knorm(int p) const { return kn[p]; }
     __device__ const uint8_t* vpage(int p) const { return vp[p]; }
     __device__ const uint8_t* vnorm(int p) const { return vn[p]; }
+    // Wave-wide page cache: lane j loads the four pointers of page `p` (its page of the
+    // current split); the `_at` accessors read them back from lane j.
+    struct Lane {
+        const uint8_t *k, *kn, *v, *vn;
+    };
+    __device__ Lane lane_load(int p) const {
+        if (!valid(p)) return Lane{nullptr, nullptr, nullptr, nullptr};
+        return Lane{kp[p], kn[p], vp[p], vn[p]};
+    }
+    static __device__ const uint8_t* rl(const uint8_t* x, int j) {
+        const uint64_t u = (uint64_t)x;
+        const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)u, j);
+        const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), j);
+        return (const uint8_t*)(((uint64_t)hi << 32) | lo);
+    }
+    __device__ const uint8_t* kpage_at(const Lane& l, int j, int) const { return rl(l.k, j); }
+    __device__ const uint8_t* knorm_at(const Lane& l, int j, int) const { return rl(l.kn, j); }
+    __device__ const uint8_t* vpage_at(const Lane& l, int j, int) const { return rl(l.v, j); }
+    __device__ const uint8_t* vnorm_at(const Lane& l, int j, int) const { return rl(l.vn, j); }
 };
 struct PoolPages {
     const uint8_t* kp;
@@ -51,6 +70,13 @@ struct PoolPages {
     __device__ const uint8_t* knorm(int p) const { return kn + p * skn; }
     __device__ const uint8_t* vpage(int p) const { return vp + p * svp; }
     __device__ const uint8_t* vnorm(int p) const { return vn + p * svn; }
+    // Page addresses are arithmetic on the id: the wave-wide page cache holds nothing.
+    struct Lane {};
+    __device__ Lane lane_load(int) const { return Lane{}; }
+    __device__ const uint8_t* kpage_at(const Lane&, int, int p) const { return kpage(p); }
+    __device__ const uint8_t* knorm_at(const Lane&, int, int p) const { return knorm(p); }
+    __device__ const uint8_t* vpage_at(const Lane&, int, int p) const { return vpage(p); }
+    __device__ const uint8_t* vnorm_at(const Lane&, int, int p) const { return vnorm(p); }
 };
 
 // Query q_i reads block-table row i (stride 0: one shared table) and attends to
@@ -61,6 +87,7 @@ struct Queries {
     int max_blocks;
     const int32_t* seq_lens;
     int kv_len, start_pos;
+    int seq_lens_count;  // number of queries (set by the MFMA launcher)
     __device__ int causal_len(int qi) const {
         int c;
         if (seq_lens) {
@@ -352,6 +379,492 @@ __global__ __launch_bounds__(256) void tq_attn_combine_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// 2'. MFMA split kernel: head_dim 128, 4-bit K and V codes, G <= 8 query heads per kv head.
+//
+// One wave per (query, kv head, 1024-position split) walks 64-position chunks:
+//   QK  D[pos][col] = sum_k A[pos][k] B[k][col] on v_mfma_f32_16x16x32_f16. The K slots come
+//       in (hi, lo') pairs per coordinate: A = (c_hi, c_lo*2^12) of the position's centroid,
+//       B = (q_hi, 0) in column h and (q_lo*2^12, q_hi) in column 8+h, so one MFMA gives
+//       D[h] = sum c_hi q_hi and D[8+h] = 2^12 (sum c_hi q_lo + c_lo q_hi), and the score is
+//       (D[h] + 2^-12 D[8+h]) * norm_k / sqrt(128): fp16 operands, ~fp32 accuracy, no fp16
+//       subnormals. A fragments come from a 16-entry LDS table code -> (c_hi | c_lo' << 16).
+//   PV  out[h][d] accumulates W[h][pos] V[pos][d] the same way: B = (v_hi, v_lo') of the V
+//       code, A = (w_hi, 0) in row h and (w_lo*2^12, w_hi) in row 8+h, w = p * norm_v.
+//       The B operand needs 4 positions of one coordinate per lane; ds_read_b64_tr_b4 reads
+//       them transposed out of the chunk's V code rows staged in LDS in their page layout.
+// Chunk position order: QK tile pt (16 rows) holds positions 4i + pt, so the 4 scores a lane
+// ends up with for tile pt (rows 4rg..4rg+3) are positions 16rg + 4e + pt, and the PV
+// K slots of lane group rg in tile pt are those same positions: no score shuffling.
+// Online softmax per head (lanes n = h), lazily rescaling the accumulators.
+// ---------------------------------------------------------------------------------------
+constexpr int kChunkM = 64;     // positions per chunk
+constexpr int kWavesM = 4;      // waves per workgroup (independent work items)
+
+typedef int v2i_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ uint32_t hi_lo_pair(float v, float& hi_f) {
+    const _Float16 hi = (_Float16)v;
+    hi_f = (float)hi;
+    const _Float16 lo = (_Float16)((v - hi_f) * 4096.0f);
+    return (uint32_t)__builtin_bit_cast(uint16_t, hi) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
+}
+__device__ __forceinline__ float ror8(float v) {  // lane n of each 16-lane row gets lane n^8
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, true));
+}
+// (byte kByte of x) & 0x3C in one v_and_b32_sdwa. Written as asm: the compiler turns the
+// shift-and-mask into two instructions for most byte positions.
+template <int kByte>
+__device__ __forceinline__ uint32_t byte_x4(uint32_t x) {
+    uint32_t r;
+    if constexpr (kByte == 0)
+        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0 src1_sel:DWORD"
+            : "=v"(r) : "v"(x), "s"(0x3Cu));
+    else if constexpr (kByte == 1)
+        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1 src1_sel:DWORD"
+            : "=v"(r) : "v"(x), "s"(0x3Cu));
+    else if constexpr (kByte == 2)
+        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2 src1_sel:DWORD"
+            : "=v"(r) : "v"(x), "s"(0x3Cu));
+    else
+        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3 src1_sel:DWORD"
+            : "=v"(r) : "v"(x), "s"(0x3Cu));
+    return r;
+}
+__device__ __forceinline__ uint32_t tab_at(const uint32_t* tab, uint32_t byte_off) {
+    return *(const uint32_t*)((const char*)tab + byte_off);
+}
+// Table entries of the nibbles of bytes kB, kB + 1 of a code word w, given wh = w >> 2 and
+// wl = w << 2 (byte k of wh & 0x3C = 4 x high nibble of byte k; of wl: 4 x low nibble).
+// Returns {hi(kB), lo(kB), hi(kB+1), lo(kB+1)}.
+template <int kB>
+__device__ __forceinline__ u32x4 tab_hl2(const uint32_t* tab, uint32_t wh, uint32_t wl) {
+    return u32x4{tab_at(tab, byte_x4<kB>(wh)), tab_at(tab, byte_x4<kB>(wl)),
+                 tab_at(tab, byte_x4<kB + 1>(wh)), tab_at(tab, byte_x4<kB + 1>(wl))};
+}
+// Same nibbles, low nibble first: {lo(kB), hi(kB), lo(kB+1), hi(kB+1)}.
+template <int kB>
+__device__ __forceinline__ u32x4 tab_lh2(const uint32_t* tab, uint32_t wh, uint32_t wl) {
+    return u32x4{tab_at(tab, byte_x4<kB>(wl)), tab_at(tab, byte_x4<kB>(wh)),
+                 tab_at(tab, byte_x4<kB + 1>(wl)), tab_at(tab, byte_x4<kB + 1>(wh))};
+}
+
+// The 4 pages of the chunk starting at t0 (page k: positions t0 + 16k .. +15; -1 past the end),
+// the mask of those holding positions to read, and the lane of the split's page cache that
+// holds page 0 (lane j caches page j of the split).
+struct ChunkPages {
+    int id[4];
+    uint32_t mask;
+    int j0;
+};
+template <class Pages>
+__device__ __forceinline__ ChunkPages chunk_pages(const Pages& pg, int split_page, int t_begin,
+                                                  int t0, int t_end) {
+    ChunkPages c;
+    c.mask = 0;
+    c.j0 = ((t0 - t_begin) / FHIP_PAGE_TOKENS) & 63;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int pos = t0 + 16 * k;
+        c.id[k] = pos < t_end ? __builtin_amdgcn_readlane(split_page, c.j0 + k) : -1;
+        if (pos < t_end && pg.valid(c.id[k])) c.mask |= 1u << k;
+    }
+    return c;
+}
+__device__ __forceinline__ const uint8_t* pick4(const uint8_t* const (&b)[4], int k) {
+    return k == 0 ? b[0] : k == 1 ? b[1] : k == 2 ? b[2] : b[3];
+}
+
+// Every lane issues the same copies whatever the chunk holds, so each chunk adds a fixed
+// number of memory instructions and the compiler's wait counts stay exact. A lane with no
+// position to read copies from `dummy` (16 readable bytes) instead.
+//
+// K codes of a chunk by LDS DMA: tile pt lands at kb + 1024 pt + 16 lane, i.e. lane (n, rg)
+// finds position 4n + pt, bytes [16rg, 16rg + 16) at its own slot.
+template <class Pages>
+__device__ __forceinline__ void dma_k(const Pages& pg, const typename Pages::Lane& pl,
+                                      const ChunkPages& c, int t0, int t_end, int kvh, int g,
+                                      uint8_t* kb, int lane, const uint8_t* dummy) {
+    const int n = lane & 15, rg = lane >> 4, k = n >> 2;
+    const uint8_t* base[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        base[i] = ((c.mask >> i) & 1u) ? pg.kpage_at(pl, c.j0 + i, c.id[i]) : dummy;
+    const bool page_ok = (c.mask >> k) & 1u;
+    const uint8_t* src = pick4(base, k) + ((int64_t)(4 * (n & 3)) * kvh + g) * 64 + 16 * rg;
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) {
+        const bool ok = page_ok && t0 + 4 * n + pt < t_end;
+        __builtin_amdgcn_global_load_lds(ok ? src + (int64_t)pt * kvh * 64 : dummy,
+                                         (lds_void_t*)(kb + 1024 * pt), 16, 0, 0);
+    }
+}
+// V codes of a chunk by LDS DMA: copy i moves page i (positions 16i .. 16i + 15); lane L takes
+// position p = 16i + L / 4 and stores 16 bytes at 64p + 16(L % 4). The 16-byte segment it
+// copies is (L % 4) ^ ((p / 2) % 4): rows are XOR-swizzled so the transposed reads of one
+// dim range from 16 rows spread over the banks.
+template <class Pages>
+__device__ __forceinline__ void dma_v(const Pages& pg, const typename Pages::Lane& pl,
+                                      const ChunkPages& c, int t0, int t_end, int64_t lane_off,
+                                      uint8_t* vb, int lane, const uint8_t* dummy) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const bool page_ok = (c.mask >> i) & 1u;
+        const uint8_t* base = page_ok ? pg.vpage_at(pl, c.j0 + i, c.id[i]) : dummy;
+        const bool ok = page_ok && t0 + 16 * i + (lane >> 2) < t_end;
+        __builtin_amdgcn_global_load_lds(ok ? base + lane_off : dummy,
+                                         (lds_void_t*)(vb + 1024 * i), 16, 0, 0);
+    }
+}
+// Norms of position t0 + lane, loaded raw: knorm | vnorm << 16 = pack() once they are
+// needed (0 where there is none). Packing later keeps the wait for them away from the copies
+// issued after them.
+struct NormRegs {
+    uint32_t k, v;
+    bool ok;
+    __device__ uint32_t pack() const {
+        uint32_t a = k, b = v;
+        // pins the pack here: the compiler would otherwise pack right after the loads
+        asm volatile("" : "+v"(a), "+v"(b));
+        return ok ? a | (b << 16) : 0u;
+    }
+};
+template <class Pages>
+__device__ __forceinline__ NormRegs load_norms(const Pages& pg, const typename Pages::Lane& pl,
+                                               const ChunkPages& c, int t0, int t_end, int kvh,
+                                               int g, int lane, const uint8_t* dummy) {
+    const uint8_t* kn[4];
+    const uint8_t* vn[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const bool ok = (c.mask >> i) & 1u;
+        kn[i] = ok ? pg.knorm_at(pl, c.j0 + i, c.id[i]) : dummy;
+        vn[i] = ok ? pg.vnorm_at(pl, c.j0 + i, c.id[i]) : dummy;
+    }
+    const int k = lane >> 4;
+    const bool ok = ((c.mask >> k) & 1u) && t0 + lane < t_end;
+    const int64_t row = ok ? (int64_t)(lane & 15) * kvh + g : 0;
+    return NormRegs{((const uint16_t*)pick4(kn, k))[row], ((const uint16_t*)pick4(vn, k))[row], ok};
+}
+
+// Reads of the DMA buffers, written as asm with their own waits. All loads of chunk i + 1
+// (norms, K copies, V copies) are issued together right after chunk i's QK; QK of chunk
+// i + 1 waits for all of them (vmcnt(0)) and PV of chunk i + 1 needs no further wait. The
+// compiler's own wait counting would also hold PV back for the copies issued after QK.
+// The "memory" clobber keeps every copy on its side of these reads.
+__device__ __forceinline__ void read_k_codes(const uint8_t* kb_lane, u32x4 (&kc)[4]) {
+    asm volatile(
+        "s_waitcnt vmcnt(0)\n"
+        "ds_read_b128 %0, %4\n"
+        "ds_read_b128 %1, %4 offset:1024\n"
+        "ds_read_b128 %2, %4 offset:2048\n"
+        "ds_read_b128 %3, %4 offset:3072\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(kc[0]), "=&v"(kc[1]), "=&v"(kc[2]), "=&v"(kc[3])
+        : "v"((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)kb_lane)
+        : "memory");
+}
+// Transposed V reads of dim tiles 0..7 (tile c at row segment (c / 2) ^ sw, half c % 2):
+// seg[s] is the lane's address of its row's segment s ^ sw.
+__device__ __forceinline__ void read_v_codes(const uint32_t (&seg)[4], v2i_t (&tv)[8]) {
+    asm volatile(
+        "ds_read_b64_tr_b4 %0, %8\n"
+        "ds_read_b64_tr_b4 %1, %8 offset:8\n"
+        "ds_read_b64_tr_b4 %2, %9\n"
+        "ds_read_b64_tr_b4 %3, %9 offset:8\n"
+        "ds_read_b64_tr_b4 %4, %10\n"
+        "ds_read_b64_tr_b4 %5, %10 offset:8\n"
+        "ds_read_b64_tr_b4 %6, %11\n"
+        "ds_read_b64_tr_b4 %7, %11 offset:8\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(tv[0]), "=&v"(tv[1]), "=&v"(tv[2]), "=&v"(tv[3]), "=&v"(tv[4]), "=&v"(tv[5]),
+          "=&v"(tv[6]), "=&v"(tv[7])
+        : "v"(seg[0]), "v"(seg[1]), "v"(seg[2]), "v"(seg[3])
+        : "memory");
+}
+
+template <class Pages>
+__global__ __launch_bounds__(64 * kWavesM) __attribute__((amdgpu_waves_per_eu(3))) void
+tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
+                    const float* __restrict__ kcent, const float* __restrict__ vcent, int qh,
+                    int kvh, float scale, float* __restrict__ part_ml,
+                    float* __restrict__ part_acc, int nsplit) {
+    constexpr int hd = 128;
+    // code -> (c_hi | c_lo' << 16); K table in words 0..15, V table in 16..31. Consecutive
+    // words sit in distinct banks, so lookups by any mix of codes are conflict-free. The DMA
+    // targets are separate objects: table reads never wait for DMA traffic.
+    __shared__ uint32_t tabs[32];
+    __shared__ __attribute__((aligned(16))) uint8_t kbuf[kWavesM][kChunkM * 64];
+    __shared__ __attribute__((aligned(16))) uint8_t vbuf[kWavesM][2][kChunkM * 64];  // by chunk parity
+    __shared__ __attribute__((aligned(16))) uint32_t nbuf[kWavesM][kChunkM];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 15, rg = lane >> 4;  // MFMA column / row group
+    if (threadIdx.x < 32) {
+        const int b = threadIdx.x & 15;
+        float hf;
+        tabs[threadIdx.x] = hi_lo_pair(threadIdx.x < 16 ? kcent[b] : vcent[b], hf);
+    }
+    __syncthreads();
+    const uint32_t* tk = tabs;
+    const uint32_t* tv = tabs + 16;
+
+    // items run kv head fastest: the heads of one (query, split) share a workgroup, so the two
+    // heads whose 64-byte rows share a 128-byte line read it together
+    const int64_t item = (int64_t)blockIdx.x * kWavesM + wave;
+    const int64_t per_q = (int64_t)kvh * nsplit;
+    const int qi = (int)(item / per_q);
+    if (qi >= qs.seq_lens_count) return;
+    const int g = (int)(item % kvh), split = (int)((item / kvh) % nsplit);
+    const int clen = qs.causal_len(qi);
+    const int t_begin = split * kSplit;
+    if (t_begin >= clen) return;
+    const int t_end = min(clen, t_begin + kSplit);
+    const int G = qh / kvh;
+    const int32_t* table = qs.table + (int64_t)qi * qs.table_stride;
+    uint8_t* kb = kbuf[wave];
+    uint8_t* vb = vbuf[wave][0];
+    uint32_t* nb = nbuf[wave];
+
+    // The split's pages, one per lane (a split is 64 pages), read once: the chunk loop then
+    // issues no memory instruction besides its copies.
+    static_assert(kSplit == 64 * FHIP_PAGE_TOKENS, "one cached page per lane");
+    const int split_page =
+        t_begin + FHIP_PAGE_TOKENS * lane < t_end ? table[t_begin / FHIP_PAGE_TOKENS + lane] : -1;
+    const typename Pages::Lane pl = pg.lane_load(split_page);
+
+    // first chunk's copies go out before the Q set-up
+    ChunkPages pc = chunk_pages(pg, split_page, t_begin, t_begin, t_end);
+    const int64_t v_lane_off =
+        ((int64_t)(lane >> 2) * kvh + g) * 64 + 16 * ((lane & 3) ^ ((lane >> 3) & 3));
+    const uint8_t* dummy = (const uint8_t*)kcent;  // 64 readable bytes
+    NormRegs nreg = load_norms(pg, pl, pc, t_begin, t_end, kvh, g, lane, dummy);
+    dma_k(pg, pl, pc, t_begin, t_end, kvh, g, kb, lane, dummy);
+    dma_v(pg, pl, pc, t_begin, t_end, v_lane_off, vb, lane, dummy);  // chunk 0: buffer 0
+    ChunkPages pn = chunk_pages(pg, split_page, t_begin, t_begin + kChunkM, t_end);
+
+    // Q as the QK B operand, pre-scaled by scale * log2(e) so scores come out in log2 units:
+    // step s, lane (n, rg) holds coordinates 32rg + 4s + c4.
+    uint32_t bq[8][4];
+    {
+        // heads past G read head 0 and are zeroed by the multiplier
+        const int h = n & 7;
+        const float* qsrc = qrot + ((int64_t)qi * qh + (int64_t)g * G + (h < G ? h : 0)) * hd;
+        const float qmul = h < G ? scale * 1.4426950408889634f : 0.0f;
+        f32x4_t qv[8];
+#pragma unroll
+        for (int s8 = 0; s8 < 8; ++s8) qv[s8] = *(const f32x4_t*)(qsrc + 32 * rg + 4 * s8);
+#pragma unroll
+        for (int s8 = 0; s8 < 8; ++s8) {
+#pragma unroll
+            for (int c4 = 0; c4 < 4; ++c4) {
+                const float q = qv[s8][c4] * qmul;
+                float qhf;
+                const uint32_t pr = hi_lo_pair(q, qhf);  // q_hi | q_lo' << 16
+                // column h: (q_hi, 0); column 8 + h: (q_lo', q_hi)
+                bq[s8][c4] = n < 8 ? (pr & 0xffffu) : ((pr >> 16) | (pr << 16));
+            }
+        }
+    }
+    // Score of head n & 7 in both lanes n and n ^ 8: D[h] + 2^-12 D[8 + h].
+    const float ca = n < 8 ? 1.0f : 1.0f / 4096.0f, cb = n < 8 ? 1.0f / 4096.0f : 1.0f;
+    // PV A operand of weight w: row h (lanes n < 8) takes (w_hi, 0), row 8 + h takes
+    // (w_lo', w_hi). Both come from r = pkrtz(w, w * wz) followed by
+    // r.lo = f16(r.lo * wb + w * wc): lanes n < 8 keep r.lo = w_hi and have r.hi = 0,
+    // lanes n >= 8 get r.lo = 2^12 (w - w_hi). w_hi is w rounded toward zero.
+    const float wz = n < 8 ? 0.0f : 1.0f, wb = n < 8 ? 1.0f : -4096.0f, wc = n < 8 ? 0.0f : 4096.0f;
+    // transposed V reads: source lane m of group rg reads position 16rg + 4(m % 4) + m / 4;
+    // segment s of that row sits at vrow[s ^ sw]
+    const int srow = 16 * rg + 4 * (n & 3) + (n >> 2);
+    const int sw = (srow >> 1) & 3;
+    uint32_t vseg[4];
+#pragma unroll
+    for (int sg = 0; sg < 4; ++sg)
+        vseg[sg] = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)(
+            vb + 64 * srow + 16 * (sg ^ sw));
+
+    float m_run = -__builtin_inff(), l_run = 0.0f;  // log2 units; lanes n, n ^ 8: head n & 7
+    f32x4_t acc[8];  // PV accumulators, dim tile c: rows 4rg..4rg+3, column n
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int t0 = t_begin, par = 0; t0 < t_end; t0 += kChunkM, par ^= 1) {
+        const int tn = t0 + kChunkM;  // next chunk
+        const ChunkPages pnn = chunk_pages(pg, split_page, t_begin, tn + kChunkM, t_end);
+        const bool full = pc.mask == 0xfu && tn <= t_end;
+
+        // ---- QK: 4 tiles x 8 steps, K codes from this wave's DMA buffer
+        float sc[4][4];  // [pt][e]: position 16rg + 4e + pt, head n & 7
+        u32x4 kcs[4];
+        read_k_codes(kb + 16 * lane, kcs);
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt) {
+            f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) {
+                const uint32_t w = kcs[pt][s2], wh = w >> 2, wl = w << 2;
+                // bytes 0, 1 of w: coordinates 8 s2 + 0..3; bytes 2, 3: 8 s2 + 4..7
+                const int s8 = 2 * s2;
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    __builtin_bit_cast(f16x8_t, tab_hl2<0>(tk, wh, wl)),
+                    __builtin_bit_cast(f16x8_t, u32x4{bq[s8][0], bq[s8][1], bq[s8][2], bq[s8][3]}),
+                    d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    __builtin_bit_cast(f16x8_t, tab_hl2<2>(tk, wh, wl)),
+                    __builtin_bit_cast(f16x8_t,
+                                       u32x4{bq[s8 + 1][0], bq[s8 + 1][1], bq[s8 + 1][2], bq[s8 + 1][3]}),
+                    d, 0, 0, 0);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sc[pt][e] = fmaf(ror8(d[e]), cb, d[e] * ca);
+        }
+        // ---- K norms; then the K buffer and the norm registers are free: all loads of the next
+        // chunk, its V codes into the other V buffer (after the last chunk: dummy copies)
+        nb[lane] = nreg.pack();
+        nreg = load_norms(pg, pl, pn, tn, t_end, kvh, g, lane, dummy);
+        dma_k(pg, pl, pn, tn, t_end, kvh, g, kb, lane, dummy);
+        dma_v(pg, pl, pn, tn, t_end, v_lane_off, vb + (par ^ 1) * (kChunkM * 64), lane, dummy);
+        f16x2_t nrm[16];  // positions 16rg + j: (knorm, vnorm)
+#pragma unroll
+        for (int j4 = 0; j4 < 4; ++j4) {
+            const u32x4 v = *(const u32x4*)&nb[16 * rg + 4 * j4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                // through a scalar: bit_cast of a vector element reads element 0 on this clang
+                const uint32_t word = v[t];
+                nrm[4 * j4 + t] = __builtin_bit_cast(f16x2_t, word);
+            }
+        }
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sc[pt][e] *= (float)nrm[4 * e + pt].x;
+        if (!full) {
+            const bool row_ok = (pc.mask >> rg) & 1u;
+#pragma unroll
+            for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (!(row_ok && t0 + 16 * rg + 4 * e + pt < t_end)) sc[pt][e] = -__builtin_inff();
+        }
+        float cmax = -__builtin_inff();
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) cmax = fmaxf(cmax, sc[pt][e]);
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+        const float m_new = fmaxf(m_run, cmax);
+        const float alpha =
+            m_run == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+        // ---- probabilities, weights, A operands of PV
+        uint32_t aw[4][4];  // [pt][e]
+        float psum = 0.0f;
+        const float mref = m_new == -__builtin_inff() ? 0.0f : m_new;
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float pr = __builtin_amdgcn_exp2f(sc[pt][e] - mref);
+                psum += pr;
+                const float w = pr * (float)nrm[4 * e + pt].y;
+                f16x2_t r = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_cvt_pkrtz(w, w * wz));
+                r.x = (_Float16)fmaf((float)r.x, wb, w * wc);
+                aw[pt][e] = __builtin_bit_cast(uint32_t, r);
+            }
+        }
+        psum += __shfl_xor(psum, 16);
+        psum += __shfl_xor(psum, 32);
+        l_run = l_run * alpha + psum;
+        // rescale the accumulators when some head's max moved
+        const bool moved_any = __ballot((n < G) && (rg == 0) && (m_new > m_run)) != 0;
+        if (moved_any) {
+            float al[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                // accumulator row 4rg + e belongs to head 4 (rg & 1) + e
+                const float a0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), e));
+                const float a1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), 4 + e));
+                al[e] = (rg & 1) ? a1 : a0;
+            }
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[c][e] *= al[e];
+        }
+        m_run = m_new;
+
+        // ---- PV: 8 dim tiles x 4 position tiles
+        v2i_t tvs[8];
+        {
+            const uint32_t vo = (uint32_t)par * (kChunkM * 64);
+            const uint32_t seg[4] = {vseg[0] + vo, vseg[1] + vo, vseg[2] + vo, vseg[3] + vo};
+            read_v_codes(seg, tvs);
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const v2i_t tvw = tvs[c];
+            // nibble 4pt + c4 = code of position (pt, c4) at dim 16c + (n ^ 1)
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+                const uint32_t w = (uint32_t)tvw[h2], wh = w >> 2, wl = w << 2;
+                acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    __builtin_bit_cast(f16x8_t, u32x4{aw[2 * h2][0], aw[2 * h2][1], aw[2 * h2][2], aw[2 * h2][3]}),
+                    __builtin_bit_cast(f16x8_t, tab_lh2<0>(tv, wh, wl)), acc[c], 0, 0, 0);
+                acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    __builtin_bit_cast(f16x8_t,
+                                       u32x4{aw[2 * h2 + 1][0], aw[2 * h2 + 1][1], aw[2 * h2 + 1][2], aw[2 * h2 + 1][3]}),
+                    __builtin_bit_cast(f16x8_t, tab_lh2<2>(tv, wh, wl)), acc[c], 0, 0, 0);
+            }
+        }
+        pc = pn;
+        pn = pnn;
+    }
+
+    // no copy may land in LDS after the wave has left
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    // ---- partials (m back in natural units): rows h (hi) + 2^-12 rows 8 + h (lo'),
+    // lanes l and l ^ 32
+    const int64_t head0 = (int64_t)qi * qh + (int64_t)g * G;
+    if (n < G && rg == 0) {
+        part_ml[((head0 + n) * nsplit + split) * 2 + 0] = m_run * 0.6931471805599453f;
+        part_ml[((head0 + n) * nsplit + split) * 2 + 1] = l_run;
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float other = __shfl_xor(acc[c][e], 32);
+            if (rg < 2) {
+                const int h = 4 * rg + e;
+                if (h < G) {
+                    const int dim = 16 * c + (n ^ 1);
+                    part_acc[((head0 + h) * nsplit + split) * hd + dim] = acc[c][e] + other * (1.0f / 4096.0f);
+                }
+            }
+        }
+    }
+}
+
+template <class Pages>
+void launch_mfma_split(const float* qrot, const Queries& qsv, const Pages& pg,
+                       const float* kcent, const float* vcent, int nq, int qh, int kvh,
+                       int nsplit, float* ml, float* acc, hipStream_t s) {
+    const int64_t items = (int64_t)nq * kvh * nsplit;
+    Queries q2 = qsv;
+    q2.seq_lens_count = nq;
+    hipLaunchKernelGGL((tq_attn_mfma_kernel<Pages>), dim3((unsigned)ceil_div(items, kWavesM)),
+                       dim3(64 * kWavesM), 0, s, qrot, q2, pg, kcent, vcent, qh, kvh,
+                       1.0f / sqrtf(128.0f), ml, acc, nsplit);
+}
+
 struct AttnArgs {
     void* out;
     const void* q;
@@ -397,7 +910,9 @@ int launch_attention(const AttnArgs& a, const Pages& pg, hipStream_t s) {
     float* acc = (float*)((char*)a.ws + off_acc);
     hipLaunchKernelGGL(tq_attn_prerotate_kernel, dim3(a.nq * a.qh), dim3(128), 0, s,
                        (const uint16_t*)a.q, a.krot, qrot, a.hd);
-    if (a.kbits == 4 && a.vbits == 4)
+    if (a.kbits == 4 && a.vbits == 4 && a.hd == 128 && a.qh / a.kvh <= 8)
+        launch_mfma_split(qrot, a.qs, pg, a.kcent, a.vcent, a.nq, a.qh, a.kvh, nsplit, ml, acc, s);
+    else if (a.kbits == 4 && a.vbits == 4)
         launch_split<4, 4>(a, pg, nsplit, ml, acc, s);
     else if (a.kbits == 4 && a.vbits == 2)
         launch_split<4, 2>(a, pg, nsplit, ml, acc, s);
@@ -450,7 +965,7 @@ int fhip_launch_attention_tq_decode(void* output, const void* q, const int32_t* 
     AttnArgs a;
     a.out = output;
     a.q = q;
-    a.qs = Queries{block_table, max_blocks, max_blocks, seq_lens, 0, 0};
+    a.qs = Queries{block_table, max_blocks, max_blocks, seq_lens, 0, 0, batch};
     a.nq = batch;
     a.krot = k_rotation;
     a.vrot = v_rotation;
@@ -503,7 +1018,7 @@ int fhip_launch_attention_paged_tq(void* output, const void* q, const int* block
     AttnArgs a;
     a.out = output;
     a.q = q;
-    a.qs = Queries{(const int32_t*)block_table, 0, mb, nullptr, kv_len, start_pos};
+    a.qs = Queries{(const int32_t*)block_table, 0, mb, nullptr, kv_len, start_pos, num_tokens};
     a.nq = num_tokens;
     a.krot = k_rotation;
     a.vrot = v_rotation;
