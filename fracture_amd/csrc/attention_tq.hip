@@ -123,20 +123,33 @@ __device__ __forceinline__ void row_group(const uint32_t* w, int g, int bits_rt,
     for (int i = 0; i < 8; ++i) codes[i] = (int)((word >> (bits * (7 - i))) & mask);
 }
 
-// 1. q_rot[qi, h, :] = Pi_k q[qi, h, :] (sequential fp32 dot, attention_paged_tq.cu:102-113).
+// 1. q_rot[v, :] = Pi_k q[v, :] (fp32 dots in coordinate order, attention_paged_tq.cu:102-113).
+// A workgroup rotates kRotVecs vectors so Pi_k is read once per workgroup: work unit
+// (row i, half) computes row i of vectors 4 half .. 4 half + 3.
+constexpr int kRotVecs = 8;
 __global__ __launch_bounds__(256) void tq_attn_prerotate_kernel(const uint16_t* __restrict__ q,
                                                                 const float* __restrict__ rot,
-                                                                float* __restrict__ qrot,
-                                                                int hd) {
-    __shared__ float qs[kMaxHd];
-    const int64_t v = blockIdx.x;
-    for (int j = threadIdx.x; j < hd; j += blockDim.x) qs[j] = h2f(q[v * hd + j]);
+                                                                float* __restrict__ qrot, int hd,
+                                                                int nvec) {
+    __shared__ float qs[kRotVecs][kMaxHd];
+    const int v0 = blockIdx.x * kRotVecs;
+    for (int e = threadIdx.x; e < kRotVecs * hd; e += blockDim.x) {
+        const int v = e / hd, j = e - v * hd;
+        qs[v][j] = v0 + v < nvec ? h2f(q[(int64_t)(v0 + v) * hd + j]) : 0.0f;
+    }
     __syncthreads();
-    for (int i = threadIdx.x; i < hd; i += blockDim.x) {
+    for (int r = threadIdx.x; r < 2 * hd; r += blockDim.x) {
+        const int i = r % hd, vb = 4 * (r / hd);
         const float* pr = rot + (int64_t)i * hd;
-        float dot = 0.0f;
-        for (int j = 0; j < hd; ++j) dot += pr[j] * qs[j];
-        qrot[v * hd + i] = dot;
+        float dot[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < hd; ++j) {
+            const float rv = pr[j];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) dot[k] += rv * qs[vb + k][j];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (v0 + vb + k < nvec) qrot[(int64_t)(v0 + vb + k) * hd + i] = dot[k];
     }
 }
 
@@ -481,16 +494,37 @@ __device__ __forceinline__ const uint8_t* pick4(const uint8_t* const (&b)[4], in
     return k == 0 ? b[0] : k == 1 ? b[1] : k == 2 ? b[2] : b[3];
 }
 
+// One 16-byte LDS DMA copy per lane: lane L writes lds + 16 L (lds wave-uniform). Issued as
+// asm so that the compiler, which counts pending LDS DMA against the LDS counter as well,
+// keeps exact LDS waits for the table lookups that run while copies are in flight (the
+// hardware tracks these copies on the vector memory counter only). Every read of the DMA
+// buffers waits for them explicitly.
+__device__ __forceinline__ void dma16(const uint8_t* src, uint8_t* lds) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds);
+    // m0 is saved and restored around the copy: the compiler may keep a value in it
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "global_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(src), "s"(m)
+        : "memory");
+}
+
 // Every lane issues the same copies whatever the chunk holds, so each chunk adds a fixed
 // number of memory instructions and the compiler's wait counts stay exact. A lane with no
 // position to read copies from `dummy` (16 readable bytes) instead.
 //
-// K codes of a chunk by LDS DMA: tile pt lands at kb + 1024 pt + 16 lane, i.e. lane (n, rg)
-// finds position 4n + pt, bytes [16rg, 16rg + 16) at its own slot.
+// K codes of a chunk, loaded straight into the registers QK uses (LDS DMA streams markedly
+// slower than vector loads, and K needs no LDS stage): tile pt is position 4n + pt, bytes
+// [16rg, 16rg + 16) for lane (n, rg).
 template <class Pages>
-__device__ __forceinline__ void dma_k(const Pages& pg, const typename Pages::Lane& pl,
-                                      const ChunkPages& c, int t0, int t_end, int kvh, int g,
-                                      uint8_t* kb, int lane, const uint8_t* dummy) {
+__device__ __forceinline__ void load_k(const Pages& pg, const typename Pages::Lane& pl,
+                                       const ChunkPages& c, int t0, int t_end, int kvh, int g,
+                                       int lane, const uint8_t* dummy, u32x4 (&kc)[4]) {
     const int n = lane & 15, rg = lane >> 4, k = n >> 2;
     const uint8_t* base[4];
 #pragma unroll
@@ -501,8 +535,7 @@ __device__ __forceinline__ void dma_k(const Pages& pg, const typename Pages::Lan
 #pragma unroll
     for (int pt = 0; pt < 4; ++pt) {
         const bool ok = page_ok && t0 + 4 * n + pt < t_end;
-        __builtin_amdgcn_global_load_lds(ok ? src + (int64_t)pt * kvh * 64 : dummy,
-                                         (lds_void_t*)(kb + 1024 * pt), 16, 0, 0);
+        kc[pt] = ld16(ok ? src + (int64_t)pt * kvh * 64 : dummy);
     }
 }
 // V codes of a chunk by LDS DMA: copy i moves page i (positions 16i .. 16i + 15); lane L takes
@@ -518,8 +551,7 @@ __device__ __forceinline__ void dma_v(const Pages& pg, const typename Pages::Lan
         const bool page_ok = (c.mask >> i) & 1u;
         const uint8_t* base = page_ok ? pg.vpage_at(pl, c.j0 + i, c.id[i]) : dummy;
         const bool ok = page_ok && t0 + 16 * i + (lane >> 2) < t_end;
-        __builtin_amdgcn_global_load_lds(ok ? base + lane_off : dummy,
-                                         (lds_void_t*)(vb + 1024 * i), 16, 0, 0);
+        dma16(ok ? base + lane_off : dummy, vb + 1024 * i);
     }
 }
 // Norms of position t0 + lane, loaded raw: knorm | vnorm << 16 = pack() once they are
@@ -553,23 +585,11 @@ __device__ __forceinline__ NormRegs load_norms(const Pages& pg, const typename P
     return NormRegs{((const uint16_t*)pick4(kn, k))[row], ((const uint16_t*)pick4(vn, k))[row], ok};
 }
 
-// Reads of the DMA buffers, written as asm with their own waits. All loads of chunk i + 1
-// (norms, K copies, V copies) are issued together right after chunk i's QK; QK of chunk
-// i + 1 waits for all of them (vmcnt(0)) and PV of chunk i + 1 needs no further wait. The
-// compiler's own wait counting would also hold PV back for the copies issued after QK.
+// Loads of chunk i + 1 (V codes by LDS DMA, then norms and K codes into registers) are issued
+// together right after chunk i's QK, and chunk i + 1 starts by waiting for all of them
+// (vmcnt(0)), so its PV reads the V buffer with no further wait. The transposed V reads are
+// asm: the compiler's own wait counting would also hold PV back for the loads issued after QK.
 // The "memory" clobber keeps every copy on its side of these reads.
-__device__ __forceinline__ void read_k_codes(const uint8_t* kb_lane, u32x4 (&kc)[4]) {
-    asm volatile(
-        "s_waitcnt vmcnt(0)\n"
-        "ds_read_b128 %0, %4\n"
-        "ds_read_b128 %1, %4 offset:1024\n"
-        "ds_read_b128 %2, %4 offset:2048\n"
-        "ds_read_b128 %3, %4 offset:3072\n"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(kc[0]), "=&v"(kc[1]), "=&v"(kc[2]), "=&v"(kc[3])
-        : "v"((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)kb_lane)
-        : "memory");
-}
 // Transposed V reads of dim tiles 0..7 (tile c at row segment (c / 2) ^ sw, half c % 2):
 // seg[s] is the lane's address of its row's segment s ^ sw.
 __device__ __forceinline__ void read_v_codes(const uint32_t (&seg)[4], v2i_t (&tv)[8]) {
@@ -600,7 +620,6 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     // words sit in distinct banks, so lookups by any mix of codes are conflict-free. The DMA
     // targets are separate objects: table reads never wait for DMA traffic.
     __shared__ uint32_t tabs[32];
-    __shared__ __attribute__((aligned(16))) uint8_t kbuf[kWavesM][kChunkM * 64];
     __shared__ __attribute__((aligned(16))) uint8_t vbuf[kWavesM][2][kChunkM * 64];  // by chunk parity
     __shared__ __attribute__((aligned(16))) uint32_t nbuf[kWavesM][kChunkM];
     const int lane = threadIdx.x & 63;
@@ -628,7 +647,6 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     const int t_end = min(clen, t_begin + kSplit);
     const int G = qh / kvh;
     const int32_t* table = qs.table + (int64_t)qi * qs.table_stride;
-    uint8_t* kb = kbuf[wave];
     uint8_t* vb = vbuf[wave][0];
     uint32_t* nb = nbuf[wave];
 
@@ -644,9 +662,10 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     const int64_t v_lane_off =
         ((int64_t)(lane >> 2) * kvh + g) * 64 + 16 * ((lane & 3) ^ ((lane >> 3) & 3));
     const uint8_t* dummy = (const uint8_t*)kcent;  // 64 readable bytes
-    NormRegs nreg = load_norms(pg, pl, pc, t_begin, t_end, kvh, g, lane, dummy);
-    dma_k(pg, pl, pc, t_begin, t_end, kvh, g, kb, lane, dummy);
     dma_v(pg, pl, pc, t_begin, t_end, v_lane_off, vb, lane, dummy);  // chunk 0: buffer 0
+    NormRegs nreg = load_norms(pg, pl, pc, t_begin, t_end, kvh, g, lane, dummy);
+    u32x4 kreg[4];
+    load_k(pg, pl, pc, t_begin, t_end, kvh, g, lane, dummy, kreg);
     ChunkPages pn = chunk_pages(pg, split_page, t_begin, t_begin + kChunkM, t_end);
 
     // Q as the QK B operand, pre-scaled by scale * log2(e) so scores come out in log2 units:
@@ -690,7 +709,9 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
             vb + 64 * srow + 16 * (sg ^ sw));
 
     float m_run = -__builtin_inff(), l_run = 0.0f;  // log2 units; lanes n, n ^ 8: head n & 7
-    f32x4_t acc[8];  // PV accumulators, dim tile c: rows 4rg..4rg+3, column n
+    // PV accumulators out^T, dim tile c: lane (n, rg) holds head slot n (n < 8: head n, hi
+    // part; n >= 8: head n - 8, lo' part) at dims 16c + ((4rg + e) ^ 1), e = 0..3
+    f32x4_t acc[8];
 #pragma unroll
     for (int c = 0; c < 8; ++c) acc[c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
@@ -701,35 +722,46 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
 
         // ---- QK: 4 tiles x 8 steps, K codes from this wave's DMA buffer
         float sc[4][4];  // [pt][e]: position 16rg + 4e + pt, head n & 7
-        u32x4 kcs[4];
-        read_k_codes(kb + 16 * lane, kcs);
+        // all loads of this chunk are in (the V copies included)
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const u32x4 kcs[4] = {kreg[0], kreg[1], kreg[2], kreg[3]};
+        // 32 MFMA steps t = (tile pt, word s2, half): the A operand of step t holds the table
+        // entries of bytes 2 half, 2 half + 1 of word s2 (coordinates 8 s2 + 4 half + 0..3).
+        // Table reads run kLookAhead steps ahead of their MFMA, so their LDS latency is
+        // covered by the MFMAs in between.
+        constexpr int kLookAhead = 2;
+        auto qk_a = [&](int t) -> u32x4 {
+            const uint32_t w = kcs[t >> 3][(t >> 1) & 3];
+            return (t & 1) ? tab_hl2<2>(tk, w >> 2, w << 2) : tab_hl2<0>(tk, w >> 2, w << 2);
+        };
+        {
+            u32x4 ahead[kLookAhead + 1];
 #pragma unroll
-        for (int pt = 0; pt < 4; ++pt) {
+            for (int t = 0; t < kLookAhead; ++t) ahead[t] = qk_a(t);
             f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int s2 = 0; s2 < 4; ++s2) {
-                const uint32_t w = kcs[pt][s2], wh = w >> 2, wl = w << 2;
-                // bytes 0, 1 of w: coordinates 8 s2 + 0..3; bytes 2, 3: 8 s2 + 4..7
-                const int s8 = 2 * s2;
+            for (int t = 0; t < 32; ++t) {
+                if (t + kLookAhead < 32) ahead[(t + kLookAhead) % (kLookAhead + 1)] = qk_a(t + kLookAhead);
+                const int s8 = t & 7;  // Q step 2 s2 + half
                 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    __builtin_bit_cast(f16x8_t, tab_hl2<0>(tk, wh, wl)),
+                    __builtin_bit_cast(f16x8_t, ahead[t % (kLookAhead + 1)]),
                     __builtin_bit_cast(f16x8_t, u32x4{bq[s8][0], bq[s8][1], bq[s8][2], bq[s8][3]}),
                     d, 0, 0, 0);
-                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    __builtin_bit_cast(f16x8_t, tab_hl2<2>(tk, wh, wl)),
-                    __builtin_bit_cast(f16x8_t,
-                                       u32x4{bq[s8 + 1][0], bq[s8 + 1][1], bq[s8 + 1][2], bq[s8 + 1][3]}),
-                    d, 0, 0, 0);
-            }
+                if ((t & 7) == 7) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) sc[pt][e] = fmaf(ror8(d[e]), cb, d[e] * ca);
+                    for (int e = 0; e < 4; ++e) sc[t >> 3][e] = fmaf(ror8(d[e]), cb, d[e] * ca);
+                    d = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+                // keeps the scheduler from sinking the look-ahead reads to their MFMAs
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
-        // ---- K norms; then the K buffer and the norm registers are free: all loads of the next
-        // chunk, its V codes into the other V buffer (after the last chunk: dummy copies)
+        // ---- K norms; then the K and norm registers are free: all loads of the next chunk,
+        // its V codes into the other V buffer (after the last chunk: dummy copies)
         nb[lane] = nreg.pack();
-        nreg = load_norms(pg, pl, pn, tn, t_end, kvh, g, lane, dummy);
-        dma_k(pg, pl, pn, tn, t_end, kvh, g, kb, lane, dummy);
         dma_v(pg, pl, pn, tn, t_end, v_lane_off, vb + (par ^ 1) * (kChunkM * 64), lane, dummy);
+        nreg = load_norms(pg, pl, pn, tn, t_end, kvh, g, lane, dummy);
+        load_k(pg, pl, pn, tn, t_end, kvh, g, lane, dummy, kreg);
         f16x2_t nrm[16];  // positions 16rg + j: (knorm, vnorm)
 #pragma unroll
         for (int j4 = 0; j4 < 4; ++j4) {
@@ -782,21 +814,13 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
         psum += __shfl_xor(psum, 16);
         psum += __shfl_xor(psum, 32);
         l_run = l_run * alpha + psum;
-        // rescale the accumulators when some head's max moved
+        // rescale the accumulators when some head's max moved (each lane holds its own head's)
         const bool moved_any = __ballot((n < G) && (rg == 0) && (m_new > m_run)) != 0;
         if (moved_any) {
-            float al[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                // accumulator row 4rg + e belongs to head 4 (rg & 1) + e
-                const float a0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), e));
-                const float a1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), 4 + e));
-                al[e] = (rg & 1) ? a1 : a0;
-            }
 #pragma unroll
             for (int c = 0; c < 8; ++c)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc[c][e] *= al[e];
+                for (int e = 0; e < 4; ++e) acc[c][e] *= alpha;
         }
         m_run = m_new;
 
@@ -807,20 +831,30 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
             const uint32_t seg[4] = {vseg[0] + vo, vseg[1] + vo, vseg[2] + vo, vseg[3] + vo};
             read_v_codes(seg, tvs);
         }
+        // out^T = V^T W^T: the V entries are the A operand (row m: dim 16c + (m ^ 1)), the
+        // weights the B operand (column n: head slot n). 32 MFMA steps t = (position tile pt,
+        // dim tile c): nibble 4pt + c4 of dim tile c's transposed read is the code of position
+        // (pt, c4) at dim 16c + (n ^ 1); tile pt sits in word pt / 2, bytes 2 (pt % 2),
+        // 2 (pt % 2) + 1. Table reads run kLookAhead steps ahead as in QK.
+        auto pv_b = [&](int t) -> u32x4 {
+            const int pt = t >> 3, c = t & 7;
+            const uint32_t w = (uint32_t)tvs[c][pt >> 1];
+            return (pt & 1) ? tab_lh2<2>(tv, w >> 2, w << 2) : tab_lh2<0>(tv, w >> 2, w << 2);
+        };
+        {
+            constexpr int kAheadPv = kLookAhead;
+            u32x4 ahead[kAheadPv + 1];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const v2i_t tvw = tvs[c];
-            // nibble 4pt + c4 = code of position (pt, c4) at dim 16c + (n ^ 1)
+            for (int t = 0; t < kAheadPv; ++t) ahead[t] = pv_b(t);
 #pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2) {
-                const uint32_t w = (uint32_t)tvw[h2], wh = w >> 2, wl = w << 2;
+            for (int t = 0; t < 32; ++t) {
+                if (t + kAheadPv < 32) ahead[(t + kAheadPv) % (kAheadPv + 1)] = pv_b(t + kAheadPv);
+                const int pt = t >> 3, c = t & 7;
                 acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    __builtin_bit_cast(f16x8_t, u32x4{aw[2 * h2][0], aw[2 * h2][1], aw[2 * h2][2], aw[2 * h2][3]}),
-                    __builtin_bit_cast(f16x8_t, tab_lh2<0>(tv, wh, wl)), acc[c], 0, 0, 0);
-                acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    __builtin_bit_cast(f16x8_t,
-                                       u32x4{aw[2 * h2 + 1][0], aw[2 * h2 + 1][1], aw[2 * h2 + 1][2], aw[2 * h2 + 1][3]}),
-                    __builtin_bit_cast(f16x8_t, tab_lh2<2>(tv, wh, wl)), acc[c], 0, 0, 0);
+                    __builtin_bit_cast(f16x8_t, ahead[t % (kAheadPv + 1)]),
+                    __builtin_bit_cast(f16x8_t, u32x4{aw[pt][0], aw[pt][1], aw[pt][2], aw[pt][3]}),
+                    acc[c], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
         pc = pn;
@@ -830,25 +864,20 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     // no copy may land in LDS after the wave has left
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-    // ---- partials (m back in natural units): rows h (hi) + 2^-12 rows 8 + h (lo'),
-    // lanes l and l ^ 32
+    // ---- partials (m back in natural units): head slot h (hi) + 2^-12 slot 8 + h (lo'),
+    // lanes n and n ^ 8
     const int64_t head0 = (int64_t)qi * qh + (int64_t)g * G;
     if (n < G && rg == 0) {
         part_ml[((head0 + n) * nsplit + split) * 2 + 0] = m_run * 0.6931471805599453f;
         part_ml[((head0 + n) * nsplit + split) * 2 + 1] = l_run;
     }
+    float* pacc = part_acc + ((head0 + (n & 7)) * nsplit + split) * hd;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const float other = __shfl_xor(acc[c][e], 32);
-            if (rg < 2) {
-                const int h = 4 * rg + e;
-                if (h < G) {
-                    const int dim = 16 * c + (n ^ 1);
-                    part_acc[((head0 + h) * nsplit + split) * hd + dim] = acc[c][e] + other * (1.0f / 4096.0f);
-                }
-            }
+            const float v = fmaf(ror8(acc[c][e]), 1.0f / 4096.0f, acc[c][e]);
+            if (n < G) pacc[16 * c + ((4 * rg + e) ^ 1)] = v;
         }
     }
 }
@@ -908,8 +937,10 @@ int launch_attention(const AttnArgs& a, const Pages& pg, hipStream_t s) {
     float* qrot = (float*)a.ws;
     float* ml = (float*)((char*)a.ws + off_ml);
     float* acc = (float*)((char*)a.ws + off_acc);
-    hipLaunchKernelGGL(tq_attn_prerotate_kernel, dim3(a.nq * a.qh), dim3(128), 0, s,
-                       (const uint16_t*)a.q, a.krot, qrot, a.hd);
+    const int nvec = a.nq * a.qh;
+    const unsigned rot_groups = (unsigned)ceil_div(nvec, kRotVecs);
+    hipLaunchKernelGGL(tq_attn_prerotate_kernel, dim3(rot_groups), dim3(256), 0, s,
+                       (const uint16_t*)a.q, a.krot, qrot, a.hd, nvec);
     if (a.kbits == 4 && a.vbits == 4 && a.hd == 128 && a.qh / a.kvh <= 8)
         launch_mfma_split(qrot, a.qs, pg, a.kcent, a.vcent, a.nq, a.qh, a.kvh, nsplit, ml, acc, s);
     else if (a.kbits == 4 && a.vbits == 4)
@@ -918,7 +949,7 @@ int launch_attention(const AttnArgs& a, const Pages& pg, hipStream_t s) {
         launch_split<4, 2>(a, pg, nsplit, ml, acc, s);
     else
         launch_split<0, 0>(a, pg, nsplit, ml, acc, s);
-    hipLaunchKernelGGL(tq_attn_combine_kernel, dim3(a.nq * a.qh), dim3(128), 0, s, a.qs, ml, acc,
+    hipLaunchKernelGGL(tq_attn_combine_kernel, dim3(nvec), dim3(128), 0, s, a.qs, ml, acc,
                        a.vrot, (uint16_t*)a.out, a.qh, a.hd, nsplit);
     return hipGetLastError();
 }
