@@ -47,31 +47,43 @@ __device__ __forceinline__ float ofloat(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
-// Largest float y in [c0, c1) with fabsf(y - c0) <= fabsf(y - c1).
-__device__ inline float exact_threshold(float c0, float c1) {
-    uint32_t lo = okey(c0), hi = okey(c1);
+// Thresholds. t_q is the largest float y in [c_q, c_q+1) with
+// fabsf(y - c_q) <= fabsf(y - c_q+1): the predicate is monotone in y, so order keys (floats
+// mapped to monotone unsigned integers) can be searched.
+// The threshold found by a whole wave (c0, c1 uniform; every lane returns it): each
+// round tests 64 evenly spaced order keys between a key where the predicate holds (lo) and
+// one where it fails (hi) and keeps the crossing, so about 6 rounds replace the 32 serial
+// steps of the bisection. Used for the pairs the short walk cannot settle, e.g. c0 = -c1,
+// whose fp32 midpoint 0 lies ~2^30 keys below the threshold.
+__device__ inline float exact_threshold_wave(float c0, float c1) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t lo = okey(c0), hi = okey(c1);  // P(lo) holds, P(hi) fails
     while (hi - lo > 1u) {
-        const uint32_t mid = lo + (hi - lo) / 2u;
-        const float y = ofloat(mid);
-        if (fabsf(y - c0) > fabsf(y - c1))
-            hi = mid;
-        else
-            lo = mid;
+        const uint32_t span = hi - lo;
+        // lane l tests lo + ceil(span (l + 1) / 64): increasing in l, lane 63 tests hi
+        const uint32_t k = lo + (uint32_t)(((uint64_t)span * (lane + 1u) + 63u) >> 6);
+        const float y = ofloat(k);
+        const bool p = k < hi && fabsf(y - c0) <= fabsf(y - c1);
+        const uint64_t m = __ballot(p);
+        // P is monotone in the key: lanes [0, n) hold, lanes [n, 64) fail
+        const int n = m == 0 ? 0 : 64 - __builtin_clzll(m);
+        const uint32_t nlo = n == 0 ? lo : __builtin_amdgcn_readlane(k, n - 1);
+        const uint32_t nhi = n == 64 ? hi : __builtin_amdgcn_readlane(k, n);
+        lo = nlo;
+        hi = nhi;
     }
     return ofloat(lo);
 }
 
-// Monotone bucket map, clamped to [0, J-1]; NaN maps to bucket 0 (med3 of NaN, 0, jmax
-// returns 0 on gfx9, like fminf(fmaxf(NaN, 0), jmax)).
-// The same threshold, found by walking from the fp32 midpoint (the boundary is within a few
-// ulps of it); falls back to the bisection when the walk does not end within 16 steps.
-__device__ inline float exact_threshold_walk(float c0, float c1) {
+// Short walk from the fp32 midpoint (the threshold is within a step of it except for
+// pairs like c0 = -c1); NaN when it does not settle within 4 steps.
+__device__ inline float threshold_walk4(float c0, float c1) {
     const float m = c0 + 0.5f * (c1 - c0);
-    if (!(m > c0 && m < c1)) return exact_threshold(c0, c1);
+    if (!(m > c0 && m < c1)) return __builtin_nanf("");
     uint32_t k = okey(m);
     const bool up = fabsf(m - c0) <= fabsf(m - c1);
 #pragma unroll 1
-    for (int it = 0; it < 16; ++it) {
+    for (int it = 0; it < 4; ++it) {
         if (up) {  // P(k) holds: advance while P(k + 1) holds
             const float n = ofloat(k + 1u);
             if (!(n < c1) || fabsf(n - c0) > fabsf(n - c1)) return ofloat(k);
@@ -82,7 +94,7 @@ __device__ inline float exact_threshold_walk(float c0, float c1) {
             if (!(n > c0) || fabsf(n - c0) <= fabsf(n - c1)) return n > c0 ? n : c0;
         }
     }
-    return exact_threshold(c0, c1);
+    return __builtin_nanf("");
 }
 
 __device__ __forceinline__ int bucket_of(const Quantizer& q, float y) {
@@ -124,13 +136,11 @@ __device__ __forceinline__ int quantize(const Quantizer& q, float y) {
     return code;
 }
 
-// Build the quantizer for L centroids (device memory) in LDS. Every thread of the block
-// must call it; it contains barriers. blockDim.x must be a multiple of 64.
-__device__ inline void quantizer_build(Quantizer& q, const float* __restrict__ cent, int L) {
+// Build the quantizer for L centroids in LDS once q.c[0, L) holds them. Every thread of the
+// block must call it; it contains barriers. blockDim.x must be a multiple of 64.
+__device__ inline void quantizer_finish(Quantizer& q, int L) {
     const int tid = threadIdx.x, bs = blockDim.x;
     const int lane = tid & 63, wave = tid >> 6, nw = bs >> 6;
-    for (int i = tid; i < L; i += bs) q.c[i] = cent[i];
-    __syncthreads();
     bool ok = true;
     float gmin = __builtin_inff(), cmax = 0.0f;
     for (int i = tid; i < L; i += bs) {
@@ -175,8 +185,16 @@ __device__ inline void quantizer_build(Quantizer& q, const float* __restrict__ c
     }
     __syncthreads();
     const bool fast = q.ybound > 0.0f;
-    if (fast)
-        for (int i = tid; i < L - 1; i += bs) q.t[i] = exact_threshold_walk(q.c[i], q.c[i + 1]);
+    if (fast) {
+        for (int i = tid; i < L - 1; i += bs) q.t[i] = threshold_walk4(q.c[i], q.c[i + 1]);
+        __syncthreads();
+        // the pairs the walk left open, one wave each
+        for (int i = wave; i < L - 1; i += nw)
+            if (q.t[i] != q.t[i]) {
+                const float t = exact_threshold_wave(q.c[i], q.c[i + 1]);
+                if (lane == 0) q.t[i] = t;
+            }
+    }
     __syncthreads();
     if (tid == 0 && fast) {
         const int J = q.J;
@@ -233,6 +251,13 @@ __device__ inline void quantizer_build(Quantizer& q, const float* __restrict__ c
     crowded = __syncthreads_or(crowded);
     if (tid == 0) q.unit_fast = (q.ybound >= 4.0f && !crowded) ? 1 : 0;
     __syncthreads();
+}
+
+// Build the quantizer for L centroids (device memory) in LDS (same contract).
+__device__ inline void quantizer_build(Quantizer& q, const float* __restrict__ cent, int L) {
+    for (int i = threadIdx.x; i < L; i += blockDim.x) q.c[i] = cent[i];
+    __syncthreads();
+    quantizer_finish(q, L);
 }
 
 // MSB-first bitstream: the 8 codes of group g occupy stream bits [8*b*g, 8*b*(g+1)), code i

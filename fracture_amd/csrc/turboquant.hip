@@ -92,32 +92,60 @@ struct RotLds {
     u32x4 frag[4][8][2][64];  // 64 KB
 };
 
-template <bool kTranspose>
-__device__ __forceinline__ void stage_rotation(const float* __restrict__ rot, RotLds& L) {
-    for (int idx = threadIdx.x; idx < 4 * 8 * 64; idx += blockDim.x) {
-        const int lane = idx & 63, s = (idx >> 6) & 7, c = idx >> 9;
-        const int i = lane & 31, h = lane >> 5;
-        const int row = 32 * c + i;
-        const int k0 = 64 * h + 8 * s;
-        uint32_t hw[4], lw[4];
+// Staging in two steps so the rotation's loads overlap the rest of a workgroup's set-up:
+// load() issues this thread's reads of Pi into registers, store() converts them to the hi / lo'
+// fragments and writes LDS. kThreads is the block size.
+template <bool kTranspose, int kThreads>
+struct RotStage {
+    static constexpr int kFrags = 4 * 8 * 64;
+    static constexpr int kN = (kFrags + kThreads - 1) / kThreads;
+    float v[kN][8];
+    __device__ __forceinline__ void load(const float* __restrict__ rot) {
 #pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2) {
-            uint32_t hb[2], lb[2];
+        for (int n = 0; n < kN; ++n) {
+            const int idx = (int)threadIdx.x + n * kThreads;
+            if (kFrags % kThreads != 0 && idx >= kFrags) break;
+            const int lane = idx & 63, s = (idx >> 6) & 7, c = idx >> 9;
+            const int row = 32 * c + (lane & 31), k0 = 64 * (lane >> 5) + 8 * s;
+            if constexpr (kTranspose) {
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const int k = k0 + 2 * e2 + t;
-                const float v = kTranspose ? rot[k * kHd + row] : rot[row * kHd + k];
-                const _Float16 hi = (_Float16)v;
-                hb[t] = __builtin_bit_cast(uint16_t, hi);
-                lb[t] = __builtin_bit_cast(uint16_t, (_Float16)((v - (float)hi) * kLoScale));
+                for (int e = 0; e < 8; ++e) v[n][e] = rot[(k0 + e) * kHd + row];
+            } else {
+                const f32x4 a = *(const f32x4*)&rot[row * kHd + k0];
+                const f32x4 b = *(const f32x4*)&rot[row * kHd + k0 + 4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[n][e] = a[e];
+                    v[n][4 + e] = b[e];
+                }
             }
-            hw[e2] = hb[0] | (hb[1] << 16);
-            lw[e2] = lb[0] | (lb[1] << 16);
         }
-        L.frag[c][s][0][lane] = u32x4{hw[0], hw[1], hw[2], hw[3]};
-        L.frag[c][s][1][lane] = u32x4{lw[0], lw[1], lw[2], lw[3]};
     }
-}
+    __device__ __forceinline__ void store(RotLds& L) const {
+#pragma unroll
+        for (int n = 0; n < kN; ++n) {
+            const int idx = (int)threadIdx.x + n * kThreads;
+            if (kFrags % kThreads != 0 && idx >= kFrags) break;
+            const int lane = idx & 63, s = (idx >> 6) & 7, c = idx >> 9;
+            uint32_t hw[4], lw[4];
+#pragma unroll
+            for (int e2 = 0; e2 < 4; ++e2) {
+                uint32_t hb[2], lb[2];
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const float x = v[n][2 * e2 + t];
+                    const _Float16 hi = (_Float16)x;
+                    hb[t] = __builtin_bit_cast(uint16_t, hi);
+                    lb[t] = __builtin_bit_cast(uint16_t, (_Float16)((x - (float)hi) * kLoScale));
+                }
+                hw[e2] = hb[0] | (hb[1] << 16);
+                lw[e2] = lb[0] | (lb[1] << 16);
+            }
+            L.frag[c][s][0][lane] = u32x4{hw[0], hw[1], hw[2], hw[3]};
+            L.frag[c][s][1][lane] = u32x4{lw[0], lw[1], lw[2], lw[3]};
+        }
+    }
+};
 
 __device__ __forceinline__ f16x8 frag(const RotLds& L, int c, int s, int hl, int lane) {
     return __builtin_bit_cast(f16x8, L.frag[c][s][hl][lane]);
@@ -214,23 +242,29 @@ __device__ __forceinline__ void compress_tile(const Quantizer& qz, const RotLds&
         if (np) *np = (uint16_t)f2h(nrm);
     }
     uint32_t half[16];  // kMode 0: half-group of group 4c + g held by this lane
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        __builtin_amdgcn_sched_barrier(0);  // keep each block's fragment loads within it
-        f32x16 acc_hi = {}, acc_lo = {};
+    // Block c's MFMAs accumulate into set c % 2 while block c - 1 is quantized from the other
+    // set, so the quantizer's VALU work overlaps the matrix core's.
+    f32x16 acc_hi[2], acc_lo[2];
+    auto mfma_block = [&](int c) {
+        const int b = c & 1;
+        acc_hi[b] = f32x16{};
+        acc_lo[b] = f32x16{};
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-            acc_hi = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag(L, c, s, 0, lane), x[s], acc_hi,
-                                                            0, 0, 0);
-            acc_lo = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag(L, c, s, 1, lane), x[s], acc_lo,
-                                                            0, 0, 0);
+            acc_hi[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag(L, c, s, 0, lane), x[s],
+                                                               acc_hi[b], 0, 0, 0);
+            acc_lo[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag(L, c, s, 1, lane), x[s],
+                                                               acc_lo[b], 0, 0, 0);
         }
+    };
+    auto quant_block = [&](int c) {
+        const int b = c & 1;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             float y[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                y[e] = fmaf(acc_lo[4 * g + e], kLoInv, acc_hi[4 * g + e]) * inv;
+                y[e] = fmaf(acc_lo[b][4 * g + e], kLoInv, acc_hi[b][4 * g + e]) * inv;
             if constexpr (kMode == 1) {
                 if (row_ok)
                     *(f32x4*)&y_out[(m0 + r) * kHd + 32 * c + 8 * g + 4 * h] =
@@ -244,7 +278,19 @@ __device__ __forceinline__ void compress_tile(const Quantizer& qz, const RotLds&
                 half[4 * c + g] = hw;
             }
         }
+    };
+    // one scheduling region per (MFMA block c, quantize block c - 1) pair: the two interleave
+    // within it, and fragment reads cannot be hoisted across regions
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_block(0);
+#pragma unroll
+    for (int c = 1; c < 4; ++c) {
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_block(c);
+        quant_block(c - 1);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    quant_block(3);
     if constexpr (kMode == 0) {
         // Group j (< 8) and group j + 8: lane h = 0 gets both halves of group j, lane h = 1
         // both halves of group j + 8, as (first half, second half) in (half[j], half[j+8]).
@@ -292,6 +338,20 @@ __device__ __forceinline__ void compress_waves(const Quantizer& qz, const RotLds
     }
 }
 
+// The general-quantizer tile loop (codebooks the fast bucket map cannot serve exactly), kept
+// out of line so that its register needs do not constrain the fast path's allocation.
+// It reloads the wave's first tile, and takes the destination by value: a reference would
+// move the kernel argument into private memory for the fast path too.
+template <int kMode, int kBits, class Dst>
+__device__ __noinline__ void compress_waves_general(const Quantizer& qz, const RotLds& L,
+                                                    const uint16_t* __restrict__ in, Dst dst,
+                                                    float* __restrict__ y_out, int64_t rows) {
+    f16x8 xa[8];
+    load_x_half(in, (int64_t)blockIdx.x * kWavesC + (threadIdx.x >> 6), ceil_div(rows, kTile),
+                rows, xa);
+    compress_waves<kMode, kBits, false>(qz, L, in, dst, y_out, rows, xa);
+}
+
 template <int kMode, int kBits, class Dst>
 __global__ __launch_bounds__(64 * kWavesC) __attribute__((amdgpu_waves_per_eu(2))) void
 tq_compress_mfma_kernel(const uint16_t* __restrict__ in, const float* __restrict__ rot,
@@ -299,17 +359,26 @@ tq_compress_mfma_kernel(const uint16_t* __restrict__ in, const float* __restrict
                         float* __restrict__ y_out, int64_t rows) {
     __shared__ Quantizer qz;
     __shared__ RotLds rl;
-    if constexpr (kMode == 0) quantizer_build(qz, cent, L);  // has barriers
-    // The first tile's loads go out before the rotation is staged, which overlaps them.
+    // The centroids' loads go out first, then the first tile's and the rotation's; the
+    // quantizer build overlaps the latter. L <= kMaxLevels <= the block size.
+    static_assert(kMaxLevels <= 64 * kWavesC, "one centroid per thread");
+    const float c_own = kMode == 0 && (int)threadIdx.x < L ? cent[threadIdx.x] : 0.0f;
     f16x8 xa[8];
     load_x_half(in, (int64_t)blockIdx.x * kWavesC + (threadIdx.x >> 6), ceil_div(rows, kTile),
                 rows, xa);
-    stage_rotation<false>(rot, rl);
+    RotStage<false, 64 * kWavesC> rs;
+    rs.load(rot);
+    if constexpr (kMode == 0) {
+        if ((int)threadIdx.x < L) qz.c[threadIdx.x] = c_own;
+        __syncthreads();
+        quantizer_finish(qz, L);  // has barriers
+    }
+    rs.store(rl);
     __syncthreads();
-    if (kMode == 0 && qz.unit_fast)
+    if (kMode == 1 || qz.unit_fast)
         compress_waves<kMode, kBits, true>(qz, rl, in, dst, y_out, rows, xa);
     else
-        compress_waves<kMode, kBits, false>(qz, rl, in, dst, y_out, rows, xa);
+        compress_waves_general<kMode, kBits>(qz, rl, in, dst, y_out, rows);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -558,6 +627,8 @@ tq_dequant_mfma_kernel(const uint8_t* __restrict__ packed, const uint16_t* __res
     // The first tile's loads go out before the set-up, which then overlaps their latency.
     CodeHalf<kBits> ca, cb;
     load_code_half<kBits>(packed, norms, tile, ntiles, rows, ca);
+    RotStage<true, 64 * kWavesD> rs;
+    rs.load(rot);
     for (int i = threadIdx.x; i < kMaxLevels; i += blockDim.x) {
         const float c = i < L ? cent[i] : 0.0f;
         const _Float16 hi = (_Float16)c;
@@ -565,7 +636,7 @@ tq_dequant_mfma_kernel(const uint8_t* __restrict__ packed, const uint16_t* __res
         const uint32_t lb = __builtin_bit_cast(uint16_t, (_Float16)((c - (float)hi) * kLoScale));
         t.tab[i] = hb | (lb << 16);
     }
-    stage_rotation<true>(rot, rl);
+    rs.store(rl);
     __syncthreads();
     if constexpr (kBits == 4) {
         for (int b = threadIdx.x; b < 256; b += blockDim.x) {
