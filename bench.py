@@ -14,6 +14,14 @@ Other workloads (parity-tested configurations, printed as their own JSON lines):
   --workload prefill      add+RMSNorm [8192,4096], SwiGLU [8192,14336], softmax/argmax [64,128256]
   --workload tq           TurboQuant compress + dequantize of K and V [32768, 8, 128], 4 and 3 bit
   --workload attention    decode attention over a K4/V4 page pool, B=64, 32/8 heads, ctx U[1024,32768]
+
+HBM traffic (the roofline's "traffic" field, from profiles/traffic.json):
+  rocprofv3 --pmc FETCH_SIZE -d <F> -o pmc -- python3 bench.py --workload pmc
+  rocprofv3 --pmc WRITE_SIZE -d <W> -o pmc -- python3 bench.py --workload pmc
+  python3 bench.py --traffic-from <F> <W>      (writes profiles/traffic.json, prints a table)
+The pmc workload runs a 1 GiB device copy (calibration: the counters' reading for a known
+number of bytes) and then every operation below once, each after a 4 KiB copy that marks
+where its dispatches start.
 """
 from __future__ import annotations
 
@@ -37,7 +45,10 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "prefill", "tq", "attention", "all"])
+                    choices=["decode", "prefill", "tq", "attention", "all", "pmc"])
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="turn two rocprofv3 --pmc runs of --workload pmc into "
+                         "profiles/traffic.json")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true", help="time the chain without a HIP graph")
@@ -251,7 +262,10 @@ def run_decode(args, torch, K, dev):
         us = timer.graph_time_us(ops[name])
         per[name] = {"us": round(us, 3), "GB/s": round(gbs(nbytes[name], us), 1),
                      "frac_of_peak": round(gbs(nbytes[name], us) / PEAK_HBM_GBS, 4),
-                     "bytes": nbytes[name]}
+                     "bytes": nbytes[name],
+                     "traffic": traffic_of({"embedding": "decode_embedding", "rope": "decode_rope",
+                                            "silu_mul": "silu_mul_64x14336",
+                                            "add_rmsnorm": "decode_add_rmsnorm"}[name])}
     dom = "silu_mul"
     traffic = traffic_of("silu_mul_64x14336")
     roof = {"kernel": "silu_mul_vec_kernel<fp16> [64,14336]", "bound": "hbm",
@@ -376,13 +390,33 @@ def run_tq(args, torch, K, dev):
 
 
 def run_attention(args, torch, K, dev):
+    fn, nb, tok, mean = attention_inputs(torch, K, dev)
+    us = Timer(torch).time_us(fn, 10, warmup=2)
+    return {"workload": "TurboQuant K4/V4 paged decode attention, B=64, 32/8 heads, hd 128",
+            "kernels": {"attention_tq_decode": {
+                "us": round(us, 1), "GB/s": round(gbs(nb, us), 1),
+                "frac_of_peak": round(gbs(nb, us) / PEAK_HBM_GBS, 4), "bytes": nb,
+                "context_tokens": tok, "mean_ctx": mean,
+                "traffic": traffic_of("attention_tq_decode")}}}
+
+
+# ---------------------------------------------------------------------------------------
+# HBM traffic from rocprofv3 PMC counters
+# ---------------------------------------------------------------------------------------
+CAL_BYTES = 1 << 30
+ATT_SHAPE = dict(B=64, QH=32, KVH=8, HD=128, kb=4, vb=4)
+
+
+def attention_inputs(torch, K, dev):
+    """The decode-attention workload: returns (fn, algorithmic bytes, context tokens, mean)."""
     import numpy as np
 
     from fracture_amd import turboquant as tq
 
+    B, QH, KVH, HD, kb, vb = (ATT_SHAPE[k] for k in ("B", "QH", "KVH", "HD", "kb", "vb"))
+    lens = attention_lens()
     rng = np.random.default_rng(5)
-    B, QH, KVH, HD, kb, vb = 64, 32, 8, 128, 4, 4
-    lens = rng.integers(1024, 32769, B).astype(np.int32)
+    rng.integers(1024, 32769, B)  # the lengths' draw: the page permutation comes next
     nbs = (lens + 15) // 16
     P = int(nbs.sum())
     maxb = int(nbs.max())
@@ -410,19 +444,172 @@ def run_attention(args, torch, K, dev):
     ws = K.attention_workspace(B, QH, HD, maxb, dev)
     fn = lambda: K.attention_tq_decode(out, q, tb, sl, kp, kn, vp, vn, krot, vrot, kc, vc, kb, vb,
                                        KVH, ws)
-    us = Timer(torch).time_us(fn, 10, warmup=2)
     tok = int(lens.sum())
     nb = tok * KVH * (pdk + pdv + 4) + B * QH * HD * 4 + B * maxb * 4
-    return {"workload": "TurboQuant K4/V4 paged decode attention, B=64, 32/8 heads, hd 128",
-            "kernels": {"attention_tq_decode": {
-                "us": round(us, 1), "GB/s": round(gbs(nb, us), 1),
-                "frac_of_peak": round(gbs(nb, us) / PEAK_HBM_GBS, 4), "bytes": nb,
-                "context_tokens": tok, "mean_ctx": float(lens.mean()),
-                "traffic": traffic_of("attention_tq_decode")}}}
+    return fn, nb, tok, float(lens.mean())
+
+
+def pmc_sequence(torch, K, dev):
+    """[(key, fn, algorithmic bytes)] of every measured operation, inputs already resident."""
+    from fracture_amd import turboquant as tq
+
+    seq = []
+    x = decode_inputs(torch, dev)
+    ops = decode_ops(K, x)
+    nb = decode_bytes()
+    seq += [("decode_embedding", ops["embedding"], nb["embedding"]),
+            ("decode_rope", ops["rope"], nb["rope"]),
+            ("silu_mul_64x14336", ops["silu_mul"], nb["silu_mul"]),
+            ("decode_add_rmsnorm", ops["add_rmsnorm"], nb["add_rmsnorm"])]
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    f16 = torch.float16
+    h = torch.randn((8192, 4096), generator=g, device=dev).to(f16)
+    d = torch.randn((8192, 4096), generator=g, device=dev).to(f16)
+    w = (torch.rand((4096,), generator=g, device=dev) + 0.5).to(f16)
+    n = torch.empty_like(h)
+    gate = torch.randn((8192, 14336), generator=g, device=dev).to(f16)
+    up = torch.randn((8192, 14336), generator=g, device=dev).to(f16)
+    act = torch.empty_like(gate)
+    lg = torch.randn((64, 128256), generator=g, device=dev) * 3
+    probs = torch.empty_like(lg)
+    idx = torch.empty(64, dtype=torch.int32, device=dev)
+    fl = torch.empty(64, dtype=torch.int32, device=dev)
+    ws = K.rows_workspace(64, 128256, dev)
+    seq += [("add_rmsnorm_8192x4096", lambda: K.add_rmsnorm(h, d, w, 1e-5, n), 4 * 8192 * 4096 * 2),
+            ("silu_mul_8192x14336", lambda: K.silu_mul(act, gate, up), 3 * 8192 * 14336 * 2),
+            ("softmax_64x128256", lambda: K.softmax_rows(lg, probs, 1.0, ws), 2 * 64 * 128256 * 4),
+            ("argmax_64x128256", lambda: K.argmax_rows(lg, idx, fl, ws), 64 * 128256 * 4),
+            ("softmax_argmax_64x128256",
+             lambda: K.softmax_argmax_rows(lg, probs, idx, fl, 1.0, ws), 2 * 64 * 128256 * 4)]
+    N, H, hd = 32768, 8, 128
+    kv = [(torch.randn((N, H, hd), generator=g, device=dev)).to(f16) for _ in range(2)]
+    rots = [torch.from_numpy(tq.rotation_matrix(hd, s)).to(dev) for s in (42, 542)]
+    for bits in (4, 3):
+        cent = torch.from_numpy(tq.codebook(hd, bits)[0]).to(dev)
+        pd = K.packed_dim(hd, bits)
+        pk = [torch.empty((N, H * pd), dtype=torch.uint8, device=dev) for _ in range(2)]
+        nm = [torch.empty((N, H), dtype=f16, device=dev) for _ in range(2)]
+        dq = [torch.empty_like(kv[0]) for _ in range(2)]
+        nbytes = 2 * (N * H * hd * 2 + N * H * pd + N * H * 2)
+
+        def comp(cent=cent, bits=bits, pk=pk, nm=nm):
+            for i in range(2):
+                K.tq_compress(kv[i], rots[i], cent, bits, pk[i], nm[i])
+
+        def deq(cent=cent, bits=bits, pk=pk, nm=nm, dq=dq):
+            for i in range(2):
+                K.tq_dequant(pk[i], nm[i], rots[i], cent, bits, dq[i])
+
+        seq += [(f"tq_compress_{bits}bit", comp, nbytes), (f"tq_dequant_{bits}bit", deq, nbytes)]
+    fn, nb_att, _, _ = attention_inputs(torch, K, dev)
+    seq.append(("attention_tq_decode", fn, nb_att))
+    return seq
+
+
+def attention_lens():
+    import numpy as np
+
+    rng = np.random.default_rng(5)
+    return rng.integers(1024, 32769, ATT_SHAPE["B"]).astype(np.int32)
+
+
+def pmc_keys():
+    """[(key, algorithmic bytes)] of pmc_sequence(), computed without a GPU."""
+    nb = decode_bytes()
+    keys = [("decode_embedding", nb["embedding"]), ("decode_rope", nb["rope"]),
+            ("silu_mul_64x14336", nb["silu_mul"]), ("decode_add_rmsnorm", nb["add_rmsnorm"]),
+            ("add_rmsnorm_8192x4096", 4 * 8192 * 4096 * 2),
+            ("silu_mul_8192x14336", 3 * 8192 * 14336 * 2),
+            ("softmax_64x128256", 2 * 64 * 128256 * 4), ("argmax_64x128256", 64 * 128256 * 4),
+            ("softmax_argmax_64x128256", 2 * 64 * 128256 * 4)]
+    N, H, hd = 32768, 8, 128
+    for bits in (4, 3):
+        pd = (hd * bits + 7) // 8
+        nbytes = 2 * (N * H * hd * 2 + N * H * pd + N * H * 2)
+        keys += [(f"tq_compress_{bits}bit", nbytes), (f"tq_dequant_{bits}bit", nbytes)]
+    lens = attention_lens()
+    a = ATT_SHAPE
+    maxb = int(((lens + 15) // 16).max())
+    pdk, pdv = a["HD"] * a["kb"] // 8, a["HD"] * a["vb"] // 8
+    keys.append(("attention_tq_decode", int(lens.sum()) * a["KVH"] * (pdk + pdv + 4) +
+                 a["B"] * a["QH"] * a["HD"] * 4 + a["B"] * maxb * 4))
+    return keys
+
+
+def run_pmc(torch, K, dev):
+    seq = pmc_sequence(torch, K, dev)
+    assert [(k, nb) for k, _, nb in seq] == pmc_keys(), "pmc_keys() out of step"
+    for _, fn, _ in seq:  # first calls (lazy set-up) outside the counted sequence
+        fn()
+    big_a = torch.ones(CAL_BYTES, dtype=torch.uint8, device=dev)
+    big_b = torch.empty_like(big_a)
+    mark_a = torch.ones(4096, dtype=torch.uint8, device=dev)
+    mark_b = torch.empty_like(mark_a)
+    torch.cuda.synchronize()
+    big_b.copy_(big_a)
+    for _, fn, _ in seq:
+        mark_b.copy_(mark_a)
+        fn()
+    mark_b.copy_(mark_a)
+    torch.cuda.synchronize()
+    return {"pmc_sequence": [(k, nb) for k, _, nb in seq], "calibration_bytes": CAL_BYTES}
+
+
+def _pmc_rows(directory: str, counter: str):
+    """(dispatch id, kernel name, value) of one counter, in dispatch order."""
+    import glob
+    import sqlite3
+
+    dbs = sorted(glob.glob(os.path.join(directory, "**", "*_results.db"), recursive=True))
+    if not dbs:
+        raise SystemExit(f"no rocpd database under {directory}")
+    rows = []
+    for db in dbs:
+        c = sqlite3.connect(db)
+        rows += c.execute("select dispatch_id, kernel_name, value from counters_collection "
+                          "where counter_name = ?", (counter,)).fetchall()
+    rows.sort()
+    return rows
+
+
+def traffic_from(fetch_dir: str, write_dir: str, keys):
+    """Per-operation HBM bytes: counter readings between marker copies, scaled by the
+    counters' reading for the 1 GiB calibration copy."""
+    out = {}
+    for counter, directory in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        rows = _pmc_rows(directory, counter)
+        copies = [i for i, r in enumerate(rows) if "copyBuffer" in r[1]]
+        if len(copies) < len(keys) + 2:
+            raise SystemExit(f"{counter}: expected {len(keys) + 2} marker copies, "
+                             f"found {len(copies)}")
+        cal, marks = copies[-(len(keys) + 2)], copies[-(len(keys) + 1):]
+        factor = rows[cal][2] * 1024.0 / CAL_BYTES  # counter KiB per true KiB
+        for j, (key, nb) in enumerate(keys):
+            seg = rows[marks[j] + 1:marks[j + 1]]
+            e = out.setdefault(key, {"algorithmic_bytes": nb})
+            e[counter.lower() + "_bytes"] = round(sum(r[2] for r in seg) * 1024.0 / factor)
+            e[counter.lower() + "_counter_per_byte"] = round(factor, 4)
+            e["dispatches"] = len(seg)
+    for e in out.values():
+        e["bytes_per_dispatch"] = e["fetch_size_bytes"] + e["write_size_bytes"]
+        e["traffic_over_algorithmic"] = round(e["bytes_per_dispatch"] / e["algorithmic_bytes"], 3)
+    return out
 
 
 def main():
     args = parse()
+    if args.traffic_from:
+        keys = pmc_keys()
+        t = traffic_from(args.traffic_from[0], args.traffic_from[1], keys)
+        (ROOT / "profiles" / "traffic.json").write_text(json.dumps(t, indent=1) + "\n")
+        print("| operation | dispatches | fetch MB | write MB | HBM MB | algorithmic MB | ratio |")
+        print("|---|---|---|---|---|---|---|")
+        for k, e in t.items():
+            print(f"| `{k}` | {e['dispatches']} | {e['fetch_size_bytes'] / 1e6:.2f} | "
+                  f"{e['write_size_bytes'] / 1e6:.2f} | {e['bytes_per_dispatch'] / 1e6:.2f} | "
+                  f"{e['algorithmic_bytes'] / 1e6:.2f} | {e['traffic_over_algorithmic']} |")
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "fracture_amd benchmarks one GPU: this build has no "
                                    "multi-GPU path; run with --gpus 1"}))
@@ -442,6 +629,8 @@ def main():
         print(json.dumps(run_tq(args, torch, K, dev)), flush=True)
     if wl in ("attention", "all"):
         print(json.dumps(run_attention(args, torch, K, dev)), flush=True)
+    if wl == "pmc":
+        print(json.dumps(run_pmc(torch, K, dev)), flush=True)
 
 
 if __name__ == "__main__":
