@@ -146,6 +146,16 @@ __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, __builtin_amdgcn_update_dpp(ninf, v, 0x143, 0xC, 0xF, false));
     return lane63(v);
 }
+__device__ __forceinline__ int wave_max_int(int v) {
+    const int lo = INT32_MIN;
+    v = max(v, __builtin_amdgcn_update_dpp(lo, v, 0xB1, 0xF, 0xF, true));
+    v = max(v, __builtin_amdgcn_update_dpp(lo, v, 0x4E, 0xF, 0xF, true));
+    v = max(v, __builtin_amdgcn_update_dpp(lo, v, 0x141, 0xF, 0xF, true));
+    v = max(v, __builtin_amdgcn_update_dpp(lo, v, 0x140, 0xF, 0xF, true));
+    v = max(v, __builtin_amdgcn_update_dpp(lo, v, 0x142, 0xA, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(lo, v, 0x143, 0xC, 0xF, false));
+    return __builtin_amdgcn_readlane(v, 63);
+}
 __device__ __forceinline__ float wave_min(float v) {
     const float pinf = __builtin_inff();
     v = fminf(v, __builtin_amdgcn_update_dpp(pinf, v, 0xB1, 0xF, 0xF, true));

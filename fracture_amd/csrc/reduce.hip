@@ -46,16 +46,12 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
     return v > bv || (v == bv && i > bi);
 }
 
+// Wave argmax of per-lane (value, index) pairs under better(): the largest value, then the
+// largest index among the lanes that hold it. Lanes without a candidate hold (-inf, -1).
 __device__ __forceinline__ void wave_argmax(float& bv, int& bi) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(bv, off);
-        const int oi = __shfl_xor(bi, off);
-        if (better(ov, oi, bv, bi)) {
-            bv = ov;
-            bi = oi;
-        }
-    }
+    const float wm = wave_max(bv);
+    bi = wave_max_int(bv == wm ? bi : -1);
+    bv = wm;
 }
 
 // exp(s - m) for the softmax; s == m gives exactly 1.
@@ -71,6 +67,10 @@ __device__ __forceinline__ void wave_softmax_pair(float& m, float& s) {
     m = mw;
 }
 
+// This lane's kPerLane elements of the chunk at base (element j at elem_index(base, j)).
+// Positions past the row's end read the row's last element or vector instead (every caller
+// ignores them), so the loads carry no branches and are all in flight at once: a guarded
+// load makes the compiler wait for the previous one before it. kVec: cols % 4 == 0.
 template <bool kVec>
 __device__ __forceinline__ void load_chunk(const float* row, int cols, int base,
                                            float (&v)[kPerLane]) {
@@ -78,23 +78,40 @@ __device__ __forceinline__ void load_chunk(const float* row, int cols, int base,
     for (int u = 0; u < kPerLane / 4; ++u) {
         const int e0 = base + u * (kBlock * 4) + threadIdx.x * 4;
         if constexpr (kVec) {
-            if (e0 + 3 < cols) {
-                const u32x4 w = ld16(row + e0);
+            const u32x4 w = ld16(row + min(e0, cols - 4));
 #pragma unroll
-                for (int i = 0; i < 4; ++i) v[4 * u + i] = __uint_as_float(w[i]);
-                continue;
-            }
-        }
+            for (int i = 0; i < 4; ++i) v[4 * u + i] = __uint_as_float(w[i]);
+        } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int e = e0 + i;
-            v[4 * u + i] = e < cols ? row[e] : 0.0f;
+            for (int i = 0; i < 4; ++i) v[4 * u + i] = row[min(e0 + i, cols - 1)];
         }
     }
 }
 
 __device__ __forceinline__ int elem_index(int base, int j) {
     return base + (j / 4) * (kBlock * 4) + threadIdx.x * 4 + (j & 3);
+}
+
+// One lane's pass over its chunk elements: non-finite screen (nf), running max of x * inv_t
+// (m), and the argmax (bv, bi). The lane visits its indices in increasing order, so `>=`
+// keeps the last maximum. kFull: the whole chunk lies inside the row. Selects rather than
+// branches keep this straight-line code.
+template <int kMode, bool kFull>
+__device__ __forceinline__ void scan_lane(const float (&v)[kPerLane], int base, int nvalid,
+                                          float inv_t, float& nf, float& m, float& bv, int& bi) {
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+        const int idx = elem_index(base, j);
+        const bool ok = kFull || idx - base < nvalid;
+        const float x = v[j];
+        nf = ok ? fmaf(x, 0.0f, nf) : nf;
+        if constexpr (kMode & kStatsArgmax) {
+            const bool t = ok && x >= bv;
+            bv = t ? x : bv;
+            bi = t ? idx : bi;
+        }
+        if constexpr (kMode & kStatsSoftmax) m = ok ? fmaxf(m, x * inv_t) : m;
+    }
 }
 
 // Pass 1. kMode: kStatsSoftmax and/or kStatsArgmax.
@@ -117,25 +134,18 @@ __global__ __launch_bounds__(kBlock) void row_stats_kernel(const float* __restri
     float nf = 0.0f;
     float m = -__builtin_inff(), s = 0.0f, bv = -__builtin_inff();
     int bi = -1;
-#pragma unroll
-    for (int j = 0; j < kPerLane; ++j) {
-        const int idx = elem_index(base, j);
-        if (idx - base >= nvalid) continue;
-        const float x = v[j];
-        nf = fmaf(x, 0.0f, nf);
-        if constexpr (kMode & kStatsArgmax) {
-            if (x >= bv) {  // lane visits its indices in increasing order: last max wins
-                bv = x;
-                bi = idx;
-            }
-        }
-        if constexpr (kMode & kStatsSoftmax) m = fmaxf(m, x * inv_t);
-    }
+    const bool full = nvalid >= kChunk;  // uniform: only a row's last chunk can be partial
+    if (full)
+        scan_lane<kMode, true>(v, base, nvalid, inv_t, nf, m, bv, bi);
+    else
+        scan_lane<kMode, false>(v, base, nvalid, inv_t, nf, m, bv, bi);
     if constexpr (kMode & kStatsSoftmax) {
         if (m != -__builtin_inff()) {
 #pragma unroll
-            for (int j = 0; j < kPerLane; ++j)
-                if (elem_index(base, j) - base < nvalid) s += exp_diff(v[j] * inv_t, m);
+            for (int j = 0; j < kPerLane; ++j) {
+                const float e = exp_diff(v[j] * inv_t, m);
+                s += (full || elem_index(base, j) - base < nvalid) ? e : 0.0f;
+            }
         }
     }
     uint32_t fl = 0;
@@ -149,7 +159,7 @@ __global__ __launch_bounds__(kBlock) void row_stats_kernel(const float* __restri
         }
     }
     if constexpr (kMode & kStatsSoftmax) wave_softmax_pair(m, s);
-    if constexpr (kMode & kStatsArgmax) wave_argmax(bv, bi);
+    if constexpr (kMode & kStatsArgmax) wave_argmax(bv, bi);  // NaN never enters bv
     const uint32_t any_nan = __ballot(fl & FHIP_ROW_HAS_NAN) != 0 ? FHIP_ROW_HAS_NAN : 0u;
     const uint32_t any_inf = __ballot(fl & FHIP_ROW_HAS_INF) != 0 ? FHIP_ROW_HAS_INF : 0u;
     if (lane == 0) {

@@ -136,10 +136,30 @@ __device__ __forceinline__ int quantize(const Quantizer& q, float y) {
     return code;
 }
 
-// Build the quantizer for L centroids in LDS once q.c[0, L) holds them. Every thread of the
-// block must call it; it contains barriers. blockDim.x must be a multiple of 64.
+// Ordering point between the phases of the quantizer build: a workgroup barrier (LDS
+// only: outstanding global loads of the caller stay in flight) or, when one wave builds
+// alone, a wavefront fence: a wave's LDS accesses are performed in program order, so the
+// fence only has to stop the compiler from moving them across.
+template <bool kOneWave>
+__device__ __forceinline__ void build_sync() {
+    if constexpr (kOneWave) {
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+    } else {
+        lds_barrier();
+    }
+}
+
+// Build the quantizer for L centroids in LDS once q.c[0, L) holds them.
+//   kOneWave = false: every thread of the block calls it (blockDim.x a multiple of 64);
+//   kOneWave = true:  exactly one whole wave calls it (the rest of the block does other
+//                     set-up work meanwhile), and the caller orders its results for the
+//                     block with a barrier afterwards. No workgroup barrier is then on the
+//                     build's path, which is a chain of short dependent LDS steps.
+template <bool kOneWave = false>
 __device__ inline void quantizer_finish(Quantizer& q, int L) {
-    const int tid = threadIdx.x, bs = blockDim.x;
+    const int tid = kOneWave ? (int)(threadIdx.x & 63) : (int)threadIdx.x;
+    const int bs = kOneWave ? 64 : (int)blockDim.x;
     const int lane = tid & 63, wave = tid >> 6, nw = bs >> 6;
     bool ok = true;
     float gmin = __builtin_inff(), cmax = 0.0f;
@@ -161,7 +181,7 @@ __device__ inline void quantizer_finish(Quantizer& q, int L) {
         q.red_f[1][wave] = cmax;
         q.red_i[wave] = wave_ok ? 1 : 0;
     }
-    __syncthreads();
+    build_sync<kOneWave>();
     if (tid == 0) {
         float g = q.red_f[0][0], m = q.red_f[1][0];
         int k = q.red_i[0];
@@ -183,11 +203,11 @@ __device__ inline void quantizer_finish(Quantizer& q, int L) {
         q.J = J;
         q.jmax = (float)(J - 1);
     }
-    __syncthreads();
+    build_sync<kOneWave>();
     const bool fast = q.ybound > 0.0f;
     if (fast) {
         for (int i = tid; i < L - 1; i += bs) q.t[i] = threshold_walk4(q.c[i], q.c[i + 1]);
-        __syncthreads();
+        build_sync<kOneWave>();
         // the pairs the walk left open, one wave each
         for (int i = wave; i < L - 1; i += nw)
             if (q.t[i] != q.t[i]) {
@@ -195,7 +215,7 @@ __device__ inline void quantizer_finish(Quantizer& q, int L) {
                 if (lane == 0) q.t[i] = t;
             }
     }
-    __syncthreads();
+    build_sync<kOneWave>();
     if (tid == 0 && fast) {
         const int J = q.J;
         const float t0 = q.t[0], t1 = q.t[L - 2];
@@ -215,11 +235,11 @@ __device__ inline void quantizer_finish(Quantizer& q, int L) {
         q.scale = s;
         q.offset = o;
     }
-    __syncthreads();
+    build_sync<kOneWave>();
     int crowded = 0;
     if (q.ybound > 0.0f) {
         for (int i = tid; i < L - 1; i += bs) q.jt[i] = bucket_of(q, q.t[i]);
-        __syncthreads();
+        build_sync<kOneWave>();
         const int n = L - 1;
         for (int j = tid; j < q.J; j += bs) {
             int lo = 0, hi = n;  // first q with jt[q] >= j
@@ -248,9 +268,16 @@ __device__ inline void quantizer_finish(Quantizer& q, int L) {
             q.ent[j] = e;
         }
     }
-    crowded = __syncthreads_or(crowded);
-    if (tid == 0) q.unit_fast = (q.ybound >= 4.0f && !crowded) ? 1 : 0;
-    __syncthreads();
+    // workgroup OR of `crowded` (red_i is free again: its last reader passed two barriers)
+    const bool wave_crowded = __ballot(crowded) != 0;
+    if (lane == 0) q.red_i[wave] = wave_crowded ? 1 : 0;
+    build_sync<kOneWave>();
+    if (tid == 0) {
+        int any = 0;
+        for (int w = 0; w < nw; ++w) any |= q.red_i[w];
+        q.unit_fast = (q.ybound >= 4.0f && !any) ? 1 : 0;
+    }
+    build_sync<kOneWave>();
 }
 
 // Build the quantizer for L centroids (device memory) in LDS (same contract).

@@ -6,9 +6,10 @@
 // of K+V at 32768 tokens x 8 heads, against ~160-170 MB of HBM traffic (~21 us). On the VALU
 // that is >100 us, so the rotation runs on MFMA (v_mfma_f32_32x32x16_f16) with fp32 accuracy
 // recovered by splitting the fp32 operand into fp16 hi + 2^12-scaled fp16 lo parts:
-//   compress:   y_raw = Pi x = Pi_hi x + 2^-12 (Pi_lo' x)       x is the raw fp16 input,
-//               exact as an fp16 operand; the norm is applied after the product by
-//               linearity: y = y_raw / (||x|| + 1e-8).
+//   compress:   y_raw = Pi x = 2^-12 (Pi_hi' x + Pi_lo' x)      Pi_hi' = 2^12 Pi_hi (exact),
+//               both products in one fp32 accumulator; x is the raw fp16 input, exact as
+//               an fp16 operand; the norm is applied after the product by linearity:
+//               y = y_raw / (||x|| + 1e-8).
 //   dequantize: x_hat = Pi^T yhat = Pi_hi^T c_hi + 2^-12 (Pi_lo'^T c_hi + Pi_hi^T c_lo')
 // Each representation error is ~2^-22 relative, the level of the fp32 sums themselves.
 //
@@ -79,6 +80,12 @@ struct PageDst {
     }
 };
 
+// The wave's index in its workgroup, as a wave-uniform (scalar) value: the compiler cannot
+// tell that threadIdx.x >> 6 is uniform, and would turn tile loops into divergent ones.
+__device__ __forceinline__ int wave_id() {
+    return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+}
+
 // ---------------------------------------------------------------------------------------
 // Rotation fragments in LDS. MFMA step s of a 32-coordinate block takes K = 16 coordinates,
 // ordered so that lane half h, element e of step s is coordinate 64h + 8s + e: a lane's B
@@ -95,7 +102,7 @@ struct RotLds {
 // Staging in two steps so the rotation's loads overlap the rest of a workgroup's set-up:
 // load() issues this thread's reads of Pi into registers, store() converts them to the hi / lo'
 // fragments and writes LDS. kThreads is the block size.
-template <bool kTranspose, int kThreads>
+template <bool kTranspose, int kThreads, bool kHiScaled>
 struct RotStage {
     static constexpr int kFrags = 4 * 8 * 64;
     static constexpr int kN = (kFrags + kThreads - 1) / kThreads;
@@ -135,7 +142,9 @@ struct RotStage {
                 for (int t = 0; t < 2; ++t) {
                     const float x = v[n][2 * e2 + t];
                     const _Float16 hi = (_Float16)x;
-                    hb[t] = __builtin_bit_cast(uint16_t, hi);
+                    // x 2^12 is exact for an fp16 value of magnitude <= 1
+                    hb[t] = __builtin_bit_cast(
+                        uint16_t, kHiScaled ? (_Float16)((float)hi * kLoScale) : hi);
                     lb[t] = __builtin_bit_cast(uint16_t, (_Float16)((x - (float)hi) * kLoScale));
                 }
                 hw[e2] = hb[0] | (hb[1] << 16);
@@ -204,28 +213,74 @@ __device__ __forceinline__ void store_bytes(uint8_t* dst, const uint32_t (&w)[16
 }
 
 // One lane's half of a 32 x 128 fp16 input tile: row r = lane & 31, coordinates
-// [64h, 64h + 64) as 8 MFMA B fragments (zeros past the end).
+// [64h, 64h + 64) as 8 MFMA B fragments. Rows past the end (or a tile past the last) read
+// row 0 instead: their MFMA columns and results are discarded, and unconditional loads
+// never make the compiler wait for a register's earlier loads before reusing it.
 __device__ __forceinline__ void load_x_half(const uint16_t* __restrict__ in, int64_t tile,
                                             int64_t ntiles, int64_t rows, f16x8 (&x)[8]) {
     const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
     const int64_t m0 = tile * kTile;
     const bool ok = tile < ntiles && r < rows - m0;
-    const uint16_t* src = in + m0 * kHd + (r * kHd + 64 * h);
+    const uint16_t* src = in + (ok ? m0 * kHd + r * kHd : 0) + 64 * h;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (ok) v = ld16(src + 8 * s);
-        x[s] = __builtin_bit_cast(f16x8, v);
-    }
+    for (int s = 0; s < 8; ++s) x[s] = __builtin_bit_cast(f16x8, ld16(src + 8 * s));
 }
 
 // ---------------------------------------------------------------------------------------
 // MFMA compress / rotate of one tile by one wave (head_dim 128).
 //   kMode 0: quantize + pack to Dst (kBits 2, 3, 4, 8);  kMode 1: fp32 y (and norms).
-// Lane (r, h) ends block c holding coordinates 32c + 8g + 4h + e (g, e = 0..3) of vector r;
-// it quantizes them into half-groups (4 codes, 4*kBits bits, MSB first). After the 4 blocks
-// lane h owns groups [8h, 8h+8) of row r: 8*kBits contiguous bytes at byte 8*kBits*h.
+// Lane (r, h) ends block c holding coordinates 32c + 8g + 4h + e (g, e = 0..3) of vector r
+// (accumulator element 4g + e); it quantizes them into half-groups (4 codes, 4*kBits bits,
+// MSB first). After the 4 blocks lane h owns groups [8h, 8h+8) of row r: 8*kBits contiguous
+// bytes at byte 8*kBits*h.
+//
+// The 32 MFMA steps (block c = q / 8, K-step s = q % 8) are software-pipelined, one
+// scheduling region per step:
+//   * the rotation fragments of step q + kAhead are read from LDS during step q;
+//   * block c's MFMAs accumulate into set c % 2 while block c - 1 (the other set) is
+//     quantized two values per step: in step s the bucket-table reads of values 2s, 2s + 1
+//     are issued and the codes of values 2s - 2, 2s - 1 (read one step earlier) finish.
 // ---------------------------------------------------------------------------------------
+template <int kMode, int kBits, bool kUnitFast>
+struct TileQuant {
+    const Quantizer& qz;
+    float scale, offset, jmax;  // the bucket map, held in registers
+    float inv_s;
+    float y[16];
+    float2 ent[16];
+    uint32_t hw[4];
+    uint32_t (&half)[16];
+    float* __restrict__ y_out;
+    int64_t yrow;  // element offset of this lane's row in y_out, or -1 (kMode 1)
+
+    // Phase A of value v (accumulator element v of block c): scale, and for the fast
+    // quantizer issue the bucket-table read.
+    __device__ __forceinline__ void a(const f32x16& acc, int c, int v) {
+        y[v] = acc[v] * inv_s;
+        if constexpr (kMode == 1) {
+            if ((v & 3) == 3 && yrow >= 0)
+                *(f32x4*)&y_out[yrow + 32 * c + 8 * (v >> 2) + 4 * (threadIdx.x >> 5 & 1)] =
+                    f32x4{y[v - 3], y[v - 2], y[v - 1], y[v]};
+        } else if constexpr (kUnitFast) {
+            const float jf = fmaf(y[v], scale, offset);
+            ent[v] = qz.ent[(int)__builtin_amdgcn_fmed3f(jf, 0.0f, jmax)];
+        }
+    }
+    // Phase B of value v: the code, packed MSB first into the half-group of group v / 4.
+    __device__ __forceinline__ void b(int c, int v) {
+        if constexpr (kMode == 0) {
+            int code;
+            if constexpr (kUnitFast)
+                code = __float_as_int(ent[v].y) + (y[v] > ent[v].x ? 1 : 0);
+            else
+                code = quantize(qz, y[v]);
+            const int g = v >> 2;
+            hw[g] = ((v & 3) == 0 ? 0u : hw[g] << kBits) | (uint32_t)code;
+            if ((v & 3) == 3) half[4 * c + g] = hw[g];
+        }
+    }
+};
+
 template <int kMode, int kBits, bool kUnitFast, class Dst>
 __device__ __forceinline__ void compress_tile(const Quantizer& qz, const RotLds& L,
                                               const f16x8 (&x)[8], const Dst& dst,
@@ -242,55 +297,53 @@ __device__ __forceinline__ void compress_tile(const Quantizer& qz, const RotLds&
         if (np) *np = (uint16_t)f2h(nrm);
     }
     uint32_t half[16];  // kMode 0: half-group of group 4c + g held by this lane
-    // Block c's MFMAs accumulate into set c % 2 while block c - 1 is quantized from the other
-    // set, so the quantizer's VALU work overlaps the matrix core's.
-    f32x16 acc_hi[2], acc_lo[2];
-    auto mfma_block = [&](int c) {
-        const int b = c & 1;
-        acc_hi[b] = f32x16{};
-        acc_lo[b] = f32x16{};
+    // Both fragment parts carry the factor 2^12 (hi stored as 2^12 Pi_hi), so hi and lo
+    // products accumulate into one fp32 sum, 2^12 y_raw, scaled out with the norm.
+    TileQuant<kMode, kBits, kUnitFast> tq{qz, qz.scale, qz.offset, qz.jmax, inv * kLoInv,
+                                          {}, {}, {}, half, y_out,
+                                          row_ok ? (m0 + r) * kHd : -1};
+    constexpr int kAhead = 2;
+    constexpr int kRing = kAhead + 1;
+    f16x8 fh[kRing], fl[kRing];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            acc_hi[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag(L, c, s, 0, lane), x[s],
-                                                               acc_hi[b], 0, 0, 0);
-            acc_lo[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag(L, c, s, 1, lane), x[s],
-                                                               acc_lo[b], 0, 0, 0);
-        }
-    };
-    auto quant_block = [&](int c) {
-        const int b = c & 1;
+    for (int q = 0; q < kAhead; ++q) {
+        fh[q] = frag(L, q >> 3, q & 7, 0, lane);
+        fl[q] = frag(L, q >> 3, q & 7, 1, lane);
+    }
+    f32x16 acc[2];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            float y[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                y[e] = fmaf(acc_lo[b][4 * g + e], kLoInv, acc_hi[b][4 * g + e]) * inv;
-            if constexpr (kMode == 1) {
-                if (row_ok)
-                    *(f32x4*)&y_out[(m0 + r) * kHd + 32 * c + 8 * g + 4 * h] =
-                        f32x4{y[0], y[1], y[2], y[3]};
-            } else {
-                uint32_t hw = 0;
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    hw = (hw << kBits) |
-                         (uint32_t)(kUnitFast ? quantize_unit(qz, y[e]) : quantize(qz, y[e]));
-                half[4 * c + g] = hw;
-            }
-        }
-    };
-    // one scheduling region per (MFMA block c, quantize block c - 1) pair: the two interleave
-    // within it, and fragment reads cannot be hoisted across regions
-    __builtin_amdgcn_sched_barrier(0);
-    mfma_block(0);
-#pragma unroll
-    for (int c = 1; c < 4; ++c) {
+    for (int q = 0; q < 32; ++q) {
+        const int c = q >> 3, s = q & 7, b = c & 1;
         __builtin_amdgcn_sched_barrier(0);
-        mfma_block(c);
-        quant_block(c - 1);
+        if (q + kAhead < 32) {
+            const int n = q + kAhead;
+            fh[n % kRing] = frag(L, n >> 3, n & 7, 0, lane);
+            fl[n % kRing] = frag(L, n >> 3, n & 7, 1, lane);
+        }
+        if (s == 0) acc[b] = f32x16{};
+        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fh[q % kRing], x[s], acc[b], 0, 0, 0);
+        if (c > 0) {
+            tq.a(acc[b ^ 1], c - 1, 2 * s);
+            tq.a(acc[b ^ 1], c - 1, 2 * s + 1);
+        }
+        // the last two values of block c - 2 were looked up in block c - 1's final step
+        if (c > 1 && s == 0) {
+            tq.b(c - 2, 14);
+            tq.b(c - 2, 15);
+        }
+        if (c > 0 && s > 0) {
+            tq.b(c - 1, 2 * s - 2);
+            tq.b(c - 1, 2 * s - 1);
+        }
+        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fl[q % kRing], x[s], acc[b], 0, 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
-    quant_block(3);
+    tq.b(2, 14);
+    tq.b(2, 15);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) tq.a(acc[1], 3, v);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) tq.b(3, v);
     if constexpr (kMode == 0) {
         // Group j (< 8) and group j + 8: lane h = 0 gets both halves of group j, lane h = 1
         // both halves of group j + 8, as (first half, second half) in (half[j], half[j+8]).
@@ -313,26 +366,31 @@ __device__ __forceinline__ void compress_tile(const Quantizer& qz, const RotLds&
     }
 }
 
-// xa holds the wave's first tile (loaded before the workgroup's set-up).
+// xa and xb hold the wave's first two tiles (loads issued before the workgroup's set-up).
 template <int kMode, int kBits, bool kUnitFast, class Dst>
 __device__ __forceinline__ void compress_waves(const Quantizer& qz, const RotLds& L,
                                                const uint16_t* __restrict__ in, const Dst& dst,
                                                float* __restrict__ y_out, int64_t rows,
-                                               f16x8 (&xa)[8]) {
+                                               f16x8 (&xa)[8], f16x8 (&xb)[8]) {
     const int64_t ntiles = ceil_div(rows, kTile);
     const int64_t stride = (int64_t)gridDim.x * kWavesC;
-    int64_t tile = (int64_t)blockIdx.x * kWavesC + (threadIdx.x >> 6);
-    f16x8 xb[8];
-    // Two tiles per trip, ping-ponging the register buffers: each tile's successor is in
-    // flight while it computes.
+    int64_t tile = (int64_t)blockIdx.x * kWavesC + wave_id();
+    f16x8 xc[8];
+    // Three register buffers in rotation, one tile per step: while a tile computes, the
+    // loads of the next two are in flight.
     while (tile < ntiles) {
-        load_x_half(in, tile + stride, ntiles, rows, xb);
+        load_x_half(in, tile + 2 * stride, ntiles, rows, xc);
         compress_tile<kMode, kBits, kUnitFast>(qz, L, xa, dst, y_out, tile * kTile,
                                                (int)min<int64_t>(kTile, rows - tile * kTile));
         tile += stride;
         if (tile >= ntiles) break;
-        load_x_half(in, tile + stride, ntiles, rows, xa);
+        load_x_half(in, tile + 2 * stride, ntiles, rows, xa);
         compress_tile<kMode, kBits, kUnitFast>(qz, L, xb, dst, y_out, tile * kTile,
+                                               (int)min<int64_t>(kTile, rows - tile * kTile));
+        tile += stride;
+        if (tile >= ntiles) break;
+        load_x_half(in, tile + 2 * stride, ntiles, rows, xb);
+        compress_tile<kMode, kBits, kUnitFast>(qz, L, xc, dst, y_out, tile * kTile,
                                                (int)min<int64_t>(kTile, rows - tile * kTile));
         tile += stride;
     }
@@ -340,16 +398,18 @@ __device__ __forceinline__ void compress_waves(const Quantizer& qz, const RotLds
 
 // The general-quantizer tile loop (codebooks the fast bucket map cannot serve exactly), kept
 // out of line so that its register needs do not constrain the fast path's allocation.
-// It reloads the wave's first tile, and takes the destination by value: a reference would
+// It reloads the wave's first tiles, and takes the destination by value: a reference would
 // move the kernel argument into private memory for the fast path too.
 template <int kMode, int kBits, class Dst>
 __device__ __noinline__ void compress_waves_general(const Quantizer& qz, const RotLds& L,
                                                     const uint16_t* __restrict__ in, Dst dst,
                                                     float* __restrict__ y_out, int64_t rows) {
-    f16x8 xa[8];
-    load_x_half(in, (int64_t)blockIdx.x * kWavesC + (threadIdx.x >> 6), ceil_div(rows, kTile),
-                rows, xa);
-    compress_waves<kMode, kBits, false>(qz, L, in, dst, y_out, rows, xa);
+    const int64_t first = (int64_t)blockIdx.x * kWavesC + wave_id();
+    const int64_t ntiles = ceil_div(rows, kTile);
+    f16x8 xa[8], xb[8];
+    load_x_half(in, first, ntiles, rows, xa);
+    load_x_half(in, first + (int64_t)gridDim.x * kWavesC, ntiles, rows, xb);
+    compress_waves<kMode, kBits, false>(qz, L, in, dst, y_out, rows, xa, xb);
 }
 
 template <int kMode, int kBits, class Dst>
@@ -359,24 +419,32 @@ tq_compress_mfma_kernel(const uint16_t* __restrict__ in, const float* __restrict
                         float* __restrict__ y_out, int64_t rows) {
     __shared__ Quantizer qz;
     __shared__ RotLds rl;
-    // The centroids' loads go out first, then the first tile's and the rotation's; the
-    // quantizer build overlaps the latter. L <= kMaxLevels <= the block size.
-    static_assert(kMaxLevels <= 64 * kWavesC, "one centroid per thread");
-    const float c_own = kMode == 0 && (int)threadIdx.x < L ? cent[threadIdx.x] : 0.0f;
-    f16x8 xa[8];
-    load_x_half(in, (int64_t)blockIdx.x * kWavesC + (threadIdx.x >> 6), ceil_div(rows, kTile),
-                rows, xa);
-    RotStage<false, 64 * kWavesC> rs;
-    rs.load(rot);
+    // The centroids are loaded alone first (behind the chip-wide burst of the other loads
+    // their latency is several times longer); then the rotation's loads and the wave's first
+    // tile go out and stay in flight while wave 0 builds the quantizer. The second tile is only
+    // requested after the set-up: a wave stalls at issue once its CU has too many bytes in
+    // flight, and the set-up would wait behind it. The set-up's barriers order LDS only
+    // (a full __syncthreads would drain the loads first).
     if constexpr (kMode == 0) {
-        if ((int)threadIdx.x < L) qz.c[threadIdx.x] = c_own;
-        __syncthreads();
-        quantizer_finish(qz, L);  // has barriers
+        if (wave_id() == 0) {
+            for (int i = (int)threadIdx.x; i < L; i += 64) qz.c[i] = cent[i];
+        }
+    }
+    RotStage<false, 64 * kWavesC, true> rs;
+    rs.load(rot);
+    const int64_t first = (int64_t)blockIdx.x * kWavesC + wave_id();
+    const int64_t ntiles = ceil_div(rows, kTile);
+    f16x8 xa[8], xb[8];
+    load_x_half(in, first, ntiles, rows, xa);
+    // wave 0 builds the quantizer while the others stage the rotation
+    if constexpr (kMode == 0) {
+        if (wave_id() == 0) quantizer_finish<true>(qz, L);
     }
     rs.store(rl);
-    __syncthreads();
+    lds_barrier();
+    load_x_half(in, first + (int64_t)gridDim.x * kWavesC, ntiles, rows, xb);
     if (kMode == 1 || qz.unit_fast)
-        compress_waves<kMode, kBits, true>(qz, rl, in, dst, y_out, rows, xa);
+        compress_waves<kMode, kBits, true>(qz, rl, in, dst, y_out, rows, xa, xb);
     else
         compress_waves_general<kMode, kBits>(qz, rl, in, dst, y_out, rows);
 }
@@ -510,27 +578,25 @@ __device__ __forceinline__ void load_code_half(const uint8_t* __restrict__ packe
     const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
     const int64_t m0 = tile * kTile;
     const bool ok = tile < ntiles && r < rows - m0;
-    const uint8_t* src = packed + m0 * pd + (r * pd + 8 * kBits * h);
+    // rows past the end read row 0 (their results are not stored); see load_x_half
+    const int64_t row = ok ? m0 + r : 0;
+    const uint8_t* src = packed + row * pd + 8 * kBits * h;
+    if constexpr (kBits % 2 == 0) {  // 16, 32 or 64 bytes at a 16-byte aligned offset
 #pragma unroll
-    for (int i = 0; i < 2 * kBits; ++i) cw.w[i] = 0u;
-    if (ok) {
-        if constexpr (kBits % 2 == 0) {  // 16, 32 or 64 bytes at a 16-byte aligned offset
+        for (int i = 0; i < kBits / 2; ++i) {
+            const u32x4 v = ld16(src + 16 * i);
 #pragma unroll
-            for (int i = 0; i < kBits / 2; ++i) {
-                const u32x4 v = ld16(src + 16 * i);
+            for (int t = 0; t < 4; ++t) cw.w[4 * i + t] = v[t];
+        }
+    } else {  // 24 bytes at an 8-byte aligned offset
 #pragma unroll
-                for (int t = 0; t < 4; ++t) cw.w[4 * i + t] = v[t];
-            }
-        } else {  // 24 bytes at an 8-byte aligned offset
-#pragma unroll
-            for (int i = 0; i < kBits; ++i) {
-                const u32x2 v = *(const u32x2*)(src + 8 * i);
-                cw.w[2 * i] = v[0];
-                cw.w[2 * i + 1] = v[1];
-            }
+        for (int i = 0; i < kBits; ++i) {
+            const u32x2 v = *(const u32x2*)(src + 8 * i);
+            cw.w[2 * i] = v[0];
+            cw.w[2 * i + 1] = v[1];
         }
     }
-    cw.norm = ok ? norms[m0 + r] : (uint16_t)0;
+    cw.norm = norms[row];
 }
 
 // The 8 codes of group s of this lane's half as fp16 hi / lo B fragments.
@@ -623,28 +689,31 @@ tq_dequant_mfma_kernel(const uint8_t* __restrict__ packed, const uint16_t* __res
     __shared__ RotLds rl;
     const int64_t ntiles = ceil_div(rows, kTile);
     const int64_t stride = (int64_t)gridDim.x * kWavesD;
-    int64_t tile = (int64_t)blockIdx.x * kWavesD + (threadIdx.x >> 6);
-    // The first tile's loads go out before the set-up, which then overlaps their latency.
+    int64_t tile = (int64_t)blockIdx.x * kWavesD + wave_id();
+    // Loads go out in the order their data is needed: the centroids, the rotation, then the
+    // first tile, which stays in flight through the set-up (whose barriers order LDS only).
+    static_assert(kMaxLevels <= 64 * kWavesD, "one centroid per thread");
+    const float c_own = (int)threadIdx.x < L ? cent[threadIdx.x] : 0.0f;
+    RotStage<true, 64 * kWavesD, false> rs;
+    rs.load(rot);
     CodeHalf<kBits> ca, cb;
     load_code_half<kBits>(packed, norms, tile, ntiles, rows, ca);
-    RotStage<true, 64 * kWavesD> rs;
-    rs.load(rot);
-    for (int i = threadIdx.x; i < kMaxLevels; i += blockDim.x) {
-        const float c = i < L ? cent[i] : 0.0f;
-        const _Float16 hi = (_Float16)c;
+    if ((int)threadIdx.x < kMaxLevels) {
+        const _Float16 hi = (_Float16)c_own;
         const uint32_t hb = __builtin_bit_cast(uint16_t, hi);
-        const uint32_t lb = __builtin_bit_cast(uint16_t, (_Float16)((c - (float)hi) * kLoScale));
-        t.tab[i] = hb | (lb << 16);
+        const uint32_t lb =
+            __builtin_bit_cast(uint16_t, (_Float16)((c_own - (float)hi) * kLoScale));
+        t.tab[threadIdx.x] = hb | (lb << 16);
     }
     rs.store(rl);
-    __syncthreads();
+    lds_barrier();
     if constexpr (kBits == 4) {
         for (int b = threadIdx.x; b < 256; b += blockDim.x) {
             uint32_t vh, vl;
             split_pair(t.tab[b >> 4], t.tab[b & 15], vh, vl);
             t.pair[b] = u32x2{vh, vl};
         }
-        __syncthreads();
+        lds_barrier();
     }
     while (tile < ntiles) {
         load_code_half<kBits>(packed, norms, tile + stride, ntiles, rows, cb);

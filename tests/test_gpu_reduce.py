@@ -86,6 +86,35 @@ def test_argmax_bit_exact_with_ties(dev, rows, cols):
     assert not fl.cpu().numpy().any()
 
 
+@pytest.mark.parametrize("cols", [4100, 12292, 128256, 8195])
+def test_argmax_row_tail(dev, cols):
+    """Maxima in and around a row's last, partial 4096-element chunk (whose out-of-row
+    positions the kernel reads as copies of the row's last elements and must ignore)."""
+    rng = np.random.default_rng(cols)
+    l = rng.integers(-50, 50, (5, cols)).astype(np.float32)
+    last = (cols - 1) // 4096 * 4096
+    l[0, cols - 1] = 99.0
+    l[1, [0, cols - 4]] = 99.0
+    l[2, last] = 99.0
+    l[3, 0] = 99.0
+    l[3, last:] = -60.0  # tail lower than the rest
+    l[4, cols - 2] = 99.0
+    l[4, cols - 1] = 98.0
+    tl = torch.from_numpy(l).to(dev)
+    idx = torch.empty(5, dtype=torch.int32, device=dev)
+    fl = torch.empty(5, dtype=torch.int32, device=dev)
+    K.argmax_rows(tl, idx, fl)
+    probs, idx2, _ = run_softmax(l, dev)
+    want, status = oracle.argmax_rows(l)
+    assert (status == 0).all()
+    assert list(want) == [cols - 1, cols - 4, last, 0, cols - 2]
+    assert np.array_equal(idx.cpu().numpy(), want.astype(np.int32))
+    assert np.array_equal(idx2, want.astype(np.int32))
+    ref = oracle.softmax_rows(l)
+    np.testing.assert_allclose(probs, ref / ref.sum(1, dtype=np.float64, keepdims=True),
+                               rtol=1e-5, atol=1e-12)
+
+
 def test_argmax_signed_zero_ties(dev):
     l = np.array([[-1.0, 0.0, -0.0, -2.0], [-1.0, -0.0, 0.0, -3.0]], np.float32)
     tl = torch.from_numpy(l).to(dev)
