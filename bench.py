@@ -373,23 +373,37 @@ def run_tq(args, torch, K, dev):
         kd = torch.empty_like(k)
         vd = torch.empty_like(v)
 
+        # the per-layer plans (built once, as the cache manager uploads the rotations and
+        # codebooks once) and the reference-signature entries that rebuild them per call
+        kplan, vplan = K.TqPlan(krot, cent, bits), K.TqPlan(vrot, cent, bits)
+
         def comp():
+            K.tq_compress_planned(kplan, k, kp, kn)
+            K.tq_compress_planned(vplan, v, vp, vn)
+
+        def deq():
+            K.tq_dequant_planned(kplan, kp, kn, kd)
+            K.tq_dequant_planned(vplan, vp, vn, vd)
+
+        def comp_unplanned():
             K.tq_compress(k, krot, cent, bits, kp, kn)
             K.tq_compress(v, vrot, cent, bits, vp, vn)
 
-        def deq():
+        def deq_unplanned():
             K.tq_dequant(kp, kn, krot, cent, bits, kd)
             K.tq_dequant(vp, vn, vrot, cent, bits, vd)
 
         nb = 2 * (N * H * hd * 2 + N * H * pd + N * H * 2)  # K and V: read fp16, write codes+norms
         flops = 2 * 2 * N * H * hd * hd
-        for name, fn in (("compress", comp), ("dequant", deq)):
+        for name, fn, tkey in (("compress", comp, "compress"), ("dequant", deq, "dequant"),
+                               ("compress_unplanned", comp_unplanned, None),
+                               ("dequant_unplanned", deq_unplanned, None)):
             us = timer.time_us(fn, 20, warmup=3)
             out[f"tq_{name}_kv_{bits}bit"] = {
                 "us": round(us, 2), "GB/s": round(gbs(nb, us), 1),
                 "frac_of_peak": round(gbs(nb, us) / PEAK_HBM_GBS, 4), "bytes": nb,
                 "rotation_TFLOP/s": round(flops / (us * 1e-6) / 1e12, 1),
-                "traffic": traffic_of(f"tq_{name}_{bits}bit")}
+                "traffic": traffic_of(f"tq_{tkey}_{bits}bit") if tkey else None}
     return {"workload": "TurboQuant KV compress / dequantize, one layer, [32768, 8, 128] K and V",
             "kernels": out}
 
@@ -498,13 +512,15 @@ def pmc_sequence(torch, K, dev):
         dq = [torch.empty_like(kv[0]) for _ in range(2)]
         nbytes = 2 * (N * H * hd * 2 + N * H * pd + N * H * 2)
 
-        def comp(cent=cent, bits=bits, pk=pk, nm=nm):
-            for i in range(2):
-                K.tq_compress(kv[i], rots[i], cent, bits, pk[i], nm[i])
+        plans = [K.TqPlan(rots[i], cent, bits) for i in range(2)]
 
-        def deq(cent=cent, bits=bits, pk=pk, nm=nm, dq=dq):
+        def comp(plans=plans, pk=pk, nm=nm):
             for i in range(2):
-                K.tq_dequant(pk[i], nm[i], rots[i], cent, bits, dq[i])
+                K.tq_compress_planned(plans[i], kv[i], pk[i], nm[i])
+
+        def deq(plans=plans, pk=pk, nm=nm, dq=dq):
+            for i in range(2):
+                K.tq_dequant_planned(plans[i], pk[i], nm[i], dq[i])
 
         seq += [(f"tq_compress_{bits}bit", comp, nbytes), (f"tq_dequant_{bits}bit", deq, nbytes)]
     fn, nb_att, _, _ = attention_inputs(torch, K, dev)

@@ -60,6 +60,11 @@ SIGNATURES = {
     "fhip_launch_tq_rotate": (I, [P, P, P, P, I, I, P]),
     "fhip_launch_tq_compress_pages": (I, [P, P, P, I, I, P, P, I64, I64, P, I, I, I, I, I, P]),
     "fhip_launch_tq_dequant": (I, [P, P, P, P, I, P, I, I, I, I, I, P]),
+    "fhip_tq_plan_create": (I, [P, P, I, I, I, P, C.POINTER(P)]),
+    "fhip_tq_plan_destroy": (None, [P]),
+    "fhip_launch_tq_compress_planned": (I, [P, P, P, P, I, I, P]),
+    "fhip_launch_tq_compress_pages_planned": (I, [P, P, P, P, I64, I64, P, I, I, I, I, P]),
+    "fhip_launch_tq_dequant_planned": (I, [P, P, P, P, I, I, P]),
     "fhip_attention_tq_workspace_bytes": (SZ, [I, I, I, I]),
     "fhip_launch_attention_tq_decode": (I, [P, P, P, P, I, I, I, P, P, P, P, I64, I64, I64, I64,
                                             P, P, P, P, I, I, I, I, I, P, P]),

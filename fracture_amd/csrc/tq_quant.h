@@ -27,7 +27,7 @@ namespace fhip {
 constexpr int kMaxLevels = 256;
 constexpr int kMaxBuckets = 1024;
 
-struct Quantizer {
+struct alignas(16) Quantizer {
     float c[kMaxLevels];             // centroids
     float t[kMaxLevels];             // exact thresholds t_q, q < L-1
     int jt[kMaxLevels];              // bucket of t_q

@@ -24,6 +24,8 @@
 // halves of a 16-byte group exchange them with v_permlane32_swap.
 // Other head dims and bit widths use a per-vector VALU path that follows the reference
 // kernel's arithmetic.
+#include <type_traits>
+
 #include "tq_quant.h"
 
 using namespace fhip;
@@ -216,12 +218,17 @@ __device__ __forceinline__ void store_bytes(uint8_t* dst, const uint32_t (&w)[16
 // [64h, 64h + 64) as 8 MFMA B fragments. Rows past the end (or a tile past the last) read
 // row 0 instead: their MFMA columns and results are discarded, and unconditional loads
 // never make the compiler wait for a register's earlier loads before reusing it.
-__device__ __forceinline__ void load_x_half(const uint16_t* __restrict__ in, int64_t tile,
-                                            int64_t ntiles, int64_t rows, f16x8 (&x)[8]) {
+__device__ __forceinline__ const uint16_t* x_half_src(const uint16_t* __restrict__ in,
+                                                     int64_t tile, int64_t ntiles,
+                                                     int64_t rows) {
     const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
     const int64_t m0 = tile * kTile;
     const bool ok = tile < ntiles && r < rows - m0;
-    const uint16_t* src = in + (ok ? m0 * kHd + r * kHd : 0) + 64 * h;
+    return in + (ok ? m0 * kHd + r * kHd : 0) + 64 * h;
+}
+__device__ __forceinline__ void load_x_half(const uint16_t* __restrict__ in, int64_t tile,
+                                            int64_t ntiles, int64_t rows, f16x8 (&x)[8]) {
+    const uint16_t* src = x_half_src(in, tile, ntiles, rows);
 #pragma unroll
     for (int s = 0; s < 8; ++s) x[s] = __builtin_bit_cast(f16x8, ld16(src + 8 * s));
 }
@@ -281,10 +288,13 @@ struct TileQuant {
     }
 };
 
+// pf / pf_src: the wave's prefetch of a later tile, issued one 16-byte load every fourth
+// step so that a wave never stalls at issue behind a full memory queue before computing.
 template <int kMode, int kBits, bool kUnitFast, class Dst>
 __device__ __forceinline__ void compress_tile(const Quantizer& qz, const RotLds& L,
                                               const f16x8 (&x)[8], const Dst& dst,
-                                              float* __restrict__ y_out, int64_t m0, int nvalid) {
+                                              float* __restrict__ y_out, int64_t m0, int nvalid,
+                                              f16x8 (&pf)[8], const uint16_t* pf_src) {
     const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
     float ssq = 0.0f;  // this lane's half of vector r
 #pragma unroll
@@ -315,6 +325,7 @@ __device__ __forceinline__ void compress_tile(const Quantizer& qz, const RotLds&
     for (int q = 0; q < 32; ++q) {
         const int c = q >> 3, s = q & 7, b = c & 1;
         __builtin_amdgcn_sched_barrier(0);
+        if ((q & 3) == 0) pf[q >> 2] = __builtin_bit_cast(f16x8, ld16(pf_src + 8 * (q >> 2)));
         if (q + kAhead < 32) {
             const int n = q + kAhead;
             fh[n % kRing] = frag(L, n >> 3, n & 7, 0, lane);
@@ -379,19 +390,19 @@ __device__ __forceinline__ void compress_waves(const Quantizer& qz, const RotLds
     // Three register buffers in rotation, one tile per step: while a tile computes, the
     // loads of the next two are in flight.
     while (tile < ntiles) {
-        load_x_half(in, tile + 2 * stride, ntiles, rows, xc);
         compress_tile<kMode, kBits, kUnitFast>(qz, L, xa, dst, y_out, tile * kTile,
-                                               (int)min<int64_t>(kTile, rows - tile * kTile));
+                                               (int)min<int64_t>(kTile, rows - tile * kTile), xc,
+                                               x_half_src(in, tile + 2 * stride, ntiles, rows));
         tile += stride;
         if (tile >= ntiles) break;
-        load_x_half(in, tile + 2 * stride, ntiles, rows, xa);
         compress_tile<kMode, kBits, kUnitFast>(qz, L, xb, dst, y_out, tile * kTile,
-                                               (int)min<int64_t>(kTile, rows - tile * kTile));
+                                               (int)min<int64_t>(kTile, rows - tile * kTile), xa,
+                                               x_half_src(in, tile + 2 * stride, ntiles, rows));
         tile += stride;
         if (tile >= ntiles) break;
-        load_x_half(in, tile + 2 * stride, ntiles, rows, xb);
         compress_tile<kMode, kBits, kUnitFast>(qz, L, xc, dst, y_out, tile * kTile,
-                                               (int)min<int64_t>(kTile, rows - tile * kTile));
+                                               (int)min<int64_t>(kTile, rows - tile * kTile), xb,
+                                               x_half_src(in, tile + 2 * stride, ntiles, rows));
         tile += stride;
     }
 }
@@ -412,13 +423,64 @@ __device__ __noinline__ void compress_waves_general(const Quantizer& qz, const R
     compress_waves<kMode, kBits, false>(qz, L, in, dst, y_out, rows, xa, xb);
 }
 
-template <int kMode, int kBits, class Dst>
+// Copy of kBytes (a multiple of 16) from global memory into LDS by the whole block, in two
+// steps so that other loads can be issued between them: load() puts every thread's chunks in
+// flight, store() writes them to LDS.
+template <int kThreads, int kBytes>
+struct LdsCopy {
+    static_assert(kBytes % 16 == 0, "16-byte chunks");
+    static constexpr int kN = kBytes / 16, kPer = (kN + kThreads - 1) / kThreads;
+    u32x4 v[kPer];
+    __device__ __forceinline__ void load(const void* __restrict__ src) {
+        const u32x4* s = (const u32x4*)src;
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) v[k] = ld16(s + min((int)threadIdx.x + k * kThreads, kN - 1));
+    }
+    // Threads past the end rewrite the last chunk with its own value: no branch, which would
+    // let the compiler sink the load into it and wait there for every older load.
+    __device__ __forceinline__ void store(void* __restrict__ dst) const {
+        u32x4* d = (u32x4*)dst;
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) d[min((int)threadIdx.x + k * kThreads, kN - 1)] = v[k];
+    }
+};
+
+struct TqPlanDev;
+__device__ __forceinline__ const Quantizer& plan_quantizer(const TqPlanDev* p);
+__device__ __forceinline__ const RotLds& plan_compress_frags(const TqPlanDev* p);
+
+// kPlanned: the quantizer and the rotation fragments come ready-made from a plan (built once
+// per rotation and codebook by tq_plan_kernel) and are only copied into LDS; otherwise the
+// workgroup builds them from rot and cent.
+template <int kMode, int kBits, class Dst, bool kPlanned>
 __global__ __launch_bounds__(64 * kWavesC) __attribute__((amdgpu_waves_per_eu(2))) void
 tq_compress_mfma_kernel(const uint16_t* __restrict__ in, const float* __restrict__ rot,
-                        const float* __restrict__ cent, int L, Dst dst,
-                        float* __restrict__ y_out, int64_t rows) {
+                        const float* __restrict__ cent, int L, const TqPlanDev* __restrict__ plan,
+                        Dst dst, float* __restrict__ y_out, int64_t rows) {
     __shared__ Quantizer qz;
     __shared__ RotLds rl;
+    if constexpr (kPlanned) {
+        // the plan's loads, then the first tile's (in flight through the copy's stores)
+        const int64_t first = (int64_t)blockIdx.x * kWavesC + wave_id();
+        const int64_t ntiles = ceil_div(rows, kTile);
+        LdsCopy<64 * kWavesC, (int)sizeof(Quantizer)> qc;
+        LdsCopy<64 * kWavesC, (int)sizeof(RotLds)> rc;
+        if constexpr (kMode == 0) qc.load(&plan_quantizer(plan));
+        rc.load(&plan_compress_frags(plan));
+        __builtin_amdgcn_sched_barrier(0);
+        f16x8 xa[8], xb[8];
+        load_x_half(in, first, ntiles, rows, xa);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (kMode == 0) qc.store(&qz);
+        rc.store(&rl);
+        lds_barrier();
+        load_x_half(in, first + (int64_t)gridDim.x * kWavesC, ntiles, rows, xb);
+        if (kMode == 1 || qz.unit_fast)
+            compress_waves<kMode, kBits, true>(qz, rl, in, dst, y_out, rows, xa, xb);
+        else
+            compress_waves_general<kMode, kBits>(qz, rl, in, dst, y_out, rows);
+        return;
+    }
     // The centroids are loaded alone first (behind the chip-wide burst of the other loads
     // their latency is several times longer); then the rotation's loads and the wave's first
     // tile go out and stay in flight while wave 0 builds the quantizer. The second tile is only
@@ -680,41 +742,23 @@ __device__ __forceinline__ void dequant_tile(const DequantLds& t, const RotLds& 
     }
 }
 
+// Table entry of centroid c: fp16 bits of c_hi | c_lo' << 16 (c = c_hi + c_lo' 2^-12).
+__device__ __forceinline__ uint32_t dq_tab_entry(float c) {
+    const _Float16 hi = (_Float16)c;
+    const uint32_t hb = __builtin_bit_cast(uint16_t, hi);
+    const uint32_t lb = __builtin_bit_cast(uint16_t, (_Float16)((c - (float)hi) * kLoScale));
+    return hb | (lb << 16);
+}
+
+// The wave's tile loop: ca holds its first tile (loads issued); each tile's successor is in
+// flight while it computes.
 template <int kBits>
-__global__ __launch_bounds__(64 * kWavesD) __attribute__((amdgpu_waves_per_eu(3))) void
-tq_dequant_mfma_kernel(const uint8_t* __restrict__ packed, const uint16_t* __restrict__ norms,
-                       const float* __restrict__ rot, const float* __restrict__ cent, int L,
-                       uint16_t* __restrict__ out, int64_t rows) {
-    __shared__ DequantLds t;
-    __shared__ RotLds rl;
-    const int64_t ntiles = ceil_div(rows, kTile);
-    const int64_t stride = (int64_t)gridDim.x * kWavesD;
-    int64_t tile = (int64_t)blockIdx.x * kWavesD + wave_id();
-    // Loads go out in the order their data is needed: the centroids, the rotation, then the
-    // first tile, which stays in flight through the set-up (whose barriers order LDS only).
-    static_assert(kMaxLevels <= 64 * kWavesD, "one centroid per thread");
-    const float c_own = (int)threadIdx.x < L ? cent[threadIdx.x] : 0.0f;
-    RotStage<true, 64 * kWavesD, false> rs;
-    rs.load(rot);
-    CodeHalf<kBits> ca, cb;
-    load_code_half<kBits>(packed, norms, tile, ntiles, rows, ca);
-    if ((int)threadIdx.x < kMaxLevels) {
-        const _Float16 hi = (_Float16)c_own;
-        const uint32_t hb = __builtin_bit_cast(uint16_t, hi);
-        const uint32_t lb =
-            __builtin_bit_cast(uint16_t, (_Float16)((c_own - (float)hi) * kLoScale));
-        t.tab[threadIdx.x] = hb | (lb << 16);
-    }
-    rs.store(rl);
-    lds_barrier();
-    if constexpr (kBits == 4) {
-        for (int b = threadIdx.x; b < 256; b += blockDim.x) {
-            uint32_t vh, vl;
-            split_pair(t.tab[b >> 4], t.tab[b & 15], vh, vl);
-            t.pair[b] = u32x2{vh, vl};
-        }
-        lds_barrier();
-    }
+__device__ __forceinline__ void dequant_waves(const DequantLds& t, const RotLds& rl,
+                                              const uint8_t* __restrict__ packed,
+                                              const uint16_t* __restrict__ norms,
+                                              uint16_t* __restrict__ out, int64_t rows,
+                                              int64_t tile, int64_t stride, int64_t ntiles,
+                                              CodeHalf<kBits>& ca, CodeHalf<kBits>& cb) {
     while (tile < ntiles) {
         load_code_half<kBits>(packed, norms, tile + stride, ntiles, rows, cb);
         dequant_tile<kBits>(t, rl, ca, out, tile * kTile,
@@ -726,6 +770,110 @@ tq_dequant_mfma_kernel(const uint8_t* __restrict__ packed, const uint16_t* __res
                             (int)min<int64_t>(kTile, rows - tile * kTile));
         tile += stride;
     }
+}
+
+// ---------------------------------------------------------------------------------------
+// Plan: everything the MFMA kernels derive from one rotation and codebook, built once
+// (tq_plan_kernel) in the layouts the kernels keep in LDS, plus the fp32 originals for the
+// generic kernels.
+// ---------------------------------------------------------------------------------------
+struct TqPlanDev {
+    RotLds comp;         // compress fragments (hi scaled by 2^12, lo')
+    RotLds deq;          // dequantize fragments (transposed, hi, lo')
+    Quantizer qz;        // the built quantizer
+    DequantLds dt;       // dequantize centroid tables
+    float rot[kHd * kHd];
+    float cent[kMaxLevels];
+};
+__device__ __forceinline__ const Quantizer& plan_quantizer(const TqPlanDev* p) { return p->qz; }
+__device__ __forceinline__ const RotLds& plan_compress_frags(const TqPlanDev* p) {
+    return p->comp;
+}
+
+template <int kBits, bool kPlanned>
+__global__ __launch_bounds__(64 * kWavesD) __attribute__((amdgpu_waves_per_eu(3))) void
+tq_dequant_mfma_kernel(const uint8_t* __restrict__ packed, const uint16_t* __restrict__ norms,
+                       const float* __restrict__ rot, const float* __restrict__ cent, int L,
+                       const TqPlanDev* __restrict__ plan, uint16_t* __restrict__ out,
+                       int64_t rows) {
+    __shared__ DequantLds t;
+    __shared__ RotLds rl;
+    const int64_t ntiles = ceil_div(rows, kTile);
+    const int64_t stride = (int64_t)gridDim.x * kWavesD;
+    int64_t tile = (int64_t)blockIdx.x * kWavesD + wave_id();
+    if constexpr (kPlanned) {
+        LdsCopy<64 * kWavesD, (int)sizeof(DequantLds)> tc;
+        LdsCopy<64 * kWavesD, (int)sizeof(RotLds)> rc;
+        tc.load(&plan->dt);
+        rc.load(&plan->deq);
+        __builtin_amdgcn_sched_barrier(0);
+        CodeHalf<kBits> ca, cb;
+        load_code_half<kBits>(packed, norms, tile, ntiles, rows, ca);
+        __builtin_amdgcn_sched_barrier(0);
+        tc.store(&t);
+        rc.store(&rl);
+        lds_barrier();
+        dequant_waves<kBits>(t, rl, packed, norms, out, rows, tile, stride, ntiles, ca, cb);
+        return;
+    }
+    // Loads go out in the order their data is needed: the centroids, the rotation, then the
+    // first tile, which stays in flight through the set-up (whose barriers order LDS only).
+    static_assert(kMaxLevels <= 64 * kWavesD, "one centroid per thread");
+    const float c_own = (int)threadIdx.x < L ? cent[threadIdx.x] : 0.0f;
+    RotStage<true, 64 * kWavesD, false> rs;
+    rs.load(rot);
+    CodeHalf<kBits> ca, cb;
+    load_code_half<kBits>(packed, norms, tile, ntiles, rows, ca);
+    if ((int)threadIdx.x < kMaxLevels) t.tab[threadIdx.x] = dq_tab_entry(c_own);
+    rs.store(rl);
+    lds_barrier();
+    if constexpr (kBits == 4) {
+        for (int b = threadIdx.x; b < 256; b += blockDim.x) {
+            uint32_t vh, vl;
+            split_pair(t.tab[b >> 4], t.tab[b & 15], vh, vl);
+            t.pair[b] = u32x2{vh, vl};
+        }
+        lds_barrier();
+    }
+    dequant_waves<kBits>(t, rl, packed, norms, out, rows, tile, stride, ntiles, ca, cb);
+}
+
+// Build a plan (one workgroup): the quantizer exactly as the compress kernel builds it, both
+// fragment layouts exactly as the kernels stage them, the dequantize tables, and copies of
+// the fp32 rotation and centroids.
+constexpr int kPlanThreads = 64 * kWavesC;
+__global__ __launch_bounds__(kPlanThreads) void tq_plan_kernel(const float* __restrict__ rot,
+                                                               const float* __restrict__ cent,
+                                                               int L, TqPlanDev* __restrict__ p) {
+    __shared__ Quantizer qz;
+    quantizer_build(qz, cent, L);
+    {
+        RotStage<false, kPlanThreads, true> rs;
+        rs.load(rot);
+        rs.store(p->comp);
+    }
+    {
+        RotStage<true, kPlanThreads, false> rs;
+        rs.load(rot);
+        rs.store(p->deq);
+    }
+    for (int i = threadIdx.x; i < kHd * kHd; i += kPlanThreads) p->rot[i] = rot[i];
+    for (int i = threadIdx.x; i < kMaxLevels; i += kPlanThreads) {
+        const float c = i < L ? cent[i] : 0.0f;
+        p->cent[i] = c;
+        p->dt.tab[i] = dq_tab_entry(c);
+    }
+    for (int b = threadIdx.x; b < 256; b += kPlanThreads) {
+        const float c0 = (b >> 4) < L ? cent[b >> 4] : 0.0f;
+        const float c1 = (b & 15) < L ? cent[b & 15] : 0.0f;
+        uint32_t vh, vl;
+        split_pair(dq_tab_entry(c0), dq_tab_entry(c1), vh, vl);
+        p->dt.pair[b] = u32x2{vh, vl};
+    }
+    __syncthreads();
+    const uint32_t* q = (const uint32_t*)&qz;
+    uint32_t* d = (uint32_t*)&p->qz;
+    for (int i = threadIdx.x; i < (int)(sizeof(Quantizer) / 4); i += kPlanThreads) d[i] = q[i];
 }
 
 // Generic-head_dim dequantize on the VALU (turboquant_decompress.cu order).
@@ -776,30 +924,71 @@ int mfma_grid(int64_t ntiles, int waves) {
     return (int)(need < cus ? (need > 0 ? need : 1) : cus);
 }
 
+// plan: non-null for the planned kernels (rot and cent then point into the plan).
 template <int kMode, class Dst>
 int launch_compress(const void* input, const float* rot, const float* cent, int L, int bits,
-                    Dst dst, float* y_out, int64_t rows, int hd, hipStream_t s) {
+                    Dst dst, float* y_out, int64_t rows, int hd, hipStream_t s,
+                    const TqPlanDev* plan = nullptr) {
     if (rows == 0) return hipSuccess;
     const bool mfma_bits = kMode == 1 || bits == 2 || bits == 3 || bits == 4 || bits == 8;
     if (hd == kHd && mfma_bits && fhip_host::aligned16(input) &&
         (kMode == 0 || fhip_host::aligned16(y_out))) {
-        auto kern = tq_compress_mfma_kernel<kMode, 4, Dst>;
-        if constexpr (kMode == 0) {
-            switch (bits) {
-                case 2: kern = tq_compress_mfma_kernel<kMode, 2, Dst>; break;
-                case 3: kern = tq_compress_mfma_kernel<kMode, 3, Dst>; break;
-                case 8: kern = tq_compress_mfma_kernel<kMode, 8, Dst>; break;
-                default: break;
+        auto pick = [&](auto planned) {
+            constexpr bool kP = decltype(planned)::value;
+            auto kern = tq_compress_mfma_kernel<kMode, 4, Dst, kP>;
+            if constexpr (kMode == 0) {
+                switch (bits) {
+                    case 2: kern = tq_compress_mfma_kernel<kMode, 2, Dst, kP>; break;
+                    case 3: kern = tq_compress_mfma_kernel<kMode, 3, Dst, kP>; break;
+                    case 8: kern = tq_compress_mfma_kernel<kMode, 8, Dst, kP>; break;
+                    default: break;
+                }
             }
-        }
+            return kern;
+        };
+        auto kern = plan ? pick(std::true_type{}) : pick(std::false_type{});
         hipLaunchKernelGGL(kern, dim3(mfma_grid(ceil_div(rows, kTile), kWavesC)),
-                           dim3(64 * kWavesC), 0, s, (const uint16_t*)input, rot, cent, L, dst,
-                           y_out, rows);
+                           dim3(64 * kWavesC), 0, s, (const uint16_t*)input, rot, cent, L, plan,
+                           dst, y_out, rows);
     } else {
         const int grid = tq_grid(rows, 2048);
         const size_t lds = 2 * (size_t)hd * sizeof(float);
         hipLaunchKernelGGL((tq_compress_generic_kernel<kMode, Dst>), dim3(grid), dim3(256), lds,
                            s, (const uint16_t*)input, rot, cent, L, bits, dst, y_out, rows, hd);
+    }
+    return hipGetLastError();
+}
+
+int launch_dequant(const void* packed_in, const void* norms_in, const float* rotation,
+                   const float* centroids, int L, void* output, int64_t rows, int head_dim,
+                   int bits, int packed_dim_per_head, hipStream_t s,
+                   const TqPlanDev* plan = nullptr) {
+    const bool mfma_bits = bits == 2 || bits == 3 || bits == 4 || bits == 8;
+    if (head_dim == kHd && mfma_bits && packed_dim_per_head == 16 * bits &&
+        fhip_host::aligned16(output) && fhip_host::aligned16(packed_in) &&
+        (((uintptr_t)norms_in) & 1u) == 0) {
+        auto pick = [&](auto planned) {
+            constexpr bool kP = decltype(planned)::value;
+            auto kern = tq_dequant_mfma_kernel<4, kP>;
+            switch (bits) {
+                case 2: kern = tq_dequant_mfma_kernel<2, kP>; break;
+                case 3: kern = tq_dequant_mfma_kernel<3, kP>; break;
+                case 8: kern = tq_dequant_mfma_kernel<8, kP>; break;
+                default: break;
+            }
+            return kern;
+        };
+        auto kern = plan ? pick(std::true_type{}) : pick(std::false_type{});
+        hipLaunchKernelGGL(kern, dim3(mfma_grid(ceil_div(rows, kTile), kWavesD)),
+                           dim3(64 * kWavesD), 0, s, (const uint8_t*)packed_in,
+                           (const uint16_t*)norms_in, rotation, centroids, L, plan,
+                           (uint16_t*)output, rows);
+    } else {
+        const int grid = tq_grid(rows, 2048);
+        hipLaunchKernelGGL(tq_dequant_generic_kernel, dim3(grid), dim3(256),
+                           (size_t)head_dim * sizeof(float), s, (const uint8_t*)packed_in,
+                           (const uint16_t*)norms_in, rotation, centroids, bits,
+                           (uint16_t*)output, rows, head_dim, (int64_t)packed_dim_per_head);
     }
     return hipGetLastError();
 }
@@ -886,30 +1075,8 @@ int fhip_launch_tq_dequant(const void* packed_in, const void* norms_in, const fl
     if (rows == 0) return hipSuccess;
     if (!packed_in || !norms_in || !rotation || !centroids || !output)
         return hipErrorInvalidValue;
-    hipStream_t s = fhip_host::as_stream(stream);
-    const int L = n_levels;
-    const bool mfma_bits = bits == 2 || bits == 3 || bits == 4 || bits == 8;
-    if (head_dim == kHd && mfma_bits && packed_dim_per_head == 16 * bits &&
-        fhip_host::aligned16(output) && fhip_host::aligned16(packed_in) &&
-        (((uintptr_t)norms_in) & 1u) == 0) {
-        auto kern = tq_dequant_mfma_kernel<4>;
-        switch (bits) {
-            case 2: kern = tq_dequant_mfma_kernel<2>; break;
-            case 3: kern = tq_dequant_mfma_kernel<3>; break;
-            case 8: kern = tq_dequant_mfma_kernel<8>; break;
-            default: break;
-        }
-        hipLaunchKernelGGL(kern, dim3(mfma_grid(ceil_div(rows, kTile), kWavesD)),
-                           dim3(64 * kWavesD), 0, s, (const uint8_t*)packed_in, (const uint16_t*)norms_in, rotation,
-                           centroids, L, (uint16_t*)output, rows);
-    } else {
-        const int grid = tq_grid(rows, 2048);
-        hipLaunchKernelGGL(tq_dequant_generic_kernel, dim3(grid), dim3(256),
-                           (size_t)head_dim * sizeof(float), s, (const uint8_t*)packed_in,
-                           (const uint16_t*)norms_in, rotation, centroids, bits,
-                           (uint16_t*)output, rows, head_dim, (int64_t)packed_dim_per_head);
-    }
-    return hipGetLastError();
+    return launch_dequant(packed_in, norms_in, rotation, centroids, n_levels, output, rows,
+                          head_dim, bits, packed_dim_per_head, fhip_host::as_stream(stream));
 }
 
 int fhip_launch_turboquant_decompress(const void* packed_in, const void* norms_in,
@@ -921,6 +1088,86 @@ int fhip_launch_turboquant_decompress(const void* packed_in, const void* norms_i
     return fhip_launch_tq_dequant(packed_in, norms_in, rotation, centroids, 1 << bits, output,
                                   num_tokens, num_kv_heads, head_dim, bits, packed_dim_per_head,
                                   stream);
+}
+
+struct fhip_tq_plan {
+    TqPlanDev* dev;
+    int n_levels, bits, head_dim;
+};
+
+int fhip_tq_plan_create(const float* rotation, const float* centroids, int n_levels, int bits,
+                        int head_dim, fhip_stream_t stream, fhip_tq_plan** out) {
+    if (!out) return hipErrorInvalidValue;
+    *out = nullptr;
+    if (!rotation || !centroids || head_dim != kHd || !tq_args_ok(n_levels, bits))
+        return hipErrorInvalidValue;
+    TqPlanDev* dev = nullptr;
+    hipError_t e = hipMalloc((void**)&dev, sizeof(TqPlanDev));
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(tq_plan_kernel, dim3(1), dim3(kPlanThreads), 0,
+                       fhip_host::as_stream(stream), rotation, centroids, n_levels, dev);
+    e = hipGetLastError();
+    if (e != hipSuccess) {
+        (void)hipFree(dev);
+        return e;
+    }
+    *out = new fhip_tq_plan{dev, n_levels, bits, head_dim};
+    return hipSuccess;
+}
+
+void fhip_tq_plan_destroy(fhip_tq_plan* plan) {
+    if (!plan) return;
+    (void)hipFree(plan->dev);  // hipFree waits for work that may still use the plan
+    delete plan;
+}
+
+int fhip_launch_tq_compress_planned(const fhip_tq_plan* plan, const void* input,
+                                    void* packed_out, void* norms_out, int num_tokens,
+                                    int num_kv_heads, fhip_stream_t stream) {
+    if (!plan || num_tokens < 0 || num_kv_heads < 0) return hipErrorInvalidValue;
+    const int64_t rows = (int64_t)num_tokens * num_kv_heads;
+    if (rows == 0) return hipSuccess;
+    if (!input || !packed_out || !norms_out) return hipErrorInvalidValue;
+    const int64_t pd = ceil_div((int64_t)plan->head_dim * plan->bits, 8);
+    FlatDst dst{(uint8_t*)packed_out, (uint16_t*)norms_out, pd};
+    const TqPlanDev* p = plan->dev;
+    return launch_compress<0>(input, p->rot, p->cent, plan->n_levels, plan->bits, dst, nullptr,
+                              rows, plan->head_dim, fhip_host::as_stream(stream), p);
+}
+
+int fhip_launch_tq_compress_pages_planned(const fhip_tq_plan* plan, const void* input,
+                                          void* packed_pool, void* norms_pool,
+                                          int64_t page_packed_bytes, int64_t page_norm_bytes,
+                                          const int32_t* page_ids, int num_pages, int first_pos,
+                                          int num_tokens, int num_kv_heads,
+                                          fhip_stream_t stream) {
+    if (!plan || num_tokens < 0 || num_kv_heads <= 0 || first_pos < 0 || num_pages < 0)
+        return hipErrorInvalidValue;
+    const int64_t pd = ceil_div((int64_t)plan->head_dim * plan->bits, 8);
+    if (page_packed_bytes < (int64_t)FHIP_PAGE_TOKENS * num_kv_heads * pd ||
+        page_norm_bytes < (int64_t)FHIP_PAGE_TOKENS * num_kv_heads * 2)
+        return hipErrorInvalidValue;
+    const int64_t rows = (int64_t)num_tokens * num_kv_heads;
+    if (rows == 0) return hipSuccess;
+    if (!input || !packed_pool || !norms_pool || !page_ids) return hipErrorInvalidValue;
+    PageDst dst{(uint8_t*)packed_pool, (uint8_t*)norms_pool, page_packed_bytes, page_norm_bytes,
+                page_ids, first_pos, num_kv_heads, num_pages, pd};
+    const TqPlanDev* p = plan->dev;
+    return launch_compress<0>(input, p->rot, p->cent, plan->n_levels, plan->bits, dst, nullptr,
+                              rows, plan->head_dim, fhip_host::as_stream(stream), p);
+}
+
+int fhip_launch_tq_dequant_planned(const fhip_tq_plan* plan, const void* packed_in,
+                                   const void* norms_in, void* output, int num_tokens,
+                                   int num_kv_heads, fhip_stream_t stream) {
+    if (!plan || num_tokens < 0 || num_kv_heads < 0) return hipErrorInvalidValue;
+    const int64_t rows = (int64_t)num_tokens * num_kv_heads;
+    if (rows == 0) return hipSuccess;
+    if (!packed_in || !norms_in || !output) return hipErrorInvalidValue;
+    const int pd = (int)ceil_div((int64_t)plan->head_dim * plan->bits, 8);
+    const TqPlanDev* p = plan->dev;
+    return launch_dequant(packed_in, norms_in, p->rot, p->cent, plan->n_levels, output, rows,
+                          plan->head_dim, plan->bits, pd, fhip_host::as_stream(stream), p);
 }
 
 }  // extern "C"

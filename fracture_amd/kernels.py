@@ -250,6 +250,82 @@ def tq_compress_pages(x: torch.Tensor, rot: torch.Tensor, centroids: torch.Tenso
                                            first_pos, T, H, hd, _stream()), "tq_compress_pages")
 
 
+class TqPlan:
+    """fhip_tq_plan for one rotation [hd, hd] f32 and codebook (head_dim 128): the quantizer
+    tables and rotation fragments built once on the device (enqueued on the current
+    stream). Freed when the object is."""
+
+    def __init__(self, rot: torch.Tensor, centroids: torch.Tensor, bits: int):
+        _dev(rot, centroids)
+        hd = rot.shape[0]
+        L = centroids.numel()
+        _need(rot.dtype == torch.float32 and rot.shape == (hd, hd), "TqPlan: rotation")
+        _need(centroids.dtype == torch.float32 and 1 <= L <= (1 << bits), "TqPlan: centroids")
+        self._h = None
+        h = C.c_void_p()
+        _ok(_L().fhip_tq_plan_create(_p(rot), _p(centroids), L, bits, hd, _stream(),
+                                     C.byref(h)), "tq_plan_create")
+        self._h, self.head_dim, self.bits, self.n_levels = h, hd, bits, L
+        self.packed_dim = packed_dim(hd, bits)
+
+    def close(self) -> None:
+        """Free the plan's device memory (waits for the device to idle)."""
+        h, self._h = getattr(self, "_h", None), None
+        if h:
+            _lib.load().fhip_tq_plan_destroy(h)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown: the library binding may be gone already
+            pass
+
+
+def tq_compress_planned(plan: TqPlan, x: torch.Tensor, packed: torch.Tensor,
+                        norms: torch.Tensor) -> None:
+    """tq_compress with a plan: x [N, kvh, hd] fp16."""
+    _dev(x, packed, norms)
+    _need(x.dtype == torch.float16 and x.dim() == 3 and x.shape[2] == plan.head_dim,
+          "tq_compress_planned: x [N, kv_heads, hd] fp16")
+    N, H = x.shape[0], x.shape[1]
+    _need(packed.dtype == torch.uint8 and packed.numel() >= N * H * plan.packed_dim, "packed")
+    _need(norms.dtype == torch.float16 and norms.numel() >= N * H, "norms")
+    _ok(_L().fhip_launch_tq_compress_planned(plan._h, _p(x), _p(packed), _p(norms), N, H,
+                                             _stream()), "tq_compress_planned")
+
+
+def tq_compress_pages_planned(plan: TqPlan, x: torch.Tensor, packed_pool: torch.Tensor,
+                              norms_pool: torch.Tensor, page_ids: torch.Tensor,
+                              first_pos: int) -> None:
+    """tq_compress_pages with a plan (same page layout and arguments)."""
+    _dev(x, packed_pool, norms_pool, page_ids)
+    _need(x.dtype == torch.float16 and x.dim() == 3 and x.shape[2] == plan.head_dim,
+          "tq_compress_pages_planned: x [T, kvh, hd] fp16")
+    T, H, _ = x.shape
+    pd = plan.packed_dim
+    P = packed_pool.shape[0]
+    _need(packed_pool.dtype == torch.uint8 and packed_pool.shape[1:] == (16, H * pd), "packed_pool")
+    _need(norms_pool.dtype == torch.float16 and norms_pool.shape == (P, 16, H), "norms_pool")
+    _need(page_ids.dtype == torch.int32 and page_ids.numel() * 16 >= first_pos + T, "page_ids")
+    _ok(_L().fhip_launch_tq_compress_pages_planned(
+        plan._h, _p(x), _p(packed_pool), _p(norms_pool), packed_pool[0].nbytes if P else 16 * H * pd,
+        norms_pool[0].nbytes if P else 32 * H, _p(page_ids), P, first_pos, T, H, _stream()),
+        "tq_compress_pages_planned")
+
+
+def tq_dequant_planned(plan: TqPlan, packed: torch.Tensor, norms: torch.Tensor,
+                       out: torch.Tensor) -> None:
+    """tq_dequant with a plan: out [N, kvh, hd] fp16."""
+    _dev(packed, norms, out)
+    _need(out.dtype == torch.float16 and out.dim() == 3 and out.shape[2] == plan.head_dim,
+          "tq_dequant_planned: out [N, kvh, hd] fp16")
+    N, H = out.shape[0], out.shape[1]
+    _need(packed.dtype == torch.uint8 and packed.numel() >= N * H * plan.packed_dim, "packed")
+    _need(norms.dtype == torch.float16 and norms.numel() >= N * H, "norms")
+    _ok(_L().fhip_launch_tq_dequant_planned(plan._h, _p(packed), _p(norms), _p(out), N, H,
+                                            _stream()), "tq_dequant_planned")
+
+
 def attention_workspace(batch: int, qh: int, hd: int, max_blocks: int, device="cuda"):
     n = int(_L().fhip_attention_tq_workspace_bytes(batch, qh, hd, max_blocks))
     return torch.empty(max(n, 16), dtype=torch.uint8, device=device)

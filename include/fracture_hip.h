@@ -183,6 +183,31 @@ int fhip_launch_tq_dequant(const void* packed_in, const void* norms_in, const fl
                            int num_kv_heads, int head_dim, int bits, int packed_dim_per_head,
                            fhip_stream_t stream);
 
+/* TurboQuant plan: what compress and dequantize derive from one rotation and codebook (the
+ * per-layer TurboQuantConfig that QuantizedKvCacheManager uploads once,
+ * quantized_paged_kv_cache.rs:137-170), built once on the device in the layouts the kernels
+ * use: the nearest-centroid quantizer tables and the fp16 hi/lo rotation fragments. The
+ * planned launchers produce bytes identical to the unplanned ones for the same rotation and
+ * centroids, without rebuilding those per call. head_dim must be 128. create allocates the
+ * plan's device memory (about 210 KB) and enqueues its build on `stream`; the rotation and
+ * centroids may change after that build has run. destroy waits for the device to idle. */
+typedef struct fhip_tq_plan fhip_tq_plan;
+int fhip_tq_plan_create(const float* rotation, const float* centroids, int n_levels, int bits,
+                        int head_dim, fhip_stream_t stream, fhip_tq_plan** out);
+void fhip_tq_plan_destroy(fhip_tq_plan* plan);
+int fhip_launch_tq_compress_planned(const fhip_tq_plan* plan, const void* input,
+                                    void* packed_out, void* norms_out, int num_tokens,
+                                    int num_kv_heads, fhip_stream_t stream);
+int fhip_launch_tq_compress_pages_planned(const fhip_tq_plan* plan, const void* input,
+                                          void* packed_pool, void* norms_pool,
+                                          int64_t page_packed_bytes, int64_t page_norm_bytes,
+                                          const int32_t* page_ids, int num_pages, int first_pos,
+                                          int num_tokens, int num_kv_heads,
+                                          fhip_stream_t stream);
+int fhip_launch_tq_dequant_planned(const fhip_tq_plan* plan, const void* packed_in,
+                                   const void* norms_in, void* output, int num_tokens,
+                                   int num_kv_heads, fhip_stream_t stream);
+
 /* Batched decode attention over a TurboQuant page pool: one query token per sequence,
  * q [B, qh, hd] fp16, block_table [B, max_blocks] int32 (physical page ids), seq_lens [B]
  * int32; pages in contiguous pools (strides in bytes between pages); positions whose page

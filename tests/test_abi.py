@@ -102,6 +102,18 @@ def test_raw_launchers_reject_bad_arguments_on_host():
     assert lib.fhip_launch_turboquant_compress(None, None, None, None, None, 1, 1, 128, 32, 4, 64,
                                                None) == 1  # 32 levels > 2^4
     assert lib.fhip_launch_tq_quantize_pack(None, None, 16, 9, None, 1, 128, 144, None) == 1
+    # plans: head_dim 128 only, a valid codebook, an output handle; launchers need a plan
+    import ctypes
+
+    h = ctypes.c_void_p(1)
+    assert lib.fhip_tq_plan_create(1, 1, 16, 4, 64, None, ctypes.byref(h)) == 1
+    assert not h.value  # cleared on failure
+    assert lib.fhip_tq_plan_create(1, 1, 17, 4, 128, None, ctypes.byref(h)) == 1
+    assert lib.fhip_tq_plan_create(None, 1, 16, 4, 128, None, ctypes.byref(h)) == 1
+    assert lib.fhip_tq_plan_create(1, 1, 16, 4, 128, None, None) == 1
+    assert lib.fhip_launch_tq_compress_planned(None, 1, 1, 1, 4, 8, None) == 1
+    assert lib.fhip_launch_tq_dequant_planned(None, 1, 1, 1, 4, 8, None) == 1
+    lib.fhip_tq_plan_destroy(None)  # no-op
     # zero-size work is a no-op success
     assert lib.fhip_launch_add(None, None, None, 0, None) == 0
     assert lib.fhip_rows_workspace_bytes(64, 128256) == 64 * 32 * 32

@@ -262,3 +262,96 @@ def test_page_writer_equals_flat_compress(dev, first_pos):
         assert np.array_equal(KP[page, slot], flat_p[t])
         assert np.array_equal(KN[page, slot].view(np.uint16), flat_n[t].view(np.uint16))
     assert (KP[~written] == 0xAB).all() and (KN[~written] == 7.0).all()
+
+
+# ---------------------------------------------------------------------------------------
+# Plans: the planned launchers are byte-identical to the unplanned ones.
+# ---------------------------------------------------------------------------------------
+def _codebook(kind, bits, rng):
+    cent = tq.codebook(128, bits)[0].copy()
+    if kind == "shuffled":  # not sorted: the bucket map refuses it, the general path runs
+        rng.shuffle(cent)
+    elif kind == "short":
+        cent = cent[: max(2, (1 << bits) - 5)]
+    return cent
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
+@pytest.mark.parametrize("kind", ["lloyd_max", "shuffled", "short"])
+def test_planned_compress_equals_unplanned(dev, bits, kind):
+    rng = np.random.default_rng(bits * 7 + len(kind))
+    x = kv(rng, 301, 8, 128)  # a ragged last tile
+    rot = tq.rotation_matrix(128, 11)
+    cent = _codebook(kind, bits, rng)
+    want_p, want_n = compress(x, rot, cent, bits, dev)
+    tr, tc = dev_t(rot, dev), dev_t(cent, dev)
+    plan = K.TqPlan(tr, tc, bits)
+    packed = torch.empty((301, 8 * K.packed_dim(128, bits)), dtype=torch.uint8, device=dev)
+    norms = torch.empty((301, 8), dtype=torch.float16, device=dev)
+    K.tq_compress_planned(plan, dev_t(x, dev), packed, norms)
+    torch.cuda.synchronize()
+    assert np.array_equal(packed.cpu().numpy(), want_p)
+    assert np.array_equal(norms.cpu().numpy().view(np.uint16), want_n.view(np.uint16))
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
+def test_planned_dequant_equals_unplanned(dev, bits):
+    rng = np.random.default_rng(bits)
+    x = kv(rng, 200, 8, 128)
+    rot = tq.rotation_matrix(128, 5)
+    cent = tq.codebook(128, bits)[0]
+    packed, norms = compress(x, rot, cent, bits, dev)
+    tp, tn, tr, tc = dev_t(packed, dev), dev_t(norms, dev), dev_t(rot, dev), dev_t(cent, dev)
+    want = torch.empty((200, 8, 128), dtype=torch.float16, device=dev)
+    K.tq_dequant(tp, tn, tr, tc, bits, want)
+    plan = K.TqPlan(tr, tc, bits)
+    got = torch.empty_like(want)
+    K.tq_dequant_planned(plan, tp, tn, got)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def test_plan_outlives_its_sources(dev):
+    """A plan keeps its own copy: overwriting the rotation and centroids after the build,
+    and compressing several inputs with one plan, still match the unplanned results."""
+    rng = np.random.default_rng(3)
+    bits = 4
+    rot = tq.rotation_matrix(128, 99)
+    cent = tq.codebook(128, bits)[0]
+    tr, tc = dev_t(rot, dev), dev_t(cent, dev)
+    plan = K.TqPlan(tr, tc, bits)
+    torch.cuda.synchronize()
+    tr.zero_()
+    tc.fill_(1.0)
+    for n in (64, 33, 1000):
+        x = kv(rng, n, 8, 128)
+        want_p, want_n = compress(x, rot, cent, bits, dev)
+        packed = torch.empty((n, 8 * 64), dtype=torch.uint8, device=dev)
+        norms = torch.empty((n, 8), dtype=torch.float16, device=dev)
+        K.tq_compress_planned(plan, dev_t(x, dev), packed, norms)
+        torch.cuda.synchronize()
+        assert np.array_equal(packed.cpu().numpy(), want_p)
+        assert np.array_equal(norms.cpu().numpy().view(np.uint16), want_n.view(np.uint16))
+
+
+def test_planned_page_writer_equals_unplanned(dev):
+    rng = np.random.default_rng(8)
+    T, H, hd, bits, first_pos = 70, 8, 128, 4, 5
+    pd = K.packed_dim(hd, bits)
+    x = kv(rng, T, H, hd)
+    rot = tq.rotation_matrix(hd, 42)
+    cent = tq.codebook(hd, bits)[0]
+    npages = 12
+    page_ids = rng.permutation(npages)[:(first_pos + T + 15) // 16].astype(np.int32)
+    tx, tr, tc, tpg = dev_t(x, dev), dev_t(rot, dev), dev_t(cent, dev), dev_t(page_ids, dev)
+    pools = []
+    for planned in (False, True):
+        kp = torch.full((npages, 16, H * pd), 0xAB, dtype=torch.uint8, device=dev)
+        kn = torch.full((npages, 16, H), 7.0, dtype=torch.float16, device=dev)
+        if planned:
+            K.tq_compress_pages_planned(K.TqPlan(tr, tc, bits), tx, kp, kn, tpg, first_pos)
+        else:
+            K.tq_compress_pages(tx, tr, tc, bits, kp, kn, tpg, first_pos)
+        torch.cuda.synchronize()
+        pools.append((kp.cpu().numpy(), kn.cpu().numpy().view(np.uint16)))
+    assert np.array_equal(pools[0][0], pools[1][0]) and np.array_equal(pools[0][1], pools[1][1])
