@@ -4,7 +4,8 @@ Default workload (the metric's configuration): one Llama-3.1-8B decode step's el
 chain at batch 64, fp16 — embedding gather from a [128256, 4096] table, RoPE on
 Q [64, 32, 128] and K [64, 8, 128] (theta 500000, positions in [0, 8192)), SwiGLU on
 [64, 14336], and two residual adds fused with RMSNorm on [64, 4096] — with inputs resident
-in HBM. A step is the five launches, replayed from a HIP graph (eager timing reported too).
+in HBM. A step is the five launches; 20 consecutive steps are captured in one HIP graph
+(`--steps-per-graph`) and replayed (eager timing reported too).
 
 Printed: one JSON line with the metric (whole-chain algorithmic GB/s; ms_per_step), per-kernel
 microseconds and GB/s, the roofline object for the dominant kernel (SwiGLU) and the CPU
@@ -52,6 +53,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true", help="time the chain without a HIP graph")
+    ap.add_argument("--steps-per-graph", type=int, default=20,
+                    help="decode-chain steps captured in one HIP graph (1: one graph per step)")
     return ap.parse_args()
 
 
@@ -224,7 +227,12 @@ def run_decode(args, torch, K, dev):
     timer = Timer(torch)
     torch.cuda.synchronize()
 
-    graph = None
+    # A graph holds `per_graph` consecutive steps, as a serving loop captures a whole decode
+    # step (every layer's kernels) in one graph: the per-launch cost of a graph is then shared
+    # by many kernels instead of landing on five. The timed region is exactly args.steps
+    # steps: full graphs, then one graph of the remaining steps.
+    per_graph = max(1, min(args.steps_per_graph, args.steps))
+    graphs = {}
     if not args.eager:
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
@@ -232,25 +240,32 @@ def run_decode(args, torch, K, dev):
             for _ in range(3):
                 decode_step(ops)  # warm the launch path on the capture stream
         torch.cuda.current_stream().wait_stream(s)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            decode_step(ops)
+        for n in {per_graph, args.steps % per_graph} - {0}:
+            graphs[n] = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graphs[n]):
+                for _ in range(n):
+                    decode_step(ops)
         torch.cuda.synchronize()
 
-    def step():
-        if graph is not None:
-            graph.replay()
-        else:
-            decode_step(ops)
+    def run_steps(n):
+        if args.eager:
+            for _ in range(n):
+                decode_step(ops)
+            return
+        for _ in range(n // per_graph):
+            graphs[per_graph].replay()
+        if n % per_graph:
+            graphs[n % per_graph].replay()
 
-    for _ in range(args.warmup):
-        step()
+    for _ in range(args.warmup):  # untimed: the warmup steps, then each graph once
+        decode_step(ops)
+    for g_ in graphs.values():
+        g_.replay()
     torch.cuda.synchronize()
     s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     s_ev.record()
-    for _ in range(args.steps):
-        step()
+    run_steps(args.steps)
     e_ev.record()
     torch.cuda.synchronize()
     us_step = s_ev.elapsed_time(e_ev) * 1e3 / args.steps
@@ -290,7 +305,7 @@ def run_decode(args, torch, K, dev):
         "config": {"workload": "llama3.1-8b decode-step elementwise chain, batch 64, fp16",
                    "batch": 64, "hidden": 4096, "vocab": 128256, "q_heads": 32,
                    "kv_heads": 8, "head_dim": 128, "ffn": 14336, "rope_theta": 500000.0,
-                   "launch": "hip graph" if graph is not None else "eager",
+                   "launch": "eager" if args.eager else f"hip graph, {per_graph} steps per graph",
                    "chain_bytes": chain_bytes},
         "eager_us_per_step": round(eager_us, 3),
         "kernels": per,

@@ -354,41 +354,114 @@ __global__ __launch_bounds__(256) void tq_attn_split_kernel(
     }
 }
 
-// 3. Merge the splits of one (query, q head) and unrotate: out = fp16(Pi_v^T (acc / l)).
+// Merge the splits of kCombHeads consecutive (query, head) vectors per workgroup and apply
+// Pi_v^T: out = Pi_v^T (sum_s w_s acc_s) / (sum_s w_s l_s), w_s = exp(m_s - max m). The work
+// is a few dependent memory round trips, so each phase issues its loads together:
+//   the rotation (hd x hd fp32) is staged in LDS first, overlapping the rest;
+//   phase 1: a half-wave per vector loads its splits' (m, l) once and folds them into
+//            weights (LDS) and 1 / L;
+//   phase 2: the weighted split sums, four (vector, coordinate) items per thread, sixteen
+//            splits per step, each item summed in split order;
+//   phase 3: the matvec from LDS, one output coordinate for 4 vectors per thread and step.
+// Dynamic LDS: hd * hd rotation floats, then kCombHeads * nsplit weights.
+constexpr int kCombHeads = 8;
 __global__ __launch_bounds__(256) void tq_attn_combine_kernel(
     Queries qs, const float* __restrict__ part_ml, const float* __restrict__ part_acc,
-    const float* __restrict__ vrot, uint16_t* __restrict__ out, int qh, int hd, int nsplit) {
-    __shared__ float o[kMaxHd];
-    __shared__ float wts[kSplit];  // per split weights (nsplit <= kSplit)
-    __shared__ float Lsum;
-    const int64_t head = blockIdx.x;  // qi * qh + h
-    const int qi = (int)(head / qh);
-    const int clen = qs.causal_len(qi);
-    const int ns = (clen + kSplit - 1) / kSplit;
-    if (threadIdx.x == 0) {
-        float M = -__builtin_inff();
-        for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, part_ml[(head * nsplit + sp) * 2]);
-        float L = 0.0f;
-        for (int sp = 0; sp < ns; ++sp) {
-            const float m = part_ml[(head * nsplit + sp) * 2];
-            const float wgt = (m == -__builtin_inff()) ? 0.0f : expf(m - M);
-            wts[sp] = wgt;
-            L += part_ml[(head * nsplit + sp) * 2 + 1] * wgt;
+    const float* __restrict__ vrot, uint16_t* __restrict__ out, int qh, int hd, int nsplit,
+    int64_t nvec) {
+    __shared__ float o[kCombHeads][kMaxHd];
+    __shared__ float linv[kCombHeads];
+    __shared__ int nsv[kCombHeads];
+    extern __shared__ uint32_t dyn[];
+    float* rl = (float*)dyn;              // [hd][hd]
+    float* wts = (float*)dyn + hd * hd;   // [kCombHeads][nsplit]
+    const int tid = threadIdx.x;
+    const int64_t h0 = (int64_t)blockIdx.x * kCombHeads;
+    {   // the rotation into LDS: hd * hd / 4 16-byte chunks, all loads first (hd % 8 == 0)
+        const int n16 = hd * hd / 4;
+        for (int c0 = tid; c0 < n16; c0 += 16 * 256) {
+            u32x4 v[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) v[u] = ld16(vrot + 4 * min(c0 + u * 256, n16 - 1));
+#pragma unroll
+            for (int u = 0; u < 16; ++u) *(u32x4*)&rl[4 * min(c0 + u * 256, n16 - 1)] = v[u];
         }
-        Lsum = L;
+    }
+    {
+        const int hh = tid >> 5, l32 = tid & 31;
+        const int64_t head = h0 + hh;
+        int ns = 0;
+        if (head < nvec) {
+            const int clen = qs.causal_len((int)(head / qh));
+            ns = (clen + kSplit - 1) / kSplit;
+        }
+        const float* ml = part_ml + head * nsplit * 2;
+        float M = -__builtin_inff();
+        for (int sp = l32; sp < ns; sp += 32) M = fmaxf(M, ml[2 * sp]);
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+        float L = 0.0f;
+        for (int sp = l32; sp < ns; sp += 32) {
+            const float m = ml[2 * sp];
+            const float w = (m == -__builtin_inff()) ? 0.0f : expf(m - M);
+            wts[hh * nsplit + sp] = w;
+            L += ml[2 * sp + 1] * w;
+        }
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) L += __shfl_xor(L, off);
+        if (l32 == 0) {
+            linv[hh] = L > 0.0f ? 1.0f / L : 0.0f;
+            nsv[hh] = ns;
+        }
     }
     __syncthreads();
-    const float inv = Lsum > 0.0f ? 1.0f / Lsum : 0.0f;
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-        float a = 0.0f;
-        for (int sp = 0; sp < ns; ++sp) a += part_acc[(head * nsplit + sp) * hd + d] * wts[sp];
-        o[d] = a * inv;
+    for (int idx0 = tid; idx0 < kCombHeads * hd; idx0 += 4 * 256) {
+        const float* a[4];
+        int hh[4], ns[4];
+        float sum[4];
+        int nsmax = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int idx = min(idx0 + k * 256, kCombHeads * hd - 1);
+            hh[k] = idx / hd;
+            const int d = idx - hh[k] * hd;
+            ns[k] = idx0 + k * 256 < kCombHeads * hd ? nsv[hh[k]] : 0;
+            nsmax = max(nsmax, ns[k]);
+            // vectors past nvec (last workgroup) read vector 0's row: in bounds, unused
+            a[k] = part_acc + (h0 + hh[k] < nvec ? (h0 + hh[k]) * nsplit * hd : 0) + d;
+            sum[k] = 0.0f;
+        }
+        for (int sp = 0; sp < nsmax; sp += 16) {
+            float v[4][16];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+#pragma unroll
+                for (int u = 0; u < 16; ++u)  // clamped: every load is in bounds, unused ones ignored
+                    v[k][u] = a[k][(int64_t)min(sp + u, max(ns[k] - 1, 0)) * hd];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+#pragma unroll
+                for (int u = 0; u < 16; ++u)
+                    if (sp + u < ns[k]) sum[k] = fmaf(v[k][u], wts[hh[k] * nsplit + sp + u], sum[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (idx0 + k * 256 < kCombHeads * hd) o[hh[k]][idx0 + k * 256 - hh[k] * hd] = sum[k] * linv[hh[k]];
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < hd; i += blockDim.x) {
-        float dot = 0.0f;
-        for (int j = 0; j < hd; ++j) dot += vrot[(int64_t)j * hd + i] * o[j];
-        out[head * hd + i] = (uint16_t)f2h(dot);
+    for (int idx = tid; idx < 2 * hd; idx += 256) {
+        const int hg = idx / hd, i = idx - hg * hd;
+        float dot[kCombHeads / 2] = {};
+        for (int j = 0; j < hd; ++j) {
+            const float v = rl[j * hd + i];
+#pragma unroll
+            for (int k = 0; k < kCombHeads / 2; ++k) dot[k] += v * o[hg + 2 * k][j];
+        }
+#pragma unroll
+        for (int k = 0; k < kCombHeads / 2; ++k) {
+            const int64_t head = h0 + hg + 2 * k;
+            if (head < nvec) out[head * hd + i] = (uint16_t)f2h(dot[k]);
+        }
     }
 }
 
@@ -949,8 +1022,10 @@ int launch_attention(const AttnArgs& a, const Pages& pg, hipStream_t s) {
         launch_split<4, 2>(a, pg, nsplit, ml, acc, s);
     else
         launch_split<0, 0>(a, pg, nsplit, ml, acc, s);
-    hipLaunchKernelGGL(tq_attn_combine_kernel, dim3(nvec), dim3(128), 0, s, a.qs, ml, acc,
-                       a.vrot, (uint16_t*)a.out, a.qh, a.hd, nsplit);
+    hipLaunchKernelGGL(tq_attn_combine_kernel, dim3((unsigned)ceil_div(nvec, kCombHeads)),
+                       dim3(256), ((size_t)a.hd * a.hd + (size_t)kCombHeads * nsplit) * sizeof(float),
+                       s, a.qs, ml, acc,
+                       a.vrot, (uint16_t*)a.out, a.qh, a.hd, nsplit, (int64_t)nvec);
     return hipGetLastError();
 }
 
