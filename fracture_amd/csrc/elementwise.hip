@@ -142,41 +142,54 @@ __global__ __launch_bounds__(1024) void rmsnorm_vec_kernel(void* __restrict__ ou
     char* hres = (char*)resid + rowoff;
     char* yout = (char*)out + rowoff;
 
+    // Every load (row, residual, weight) goes out at once with clamped indices (lanes past
+    // the row end reload its last vector and store nothing): a guarded load, or the weight
+    // loaded after the reduction, would each add a memory round trip to this short kernel.
     float x[kVpt][V];
-    u32x4 raw[kVpt], rres[kVpt];
+    u32x4 raw[kVpt], rres[kVpt], wraw[kVpt];
 #pragma unroll
     for (int k = 0; k < kVpt; ++k) {
-        const int vi = k * bs + threadIdx.x;
-        if (vi < nvec) {
-            raw[k] = ld16(xin + (int64_t)vi * 16);
-            if constexpr (kResid) rres[k] = ld16(hres + (int64_t)vi * 16);
-        }
+        const int64_t vc = min(k * bs + (int)threadIdx.x, nvec - 1);
+        raw[k] = ld16(xin + vc * 16);
+        if constexpr (kResid) rres[k] = ld16(hres + vc * 16);
+        wraw[k] = ld16((const char*)weight + vc * 16);
     }
+    __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the first use
     float ss = 0.0f;
 #pragma unroll
     for (int k = 0; k < kVpt; ++k) {
         const int vi = k * bs + threadIdx.x;
-        if (vi < nvec) {
-            unpack16<Tr>(raw[k], x[k]);
-            if constexpr (kResid) {
-                float h[V];
-                unpack16<Tr>(rres[k], h);
+        unpack16<Tr>(raw[k], x[k]);
+        if constexpr (kResid) {
+            float h[V];
+            unpack16<Tr>(rres[k], h);
 #pragma unroll
-                for (int i = 0; i < V; ++i) x[k][i] = round_to<Tr>(h[i] + x[k][i]);
-                st16(hres + (int64_t)vi * 16, pack16<Tr>(x[k]));
-            }
+            for (int i = 0; i < V; ++i) x[k][i] = round_to<Tr>(h[i] + x[k][i]);
+            if (vi < nvec) st16(hres + (int64_t)vi * 16, pack16<Tr>(x[k]));
+        }
+        if (vi < nvec) {
 #pragma unroll
             for (int i = 0; i < V; ++i) ss += x[k][i] * x[k][i];
         }
     }
-    ss = block_sum(ss, red);
+    // workgroup sum (waves in order) behind an LDS-only barrier: __syncthreads would also
+    // wait for the residual stores above
+    {
+        const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+        ss = wave_sum(ss);
+        if (lane == 0) red[wave] = ss;
+        lds_barrier();
+        float t = 0.0f;
+        for (int w = 0; w < (bs + kWave - 1) / kWave; ++w) t += red[w];
+        ss = t;
+    }
     const float inv = 1.0f / sqrtf(ss / (float)cols + eps);
 #pragma unroll
     for (int k = 0; k < kVpt; ++k) {
         const int vi = k * bs + threadIdx.x;
         if (vi < nvec) {
             float w[V];
-            unpack16<Tr>(ld16((const char*)weight + (int64_t)vi * 16), w);
+            unpack16<Tr>(wraw[k], w);
 #pragma unroll
             for (int i = 0; i < V; ++i) x[k][i] = x[k][i] * inv * w[i];
             st16(yout + (int64_t)vi * 16, pack16<Tr>(x[k]));
@@ -225,29 +238,43 @@ __global__ __launch_bounds__(256) void rope_kernel(void* __restrict__ q, void* _
     extern __shared__ float cs[];  // [hd/2][2] = (cos, sin)
     const int t = blockIdx.x;
     const int half = hd / 2;
+    const int tid = threadIdx.x;
+    // The position and this lane's first frequency are loaded before any row: loads return
+    // in order, so waiting for them after the row prefetch would also wait for the rows.
     const float p = (float)positions[t];
-    for (int d = threadIdx.x; d < half; d += blockDim.x) {
-        float s, c;
-        sincosf(p * freq[d], &s, &c);
-        cs[2 * d] = c;
-        cs[2 * d + 1] = s;
-    }
-    __syncthreads();
+    const float fr0 = freq[min(tid, half - 1)];
+    auto angles = [&]() {
+        if (tid < half) {
+            float s, c;
+            sincosf(p * fr0, &s, &c);
+            cs[2 * tid] = c;
+            cs[2 * tid + 1] = s;
+        }
+        for (int d = tid + blockDim.x; d < half; d += blockDim.x) {
+            float s, c;
+            sincosf(p * freq[d], &s, &c);
+            cs[2 * d] = c;
+            cs[2 * d + 1] = s;
+        }
+    };
     using S = typename Tr::S;
     if constexpr (kVecPath) {
         constexpr int V = Tr::kVec;
         const int chunks = half / V;
         const int items = (qh + kvh) * chunks;
-        for (int it = threadIdx.x; it < items; it += blockDim.x) {
+        auto item_row = [&](int it) -> S* {
             const int head = it / chunks;
             const int ch = it - head * chunks;
             S* row = head < qh ? (S*)q + ((int64_t)t * qh + head) * hd
                                : (S*)k + ((int64_t)t * kvh + (head - qh)) * hd;
-            S* p0 = row + ch * V;
-            S* p1 = p0 + half;
+            return row + ch * V;
+        };
+        auto rotate = [&](int it, u32x4 r0, u32x4 r1) {
+            const int ch = it % chunks;
+            S* p0 = item_row(it);
             float x0[V], x1[V];
-            unpack16<Tr>(ld16(p0), x0);
-            unpack16<Tr>(ld16(p1), x1);
+            unpack16<Tr>(r0, x0);
+            unpack16<Tr>(r1, x1);
 #pragma unroll
             for (int e = 0; e < V; ++e) {
                 const int d = ch * V + e;
@@ -257,9 +284,33 @@ __global__ __launch_bounds__(256) void rope_kernel(void* __restrict__ q, void* _
                 x1[e] = a * s + b * c;
             }
             st16(p0, pack16<Tr>(x0));
-            st16(p1, pack16<Tr>(x1));
+            st16(p0 + half, pack16<Tr>(x1));
+        };
+        // The lane's first kPre items are read while the angles are computed. A lane with
+        // fewer items reloads item 0 in place of the missing ones and stores nothing there.
+        constexpr int kPre = 2;
+        u32x4 pre0[kPre], pre1[kPre];
+#pragma unroll
+        for (int j = 0; j < kPre; ++j) {
+            const int it = tid + j * (int)blockDim.x;
+            const S* p0 = item_row(it < items ? it : 0);
+            pre0[j] = ld16(p0);
+            pre1[j] = ld16(p0 + half);
+        }
+        angles();
+        lds_barrier();
+#pragma unroll
+        for (int j = 0; j < kPre; ++j) {
+            const int it = tid + j * (int)blockDim.x;
+            if (it < items) rotate(it, pre0[j], pre1[j]);
+        }
+        for (int it = tid + kPre * (int)blockDim.x; it < items; it += blockDim.x) {
+            const S* p0 = item_row(it);
+            rotate(it, ld16(p0), ld16(p0 + half));
         }
     } else {
+        angles();
+        __syncthreads();
         const int items = (qh + kvh) * half;
         for (int it = threadIdx.x; it < items; it += blockDim.x) {
             const int head = it / half;
@@ -380,7 +431,7 @@ int launch_rms_t(void* out, void* resid, const void* in, const void* w, float ep
 template <class Tr>
 int launch_rope_t(void* q, void* k, const uint32_t* pos, const float* freq, int T, int qh, int kvh,
                   int hd, hipStream_t s) {
-    if (T == 0) return hipSuccess;
+    if (T == 0 || qh + kvh == 0) return hipSuccess;
     const int half = hd / 2;
     const size_t lds = (size_t)half * 2 * sizeof(float);
     const bool vec_ok = half % Tr::kVec == 0 && fhip_host::aligned16(q) &&
