@@ -15,6 +15,7 @@ Other workloads (parity-tested configurations, printed as their own JSON lines):
   --workload prefill      add+RMSNorm [8192,4096], SwiGLU [8192,14336], softmax/argmax [64,128256]
   --workload tq           TurboQuant compress + dequantize of K and V [32768, 8, 128], 4 and 3 bit
   --workload attention    decode attention over a K4/V4 page pool, B=64, 32/8 heads, ctx U[1024,32768]
+  --workload paged        the same decode attention over an FP16 page pool (attention_paged.cu)
 
 HBM traffic (the roofline's "traffic" field, from profiles/traffic.json):
   rocprofv3 --pmc FETCH_SIZE -d <F> -o pmc -- python3 bench.py --workload pmc
@@ -46,7 +47,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "prefill", "tq", "attention", "all", "pmc"])
+                    choices=["decode", "prefill", "tq", "attention", "paged", "all", "pmc"])
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn two rocprofv3 --pmc runs of --workload pmc into "
                          "profiles/traffic.json")
@@ -434,6 +435,50 @@ def run_attention(args, torch, K, dev):
                 "traffic": traffic_of("attention_tq_decode")}}}
 
 
+def paged_inputs(torch, K, dev):
+    """FP16 paged decode attention at the same batch, heads and lengths as the TurboQuant
+    workload: returns (fn, algorithmic bytes, context tokens, mean)."""
+    import numpy as np
+
+    B, QH, KVH, HD = (ATT_SHAPE[k] for k in ("B", "QH", "KVH", "HD"))
+    lens = attention_lens()
+    rng = np.random.default_rng(5)
+    rng.integers(1024, 32769, B)
+    nbs = (lens + 15) // 16
+    P = int(nbs.sum())
+    maxb = int(nbs.max())
+    perm = rng.permutation(P).astype(np.int32)
+    table = np.zeros((B, maxb), np.int32)
+    at = 0
+    for b in range(B):
+        table[b, :nbs[b]] = perm[at:at + nbs[b]]
+        at += nbs[b]
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    kp = torch.randn((P, 16, KVH, HD), generator=g, device=dev, dtype=torch.float16)
+    vp = torch.randn((P, 16, KVH, HD), generator=g, device=dev, dtype=torch.float16)
+    q = torch.randn((B, QH, HD), generator=g, device=dev, dtype=torch.float16)
+    out = torch.empty_like(q)
+    tb = torch.from_numpy(table).to(dev)
+    sl = torch.from_numpy(lens).to(dev)
+    ws = K.attention_paged_workspace(B, QH, HD, maxb, dev)
+    fn = lambda: K.attention_paged_decode(out, q, tb, sl, kp, vp, KVH, ws)
+    tok = int(lens.sum())
+    nb = tok * KVH * HD * 2 * 2 + 2 * B * QH * HD * 2 + B * maxb * 4
+    return fn, nb, tok, float(lens.mean())
+
+
+def run_paged(args, torch, K, dev):
+    fn, nb, tok, mean = paged_inputs(torch, K, dev)
+    us = Timer(torch).time_us(fn, 10, warmup=2)
+    return {"workload": "FP16 paged decode attention, B=64, 32/8 heads, hd 128",
+            "kernels": {"attention_paged_decode": {
+                "us": round(us, 1), "GB/s": round(gbs(nb, us), 1),
+                "frac_of_peak": round(gbs(nb, us) / PEAK_HBM_GBS, 4), "bytes": nb,
+                "context_tokens": tok, "mean_ctx": mean,
+                "traffic": traffic_of("attention_paged_decode")}}}
+
+
 # ---------------------------------------------------------------------------------------
 # HBM traffic from rocprofv3 PMC counters
 # ---------------------------------------------------------------------------------------
@@ -665,6 +710,8 @@ def main():
         print(json.dumps(run_tq(args, torch, K, dev)), flush=True)
     if wl in ("attention", "all"):
         print(json.dumps(run_attention(args, torch, K, dev)), flush=True)
+    if wl in ("paged", "all"):
+        print(json.dumps(run_paged(args, torch, K, dev)), flush=True)
     if wl == "pmc":
         print(json.dumps(run_pmc(torch, K, dev)), flush=True)
 

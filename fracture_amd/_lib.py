@@ -45,6 +45,7 @@ SIGNATURES = {
     "fhip_launch_turboquant_decompress": (I, [P, P, P, P, P, I, I, I, I, I, P]),
     "fhip_launch_attention_paged_tq": (I, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I,
                                            I, I, I, I, P]),
+    "fhip_launch_paged_attention": (I, [P, P, P, P, P, I, I, I, I, I, I, I, P]),
     # additive raw launchers
     "fhip_launch_rmsnorm_ex": (I, [P, P, P, F, I, I, I, P]),
     "fhip_launch_add_ex": (I, [P, P, P, I64, I, P]),
@@ -68,6 +69,9 @@ SIGNATURES = {
     "fhip_attention_tq_workspace_bytes": (SZ, [I, I, I, I]),
     "fhip_launch_attention_tq_decode": (I, [P, P, P, P, I, I, I, P, P, P, P, I64, I64, I64, I64,
                                             P, P, P, P, I, I, I, I, I, P, P]),
+    "fhip_attention_paged_workspace_bytes": (SZ, [I, I, I, I]),
+    "fhip_launch_attention_paged_decode": (I, [P, P, P, P, I, I, I, P, P, I64, I64, I, I, I, P,
+                                               P]),
     # handle runtime (Backend trait mirror)
     "fhip_last_error": (C.c_char_p, []),
     "fhip_backend_create": (I, [I, C.POINTER(P)]),

@@ -37,6 +37,7 @@ PER_FILE = {
     "tq_host.cpp": ["-ffp-contract=off"],
 }
 SOURCES = ["elementwise.hip", "reduce.hip", "turboquant.hip", "attention_tq.hip",
+           "attention_paged.hip",
            "tq_host.cpp", "runtime.cpp"]
 
 _NOISE = "'-packed-fp32-ops' is not a recognized feature for this target"

@@ -1,0 +1,462 @@
+// GQA decode / prefill attention over an FP16 paged KV cache, for gfx950.
+//
+// Semantics follow attention_paged.cu:36-170: query token i of a sequence attends to
+// positions 0 .. min(start_pos + i + 1, kv_len) - 1 (or seq_lens[i] in the batched form);
+// position t lives in page block_table[t / 16], row (t % 16), as a [16][kv_heads][head_dim]
+// fp16 block; score = dot(q, k) / sqrt(head_dim) with fp32 accumulation, softmax in fp32,
+// out = half(sum_t p_t v_t). The reference keeps a kv_len-float score row in shared memory
+// (attention_paged.cu:58-59, 176); here the context is split into 1024-position pieces with an
+// online softmax each, merged by a second kernel, so kv_len is bounded only by the block table.
+//
+// Work split: one wave per (query, kv head, block of up to 8 of its q heads, split). Each K
+// row crosses HBM once per (query, kv head) for up to 8 q heads. Per 32-position chunk
+// (16 when head_dim is 256):
+//   QK on v_mfma_f32_16x16x32_f16: A = K rows (row = position, 8 consecutive dims per lane,
+//      exactly their memory layout), B = Q^T (column = q head): fp16 x fp16 products are
+//      exact in fp32, the sums are fp32;
+//   online softmax per head in log2 units, weights to LDS;
+//   PV on the VALU in fp32: lane (dim group of 8, position subset) loads 16 bytes of a V row
+//      and accumulates p_h * v for the wave's heads. V needs no transpose this way, and the
+//      fp32 weights need no fp16 rounding.
+// The kernel streams 4 * head_dim bytes per (position, kv head) and is bound by HBM.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fhip_common.h"
+#include "fracture_hip.h"
+
+using namespace fhip;
+
+namespace {
+
+constexpr int kPSplit = 1024;  // positions per split: 64 pages, one per lane of the page cache
+constexpr int kPWaves = 4;     // waves per workgroup (independent work items)
+constexpr int kHeadsMax = 8;   // q heads per wave
+
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+// Page sources: per-block pointer arrays (the reference's interface) or contiguous pools.
+struct F16PtrPages {
+    const uint8_t* const* k;
+    const uint8_t* const* v;
+    int num_pages;
+    __device__ bool valid(int p) const { return p >= 0 && p < num_pages; }
+    // Wave-wide page cache: lane j holds the pointers of page j of the current split; the
+    // `_at` accessors read them back from lane j.
+    struct Lane {
+        const uint8_t *k, *v;
+    };
+    __device__ Lane lane_load(int p) const {
+        if (!valid(p)) return Lane{nullptr, nullptr};
+        return Lane{k[p], v[p]};
+    }
+    static __device__ const uint8_t* rl(const uint8_t* x, int j) {
+        const uint64_t u = (uint64_t)x;
+        const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)u, j);
+        const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), j);
+        return (const uint8_t*)(((uint64_t)hi << 32) | lo);
+    }
+    __device__ const uint8_t* k_at(const Lane& l, int j, int) const { return rl(l.k, j); }
+    __device__ const uint8_t* v_at(const Lane& l, int j, int) const { return rl(l.v, j); }
+};
+struct F16PoolPages {
+    const uint8_t* k;
+    const uint8_t* v;
+    int64_t sk, sv;  // bytes between pages
+    int num_pages;
+    __device__ bool valid(int p) const { return p >= 0 && p < num_pages; }
+    struct Lane {};
+    __device__ Lane lane_load(int) const { return Lane{}; }
+    __device__ const uint8_t* k_at(const Lane&, int, int p) const { return k + p * sk; }
+    __device__ const uint8_t* v_at(const Lane&, int, int p) const { return v + p * sv; }
+};
+
+// Query i reads block-table row i (stride 0: one shared table) and attends to seq_lens[i]
+// positions, or min(start_pos + i + 1, kv_len) when seq_lens is null; never more than the
+// table holds.
+struct PQueries {
+    const int32_t* table;
+    int64_t table_stride;
+    int max_blocks;
+    const int32_t* seq_lens;
+    int kv_len, start_pos;
+    int count;
+    __device__ int causal_len(int qi) const {
+        int c;
+        if (seq_lens) {
+            c = seq_lens[qi];
+        } else {
+            c = start_pos + qi + 1;
+            if (c > kv_len) c = kv_len;
+        }
+        const int cap = max_blocks * FHIP_PAGE_TOKENS;
+        if (c > cap) c = cap;
+        return c < 0 ? 0 : c;
+    }
+};
+
+// Split partials: per (query, q head, split) the running max m (natural log units), the sum
+// l and the unnormalised accumulator acc[hd]. Splits at or past the causal length are not
+// written; the combine kernel reads only the splits below it.
+template <int HD, int NH, class Pages>
+__global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2))) void
+paged_attn_split_kernel(const uint16_t* __restrict__ q, PQueries qs, Pages pg, int qh, int kvh,
+                        int nhb, float scale_log2, float* __restrict__ part_ml,
+                        float* __restrict__ part_acc, int nsplit) {
+    constexpr int kChunk = HD <= 128 ? 32 : 16;  // positions per chunk
+    constexpr int kTiles = kChunk / 16;          // 16-position MFMA tiles (= pages) per chunk
+    constexpr int kSteps = HD / 32;              // MFMA steps per tile
+    constexpr int kDg = HD / 8;                  // lanes per V row, 8 dims each
+    constexpr int kPpl = 64 / kDg;               // positions per V load
+    constexpr int kVLoads = kChunk / kPpl;
+    static_assert(kPpl <= 16 && 16 % kPpl == 0, "a V load stays inside one page");
+    __shared__ __attribute__((aligned(16))) float pbuf[kPWaves][kChunk][kHeadsMax];
+    __shared__ __attribute__((aligned(16))) float abuf[kPWaves][kHeadsMax];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t item = (int64_t)blockIdx.x * kPWaves + wave;
+    const int64_t per_q = (int64_t)kvh * nhb * nsplit;
+    const int qi = (int)(item / per_q);
+    if (qi >= qs.count) return;
+    // kv head fastest: waves of one workgroup read neighbouring rows of the same pages
+    const int g = (int)(item % kvh);
+    const int hb = (int)((item / kvh) % nhb);
+    const int split = (int)((item / ((int64_t)kvh * nhb)) % nsplit);
+    const int clen = qs.causal_len(qi);
+    const int t_begin = split * kPSplit;
+    if (t_begin >= clen) return;
+    const int t_end = min(clen, t_begin + kPSplit);
+    const int G = qh / kvh;
+    const int h0 = g * G + hb * kHeadsMax;
+    const int nh = min(kHeadsMax, G - hb * kHeadsMax);  // <= NH
+    const int32_t* table = qs.table + (int64_t)qi * qs.table_stride;
+
+    // the split's pages, one per lane, read once
+    static_assert(kPSplit == 64 * FHIP_PAGE_TOKENS, "one cached page per lane");
+    const int split_page =
+        t_begin + FHIP_PAGE_TOKENS * lane < t_end ? table[t_begin / FHIP_PAGE_TOKENS + lane] : -1;
+    const typename Pages::Lane pl = pg.lane_load(split_page);
+
+    // Q^T as the QK B operand: lane (column n, k group kg) holds q[h0 + n][32 s + 8 kg + 0..7]
+    // at step s; columns n >= nh are zero.
+    const int n = lane & 15, kg = lane >> 4;
+    u32x4 bq[kSteps];
+    {
+        const uint16_t* qrow = q + ((int64_t)qi * qh + h0 + (n < nh ? n : 0)) * HD + 8 * kg;
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) {
+            const u32x4 v = ld16(qrow + 32 * s);
+            bq[s] = n < nh ? v : u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+    // lane offsets inside a page: K row (lane & 15) segment kg; V row of position subset ps,
+    // dims 8 dg .. 8 dg + 7
+    const int64_t k_off = ((int64_t)(lane & 15) * kvh + g) * (HD * 2) + 16 * kg;
+    const int dg = lane % kDg, ps = lane / kDg;
+    const uint8_t* dummy = (const uint8_t*)q;  // >= 2 HD readable bytes, finite values
+
+    float m_run = -__builtin_inff(), l_run = 0.0f;  // lanes n (any kg): head n
+    float acc[NH][8];
+#pragma unroll
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[h][i] = 0.0f;
+
+    for (int t0 = t_begin; t0 < t_end; t0 += kChunk) {
+        const int j0 = (t0 - t_begin) / FHIP_PAGE_TOKENS;
+        // ---- every load of the chunk first: K rows, then V rows. Loads of positions past
+        // the end or in invalid pages read `dummy` and are masked below.
+        bool pok[kTiles];
+        const uint8_t* kb[kTiles];
+        const uint8_t* vb[kTiles];
+#pragma unroll
+        for (int tt = 0; tt < kTiles; ++tt) {
+            const int id = __builtin_amdgcn_readlane(split_page, j0 + tt);
+            pok[tt] = pg.valid(id);
+            kb[tt] = pok[tt] ? pg.k_at(pl, j0 + tt, id) : dummy;
+            vb[tt] = pok[tt] ? pg.v_at(pl, j0 + tt, id) : dummy;
+        }
+        u32x4 kr[kTiles][kSteps];
+#pragma unroll
+        for (int tt = 0; tt < kTiles; ++tt) {
+            const bool ok = pok[tt] && t0 + 16 * tt + (lane & 15) < t_end;
+            const uint8_t* src = ok ? kb[tt] + k_off : dummy;
+#pragma unroll
+            for (int s = 0; s < kSteps; ++s) kr[tt][s] = ld16(src + 64 * s);
+        }
+        u32x4 vr[kVLoads];
+        bool vok[kVLoads];
+#pragma unroll
+        for (int j = 0; j < kVLoads; ++j) {
+            const int pp = j * kPpl + ps;  // position in the chunk
+            const int tt = (j * kPpl) / 16;
+            vok[j] = pok[tt] && t0 + pp < t_end;
+            const uint8_t* src =
+                vok[j] ? vb[tt] + (((int64_t)(pp % 16) * kvh + g) * HD + 8 * dg) * 2 : dummy;
+            vr[j] = ld16(src);
+        }
+
+        // ---- QK: lane (n, rg) gets positions 16 tt + 4 rg + e of head n
+        float sc[kTiles][4];
+#pragma unroll
+        for (int tt = 0; tt < kTiles; ++tt) {
+            f4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < kSteps; ++s)
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, kr[tt][s]),
+                                                           __builtin_bit_cast(h8_t, bq[s]), d,
+                                                           0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int pos = t0 + 16 * tt + 4 * kg + e;
+                sc[tt][e] = pok[tt] && pos < t_end ? d[e] * scale_log2 : -__builtin_inff();
+            }
+        }
+        // ---- online softmax per head (lanes n, n + 16, n + 32, n + 48 share head n)
+        float cmax = -__builtin_inff();
+#pragma unroll
+        for (int tt = 0; tt < kTiles; ++tt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) cmax = fmaxf(cmax, sc[tt][e]);
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+        const float m_new = fmaxf(m_run, cmax);
+        const float mref = m_new == -__builtin_inff() ? 0.0f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - mref);  // 0 while m_run is -inf
+        float psum = 0.0f;
+#pragma unroll
+        for (int tt = 0; tt < kTiles; ++tt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float p = __builtin_amdgcn_exp2f(sc[tt][e] - mref);
+                psum += p;
+                if (n < kHeadsMax) pbuf[wave][16 * tt + 4 * kg + e][n] = p;
+            }
+        psum += __shfl_xor(psum, 16);
+        psum += __shfl_xor(psum, 32);
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+        if (lane < kHeadsMax) abuf[wave][lane] = alpha;
+
+        // ---- PV (this wave's LDS writes above complete before its reads below: one wave's
+        // LDS instructions execute in order)
+        float al[kHeadsMax];
+        {
+            const f4_t a0 = *(const f4_t*)&abuf[wave][0];
+            const f4_t a1 = *(const f4_t*)&abuf[wave][4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                al[i] = a0[i];
+                al[4 + i] = a1[i];
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < NH; ++h)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[h][i] *= al[h];
+#pragma unroll
+        for (int j = 0; j < kVLoads; ++j) {
+            const int pp = j * kPpl + ps;
+            float pw[kHeadsMax];
+            {
+                const f4_t p0 = *(const f4_t*)&pbuf[wave][pp][0];
+                const f4_t p1 = *(const f4_t*)&pbuf[wave][pp][4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    pw[i] = p0[i];
+                    pw[4 + i] = p1[i];
+                }
+            }
+            float v[8];
+            unpack16<TrF16>(vok[j] ? vr[j] : u32x4{0u, 0u, 0u, 0u}, v);
+#pragma unroll
+            for (int h = 0; h < NH; ++h)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[h][i] = fmaf(pw[h], v[i], acc[h][i]);
+        }
+    }
+
+    // ---- partials: sum the position subsets (lanes with the same dim group), then lanes of
+    // subset 0 write dims 8 dg .. 8 dg + 7 of each head
+#pragma unroll
+    for (int o = kDg; o < 64; o <<= 1)
+#pragma unroll
+        for (int h = 0; h < NH; ++h)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[h][i] += __shfl_xor(acc[h][i], o);
+    const int64_t v0 = (int64_t)qi * qh + h0;
+    if (lane < nh) {
+        part_ml[((v0 + lane) * nsplit + split) * 2 + 0] = m_run * 0.6931471805599453f;
+        part_ml[((v0 + lane) * nsplit + split) * 2 + 1] = l_run;
+    }
+    if (ps == 0) {
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+            if (h < nh) {
+                float* dst = part_acc + ((v0 + h) * nsplit + split) * HD + 8 * dg;
+                *(f4_t*)dst = f4_t{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
+                *(f4_t*)(dst + 4) = f4_t{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
+            }
+        }
+    }
+}
+
+// Merge of the splits of one (query, q head) vector per wave:
+// out = (sum_s w_s acc_s) / (sum_s w_s l_s), w_s = exp(m_s - max m); zeros when the query
+// attends to no position.
+__global__ __launch_bounds__(64) void paged_attn_combine_kernel(PQueries qs,
+                                                                const float* __restrict__ ml,
+                                                                const float* __restrict__ acc,
+                                                                uint16_t* __restrict__ out,
+                                                                int qh, int hd, int nsplit) {
+    const int64_t vec = blockIdx.x;
+    const int qi = (int)(vec / qh);
+    const int clen = qs.causal_len(qi);
+    const int ns = (clen + kPSplit - 1) / kPSplit;
+    const float* m = ml + vec * nsplit * 2;
+    float M = -__builtin_inff();
+    for (int s = 0; s < ns; ++s) M = fmaxf(M, m[2 * s]);
+    float L = 0.0f;
+    if (M != -__builtin_inff())
+        for (int s = 0; s < ns; ++s) L += expf(m[2 * s] - M) * m[2 * s + 1];
+    const float* a = acc + vec * nsplit * hd;
+    for (int d = threadIdx.x; d < hd; d += 64) {
+        float o = 0.0f;
+        if (L > 0.0f) {
+            for (int s = 0; s < ns; ++s) o += expf(m[2 * s] - M) * a[(int64_t)s * hd + d];
+            o /= L;
+        }
+        out[vec * hd + d] = (uint16_t)f2h(o);
+    }
+}
+
+size_t paged_ws_layout(int nq, int qh, int hd, int max_tokens, size_t* off_acc, int* nsplit) {
+    const int ns = max_tokens > 0 ? (max_tokens + kPSplit - 1) / kPSplit : 1;
+    const size_t ml = (size_t)nq * qh * ns * 2 * sizeof(float);
+    const size_t acc = (size_t)nq * qh * ns * hd * sizeof(float);
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    if (off_acc) *off_acc = al(ml);
+    if (nsplit) *nsplit = ns;
+    return al(ml) + al(acc);
+}
+
+bool paged_shape_ok(int qh, int kvh, int hd) {
+    return kvh > 0 && qh > 0 && qh % kvh == 0 &&
+           (hd == 32 || hd == 64 || hd == 128 || hd == 256);
+}
+
+template <int HD, int NH, class Pages>
+void launch_split_t(const uint16_t* q, const PQueries& qs, const Pages& pg, int qh, int kvh,
+                    int nhb, float* ml, float* acc, int nsplit, int64_t groups, hipStream_t s) {
+    const float scale_log2 = 1.4426950408889634f / sqrtf((float)HD);
+    hipLaunchKernelGGL((paged_attn_split_kernel<HD, NH, Pages>), dim3((unsigned)groups),
+                       dim3(64 * kPWaves), 0, s, q, qs, pg, qh, kvh, nhb, scale_log2, ml, acc,
+                       nsplit);
+}
+
+template <int HD, class Pages>
+void launch_split_hd(const uint16_t* q, const PQueries& qs, const Pages& pg, int qh, int kvh,
+                     int nhb, float* ml, float* acc, int nsplit, int64_t groups, hipStream_t s) {
+    if (qh / kvh <= 4)
+        launch_split_t<HD, 4>(q, qs, pg, qh, kvh, nhb, ml, acc, nsplit, groups, s);
+    else
+        launch_split_t<HD, 8>(q, qs, pg, qh, kvh, nhb, ml, acc, nsplit, groups, s);
+}
+
+template <class Pages>
+int launch_paged(void* out, const void* q, const PQueries& qs, int nq, const Pages& pg, int qh,
+                 int kvh, int hd, void* ws, hipStream_t s) {
+    if (nq == 0) return hipSuccess;
+    size_t off_acc;
+    int nsplit;
+    paged_ws_layout(nq, qh, hd, qs.max_blocks * FHIP_PAGE_TOKENS, &off_acc, &nsplit);
+    float* ml = (float*)ws;
+    float* acc = (float*)((char*)ws + off_acc);
+    const int nhb = (qh / kvh + kHeadsMax - 1) / kHeadsMax;
+    const int64_t items = (int64_t)nq * kvh * nhb * nsplit;
+    const int64_t groups = ceil_div(items, kPWaves);
+    if (groups > 0x7fffffff || (int64_t)nq * qh > 0x7fffffff) return hipErrorInvalidValue;
+    PQueries q2 = qs;
+    q2.count = nq;
+    const uint16_t* qp = (const uint16_t*)q;
+    switch (hd) {
+        case 32: launch_split_hd<32>(qp, q2, pg, qh, kvh, nhb, ml, acc, nsplit, groups, s); break;
+        case 64: launch_split_hd<64>(qp, q2, pg, qh, kvh, nhb, ml, acc, nsplit, groups, s); break;
+        case 128: launch_split_hd<128>(qp, q2, pg, qh, kvh, nhb, ml, acc, nsplit, groups, s); break;
+        default: launch_split_hd<256>(qp, q2, pg, qh, kvh, nhb, ml, acc, nsplit, groups, s); break;
+    }
+    hipLaunchKernelGGL(paged_attn_combine_kernel, dim3((unsigned)((int64_t)nq * qh)), dim3(64), 0,
+                       s, q2, ml, acc, (uint16_t*)out, qh, hd, nsplit);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t fhip_attention_paged_workspace_bytes(int batch, int num_q_heads, int head_dim,
+                                            int max_blocks) {
+    if (batch <= 0 || num_q_heads <= 0 || head_dim <= 0 || max_blocks <= 0) return 0;
+    return paged_ws_layout(batch, num_q_heads, head_dim, max_blocks * FHIP_PAGE_TOKENS, nullptr,
+                           nullptr);
+}
+
+int fhip_launch_attention_paged_decode(void* output, const void* q, const int32_t* block_table,
+                                       const int32_t* seq_lens, int batch, int max_blocks,
+                                       int num_pages, const void* k_pool, const void* v_pool,
+                                       int64_t page_k_bytes, int64_t page_v_bytes,
+                                       int num_q_heads, int num_kv_heads, int head_dim,
+                                       void* workspace, fhip_stream_t stream) {
+    if (batch < 0 || max_blocks <= 0 || num_pages < 0 || page_k_bytes < 0 || page_v_bytes < 0 ||
+        !paged_shape_ok(num_q_heads, num_kv_heads, head_dim) ||
+        (int64_t)max_blocks * FHIP_PAGE_TOKENS > 0x7fffffff)
+        return hipErrorInvalidValue;
+    if (batch == 0) return hipSuccess;
+    if (!output || !q || !block_table || !seq_lens || !k_pool || !v_pool || !workspace)
+        return hipErrorInvalidValue;
+    const PQueries qs{block_table, max_blocks, max_blocks, seq_lens, 0, 0, batch};
+    const F16PoolPages pg{(const uint8_t*)k_pool, (const uint8_t*)v_pool, page_k_bytes,
+                          page_v_bytes, num_pages};
+    return launch_paged(output, q, qs, batch, pg, num_q_heads, num_kv_heads, head_dim, workspace,
+                        fhip_host::as_stream(stream));
+}
+
+// The reference interface: one sequence, num_tokens queries at positions
+// start_pos .. start_pos + num_tokens - 1, per-block pointer arrays indexed by the physical
+// block ids of block_table[0 .. num_blocks_in_seq). The split partials live in a
+// stream-ordered allocation freed on the same stream.
+int fhip_launch_paged_attention(void* output, const void* q, const int* block_table,
+                                const void** k_block_ptrs, const void** v_block_ptrs,
+                                int num_tokens, int num_q_heads, int num_kv_heads, int head_dim,
+                                int kv_len, int start_pos, int num_blocks_in_seq,
+                                fhip_stream_t stream) {
+    if (num_tokens < 0 || kv_len < 0 || start_pos < 0 || num_blocks_in_seq < 0 ||
+        !paged_shape_ok(num_q_heads, num_kv_heads, head_dim) ||
+        (int64_t)num_blocks_in_seq * FHIP_PAGE_TOKENS > 0x7fffffff)
+        return hipErrorInvalidValue;
+    if (num_tokens == 0) return hipSuccess;
+    if (!output || !q) return hipErrorInvalidValue;
+    if (num_blocks_in_seq > 0 && (!block_table || !k_block_ptrs || !v_block_ptrs))
+        return hipErrorInvalidValue;
+    hipStream_t s = fhip_host::as_stream(stream);
+    const int mb = num_blocks_in_seq > 0 ? num_blocks_in_seq : 1;
+    // with no blocks every query attends to nothing: the table is never read
+    const PQueries qs{(const int32_t*)block_table, 0, num_blocks_in_seq, nullptr, kv_len,
+                      start_pos, num_tokens};
+    const size_t bytes = paged_ws_layout(num_tokens, num_q_heads, head_dim,
+                                         mb * FHIP_PAGE_TOKENS, nullptr, nullptr);
+    void* ws = nullptr;
+    hipError_t e = hipMallocAsync(&ws, bytes, s);
+    if (e != hipSuccess) return e;
+    const F16PtrPages pg{(const uint8_t* const*)k_block_ptrs, (const uint8_t* const*)v_block_ptrs,
+                         0x7fffffff};
+    int r = launch_paged(output, q, qs, num_tokens, pg, num_q_heads, num_kv_heads, head_dim, ws,
+                         s);
+    hipError_t e2 = hipFreeAsync(ws, s);
+    if (r != hipSuccess) return r;
+    return e2;
+}
+
+}  // extern "C"

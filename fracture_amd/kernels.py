@@ -361,3 +361,48 @@ def attention_tq_decode(out: torch.Tensor, q: torch.Tensor, block_table: torch.T
         _p(out), _p(q), _p(block_table), _p(seq_lens), B, mb, P, _p(kp), _p(kn), _p(vp), _p(vn),
         kp[0].nbytes, kn[0].nbytes, vp[0].nbytes, vn[0].nbytes, _p(krot), _p(vrot), _p(kc),
         _p(vc), qh, H, hd, key_bits, value_bits, _p(ws), _stream()), "attention_tq_decode")
+
+
+def attention_paged_workspace(batch: int, qh: int, hd: int, max_blocks: int, device="cuda"):
+    n = int(_L().fhip_attention_paged_workspace_bytes(batch, qh, hd, max_blocks))
+    return torch.empty(max(n, 16), dtype=torch.uint8, device=device)
+
+
+def attention_paged_decode(out: torch.Tensor, q: torch.Tensor, block_table: torch.Tensor,
+                           seq_lens: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                           num_kv_heads: int, workspace: torch.Tensor | None = None) -> None:
+    """One query per sequence over FP16 pages: q/out [B, qh, hd] fp16; block_table
+    [B, max_blocks] int32; seq_lens [B] int32; k_pool/v_pool [P, 16, kvh, hd] fp16."""
+    _dev(out, q, block_table, seq_lens, k_pool, v_pool)
+    _need(q.dtype == torch.float16 and q.dim() == 3 and out.shape == q.shape and
+          out.dtype == torch.float16, "q/out")
+    B, qh, hd = q.shape
+    _need(block_table.dtype == torch.int32 and block_table.dim() == 2 and
+          block_table.shape[0] == B and block_table.is_contiguous(), "block_table")
+    _need(seq_lens.dtype == torch.int32 and seq_lens.numel() == B, "seq_lens")
+    mb = block_table.shape[1]
+    P = k_pool.shape[0]
+    for t, name in ((k_pool, "k pool"), (v_pool, "v pool")):
+        _need(t.dtype == torch.float16 and t.is_contiguous() and t.shape[0] == P and
+              t[0].numel() == 16 * num_kv_heads * hd, name)
+    ws = workspace if workspace is not None else attention_paged_workspace(B, qh, hd, mb,
+                                                                           q.device)
+    _need(ws.numel() >= _L().fhip_attention_paged_workspace_bytes(B, qh, hd, mb), "workspace")
+    _ok(_L().fhip_launch_attention_paged_decode(
+        _p(out), _p(q), _p(block_table), _p(seq_lens), B, mb, P, _p(k_pool), _p(v_pool),
+        k_pool[0].nbytes, v_pool[0].nbytes, qh, num_kv_heads, hd, _p(ws), _stream()),
+        "attention_paged_decode")
+
+
+def paged_attention(out: torch.Tensor, q: torch.Tensor, block_table: torch.Tensor,
+                    k_block_ptrs: torch.Tensor, v_block_ptrs: torch.Tensor, num_kv_heads: int,
+                    kv_len: int, start_pos: int) -> None:
+    """The reference interface (attention_paged.cu:172-185): T causal queries of one sequence;
+    block_table [nblocks] int32; k/v_block_ptrs int64 device arrays of block addresses."""
+    _dev(out, q, block_table, k_block_ptrs, v_block_ptrs)
+    _need(q.dtype == torch.float16 and q.dim() == 3 and out.shape == q.shape, "q/out")
+    _need(block_table.dtype == torch.int32 and block_table.dim() == 1, "block_table")
+    T, qh, hd = q.shape
+    _ok(_L().fhip_launch_paged_attention(
+        _p(out), _p(q), _p(block_table), _p(k_block_ptrs), _p(v_block_ptrs), T, qh,
+        num_kv_heads, hd, kv_len, start_pos, block_table.numel(), _stream()), "paged_attention")

@@ -114,6 +114,17 @@ int fhip_launch_attention_paged_tq(void* output, const void* q, const int* block
                                    int value_bits, int k_packed_dim_per_head,
                                    int v_packed_dim_per_head, fhip_stream_t stream);
 
+/* ffi.rs:186-200 `launch_paged_attention` (attention_paged.cu:172-185): causal GQA attention
+ * of q [T, qh, hd] fp16 over FP16 pages given as per-block pointer arrays (device memory,
+ * indexed by the physical block ids of block_table), each block [16, kvh, hd] fp16. head_dim
+ * is 32, 64, 128 or 256. Unlike the reference kernel it keeps no kv_len-sized score row, so
+ * kv_len is bounded only by the block table. */
+int fhip_launch_paged_attention(void* output, const void* q, const int* block_table,
+                                const void** k_block_ptrs, const void** v_block_ptrs,
+                                int num_tokens, int num_q_heads, int num_kv_heads, int head_dim,
+                                int kv_len, int start_pos, int num_blocks_in_seq,
+                                fhip_stream_t stream);
+
 /* --- additive raw launchers ---------------------------------------------------------- */
 
 /* dtype-generic forms of rmsnorm / add / silu_mul (FHIP_FP16, FHIP_BF16, FHIP_FP32). */
@@ -227,6 +238,20 @@ int fhip_launch_attention_tq_decode(void* output, const void* q, const int32_t* 
                                     int num_q_heads, int num_kv_heads, int head_dim,
                                     int key_bits, int value_bits, void* workspace,
                                     fhip_stream_t stream);
+
+/* Batched decode attention over an FP16 page pool (the FP16 form of the call above, for
+ * batched decode): q [B, qh, hd] fp16, block_table [B, max_blocks] int32, seq_lens [B] int32;
+ * page p of K at k_pool + p * page_k_bytes holds [16, kvh, hd] fp16, likewise V; positions
+ * whose page id is outside [0, num_pages) are masked out. Output [B, qh, hd] fp16.
+ * The workspace holds split partials; size it with fhip_attention_paged_workspace_bytes. */
+size_t fhip_attention_paged_workspace_bytes(int batch, int num_q_heads, int head_dim,
+                                            int max_blocks);
+int fhip_launch_attention_paged_decode(void* output, const void* q, const int32_t* block_table,
+                                       const int32_t* seq_lens, int batch, int max_blocks,
+                                       int num_pages, const void* k_pool, const void* v_pool,
+                                       int64_t page_k_bytes, int64_t page_v_bytes,
+                                       int num_q_heads, int num_kv_heads, int head_dim,
+                                       void* workspace, fhip_stream_t stream);
 
 /* =====================================================================================
  * 2. Handle runtime (mirror of the Backend trait)

@@ -80,6 +80,8 @@ def _declare(L: C.CDLL) -> None:
         "o_tq_dequant": (None, [P, P, I64, C.c_int, P, P, C.c_int, P]),
         "o_tq_attention": (None, [P, P, C.c_int, P, P, P, P, I64, I64, I64, I64, P, P, P, P,
                                   C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, P]),
+        "o_paged_attention": (None, [P, P, C.c_int, P, P, I64, I64, C.c_int, C.c_int, C.c_int,
+                                     P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -360,4 +362,18 @@ def tq_attention(q16, block_table, causal_len, kp, kn, vp, vn, krot, vrot, kc, v
         _p(np.ascontiguousarray(krot, np.float32)), _p(np.ascontiguousarray(vrot, np.float32)),
         _p(np.ascontiguousarray(kc, np.float32)), _p(np.ascontiguousarray(vc, np.float32)),
         kbits, vbits, qh, kvh, hd, _p(out))
+    return out
+
+
+def paged_attention(q16, block_table, causal_len, kpool, vpool, kvh):
+    """One query token over FP16 pages: q16 [qh, hd] float16; kpool/vpool [pages, 16, kvh, hd]
+    float16 (any page shape whose rows are [16][kvh][hd])."""
+    q = np.ascontiguousarray(q16, dtype=np.float16)
+    qh, hd = q.shape
+    bt = np.ascontiguousarray(block_table, dtype=np.int32)
+    kp = np.ascontiguousarray(kpool, dtype=np.float16)
+    vp = np.ascontiguousarray(vpool, dtype=np.float16)
+    out = np.empty((qh, hd), np.float16)
+    lib().o_paged_attention(_p(q), _p(bt), int(causal_len), _p(kp), _p(vp), kp[0].nbytes,
+                            vp[0].nbytes, qh, kvh, hd, _p(out))
     return out

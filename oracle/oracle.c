@@ -22,6 +22,8 @@
  *                       reference kernel vs the MSB-first generalisation
  *   compress/dequant .. composition of the above + round-trip cosine thresholds
  *   attention ......... float64 softmax attention over dequantized K/V, rotation identities
+ *   paged attention ... float64 softmax(QK^T/sqrt(d))V, one-position and equal-key closed forms,
+ *                       page-permutation invariance
  */
 #include <math.h>
 #include <stdint.h>
@@ -623,5 +625,52 @@ void o_tq_attention(const uint16_t* q16, const int32_t* block_table, int causal_
     }
     free(qrot);
     free(acc);
+    free(sc);
+}
+
+/* FP16 paged GQA attention for one query token (attention_paged.cu:36-170).
+ * Pages live in pools: K page p at kpool + p*skp bytes, layout [16][kvh][hd] fp16; likewise V.
+ * q16/out16: [qh][hd] fp16 for this token; causal_len positions are attended through
+ * block_table. Per head: score_t = (sum_d q_d k_d, in d order) * (1/sqrt(hd)) (:61-70; the
+ * kernel's rsqrtf), max, e_t = exp(score_t - max), sum, p_t = e_t / sum (:107-134), then
+ * out_d = half(sum_t p_t v_td, in t order) (:138-150). causal_len 0 gives zeros. */
+void o_paged_attention(const uint16_t* q16, const int32_t* block_table, int causal_len,
+                       const uint8_t* kpool, const uint8_t* vpool, int64_t skp, int64_t svp,
+                       int qh, int kvh, int hd, uint16_t* out16) {
+    const int G = qh / kvh;
+    const float scale = 1.0f / sqrtf((float)hd);
+    float* sc = (float*)malloc(sizeof(float) * (size_t)(causal_len > 0 ? causal_len : 1));
+    for (int h = 0; h < qh; ++h) {
+        const int kvhd = h / G;
+        const uint16_t* qv = q16 + (int64_t)h * hd;
+        float mx = -3.402823466e38f;
+        for (int t = 0; t < causal_len; ++t) {
+            const int page = block_table[t / 16], off = t % 16;
+            const uint16_t* k = (const uint16_t*)(kpool + (int64_t)page * skp) +
+                                ((int64_t)off * kvh + kvhd) * hd;
+            float dot = 0.0f;
+            for (int d = 0; d < hd; ++d) dot += o_f16_to_f32(qv[d]) * o_f16_to_f32(k[d]);
+            dot *= scale;
+            sc[t] = dot;
+            if (dot > mx) mx = dot;
+        }
+        float sum = 0.0f;
+        for (int t = 0; t < causal_len; ++t) {
+            sc[t] = expf(sc[t] - mx);
+            sum += sc[t];
+        }
+        const float inv = 1.0f / sum;
+        for (int t = 0; t < causal_len; ++t) sc[t] *= inv;
+        for (int d = 0; d < hd; ++d) {
+            float a = 0.0f;
+            for (int t = 0; t < causal_len; ++t) {
+                const int page = block_table[t / 16], off = t % 16;
+                const uint16_t* v = (const uint16_t*)(vpool + (int64_t)page * svp) +
+                                    ((int64_t)off * kvh + kvhd) * hd;
+                a += sc[t] * o_f16_to_f32(v[d]);
+            }
+            out16[(int64_t)h * hd + d] = o_f32_to_f16(a);
+        }
+    }
     free(sc);
 }

@@ -1,0 +1,149 @@
+"""GPU parity of FP16 paged attention against the oracle's restatement of attention_paged.cu
+(fp16 output, |a - e| <= 1e-3 + 1e-3|e|).
+
+Covers the batched decode entry over contiguous page pools (one query per sequence,
+per-sequence lengths around page and 1024-position split edges, permuted block tables, GQA
+groups of 1 to 12 q heads, head_dim 32 / 64 / 128 / 256, masked pages, empty sequences) and the
+reference-interface entry with per-block pointer arrays and causal prefill queries.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import assert_close
+from fracture_amd import kernels as K
+
+pytestmark = pytest.mark.gpu
+
+
+def dev_t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def build_pool(rng, lens, kvh, hd, extra_pages=3):
+    """Random fp16 K/V pages for each sequence in a shared, permuted pool; unused rows hold
+    garbage (large values and NaN) that must never reach the output."""
+    nbs = [(n + 15) // 16 for n in lens]
+    P = sum(nbs) + extra_pages
+    perm = rng.permutation(P).astype(np.int32)
+    kp = rng.standard_normal((P, 16, kvh, hd)).astype(np.float16)
+    vp = rng.standard_normal((P, 16, kvh, hd)).astype(np.float16)
+    maxb = max(max(nbs), 1)
+    table = np.full((len(lens), maxb), -7, np.int32)
+    at = 0
+    for b, n in enumerate(lens):
+        pages = perm[at:at + nbs[b]]
+        at += nbs[b]
+        table[b, :nbs[b]] = pages
+        if n % 16:  # rows past the sequence end in its last page
+            kp[pages[-1], n % 16:] = np.float16(6e4)
+            vp[pages[-1], n % 16:] = np.float16(np.nan)
+    return kp, vp, table
+
+
+def run_decode(dev, q, table, lens, kp, vp, kvh):
+    out = torch.empty(q.shape, dtype=torch.float16, device=dev)
+    K.attention_paged_decode(out, dev_t(q, dev), dev_t(table, dev),
+                             dev_t(np.asarray(lens, np.int32), dev), dev_t(kp, dev),
+                             dev_t(vp, dev), kvh)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("hd", [32, 64, 128, 256])
+@pytest.mark.parametrize("qh,kvh", [(32, 8), (8, 8), (16, 1), (24, 2)])
+def test_decode_small_contexts(dev, hd, qh, kvh):
+    rng = np.random.default_rng(hd * 100 + qh + kvh)
+    lens = [1, 15, 16, 17, 33, 100]
+    kp, vp, table = build_pool(rng, lens, kvh, hd)
+    q = (rng.standard_normal((len(lens), qh, hd)) * 2).astype(np.float16)
+    got = run_decode(dev, q, table, lens, kp, vp, kvh)
+    for b, n in enumerate(lens):
+        want = oracle.paged_attention(q[b], table[b], n, kp, vp, kvh)
+        assert_close(got[b].astype(np.float32), want.astype(np.float32), 1e-3, 1e-3,
+                     f"seq {b} len {n}")
+
+
+@pytest.mark.parametrize("hd", [128, 64])
+def test_decode_split_edges(dev, hd):
+    """Lengths around the 1024-position splits: the combine merges 1 to 3 splits."""
+    rng = np.random.default_rng(7 + hd)
+    qh, kvh = 16, 4
+    lens = [1023, 1024, 1025, 2048, 2100, 3001]
+    kp, vp, table = build_pool(rng, lens, kvh, hd)
+    q = (rng.standard_normal((len(lens), qh, hd)) * 3).astype(np.float16)
+    got = run_decode(dev, q, table, lens, kp, vp, kvh)
+    for b, n in enumerate(lens):
+        want = oracle.paged_attention(q[b], table[b], n, kp, vp, kvh)
+        assert_close(got[b].astype(np.float32), want.astype(np.float32), 1e-3, 1e-3,
+                     f"seq {b} len {n}")
+
+
+def test_decode_long_contexts(dev):
+    """Llama-3.1-8B heads (32 q / 8 kv, hd 128) at contexts up to 32768 positions."""
+    rng = np.random.default_rng(11)
+    qh, kvh, hd = 32, 8, 128
+    lens = [32768, 20000, 5000, 1]
+    kp, vp, table = build_pool(rng, lens, kvh, hd, extra_pages=1)
+    q = (rng.standard_normal((len(lens), qh, hd)) * 3).astype(np.float16)
+    got = run_decode(dev, q, table, lens, kp, vp, kvh)
+    for b, n in enumerate(lens):
+        want = oracle.paged_attention(q[b], table[b], n, kp, vp, kvh)
+        assert_close(got[b].astype(np.float32), want.astype(np.float32), 1e-3, 1e-3,
+                     f"seq {b} len {n}")
+
+
+def test_decode_empty_sequence_and_masked_pages(dev):
+    """Length 0 gives zeros; a page id outside the pool masks its 16 positions, which equals
+    attending to the sequence without that page."""
+    rng = np.random.default_rng(12)
+    qh, kvh, hd = 8, 2, 128
+    lens = [0, 80, 1100]
+    kp, vp, table = build_pool(rng, lens, kvh, hd)
+    P = kp.shape[0]
+    table[1, 2] = P + 5          # page 2 of sequence 1 (positions 32..47)
+    table[2, 10] = -3            # page 10 of sequence 2 (positions 160..175)
+    q = (rng.standard_normal((len(lens), qh, hd)) * 2).astype(np.float16)
+    got = run_decode(dev, q, table, lens, kp, vp, kvh)
+    assert not got[0].any()
+    keep1 = np.delete(table[1], 2)
+    want1 = oracle.paged_attention(q[1], keep1, 80 - 16, kp, vp, kvh)
+    assert_close(got[1].astype(np.float32), want1.astype(np.float32), 1e-3, 1e-3, "seq 1")
+    keep2 = np.delete(table[2], 10)
+    want2 = oracle.paged_attention(q[2], keep2, 1100 - 16, kp, vp, kvh)
+    assert_close(got[2].astype(np.float32), want2.astype(np.float32), 1e-3, 1e-3, "seq 2")
+
+
+@pytest.mark.parametrize("kv_len,T,start_pos", [(90, 6, 84), (40, 5, 38), (1030, 3, 1027),
+                                                (16, 1, 15)])
+def test_reference_interface_prefill_causal(dev, kv_len, T, start_pos):
+    """fhip_launch_paged_attention: T queries at start_pos.. over per-block pointer arrays;
+    query i attends to min(start_pos + i + 1, kv_len) positions."""
+    rng = np.random.default_rng(kv_len + T)
+    qh, kvh, hd = 8, 2, 64
+    kp, vp, table = build_pool(rng, [kv_len], kvh, hd, extra_pages=2)
+    P = kp.shape[0]
+    tk, tv = dev_t(kp, dev), dev_t(vp, dev)
+    kptr = torch.tensor([tk[i].data_ptr() for i in range(P)], dtype=torch.int64, device=dev)
+    vptr = torch.tensor([tv[i].data_ptr() for i in range(P)], dtype=torch.int64, device=dev)
+    q = (rng.standard_normal((T, qh, hd)) * 2).astype(np.float16)
+    tq_ = dev_t(q, dev)
+    out = torch.empty_like(tq_)
+    K.paged_attention(out, tq_, dev_t(table[0], dev), kptr, vptr, kvh, kv_len, start_pos)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for t in range(T):
+        clen = min(start_pos + t + 1, kv_len)
+        want = oracle.paged_attention(q[t], table[0], clen, kp, vp, kvh)
+        assert_close(got[t].astype(np.float32), want.astype(np.float32), 1e-3, 1e-3,
+                     f"token {t}")
+
+
+def test_reference_interface_rejects_unsupported_head_dim(dev):
+    q = torch.zeros((1, 4, 96), dtype=torch.float16, device=dev)
+    out = torch.empty_like(q)
+    bt = torch.zeros(1, dtype=torch.int32, device=dev)
+    ptr = torch.zeros(1, dtype=torch.int64, device=dev)
+    with pytest.raises(RuntimeError):
+        K.paged_attention(out, q, bt, ptr, ptr, 4, 1, 0)
