@@ -6,7 +6,7 @@
 // fp16 block; score = dot(q, k) / sqrt(head_dim) with fp32 accumulation, softmax in fp32,
 // out = half(sum_t p_t v_t). The reference keeps a kv_len-float score row in shared memory
 // (attention_paged.cu:58-59, 176); here the context is split into 1024-position pieces with an
-// online softmax each, merged by a second kernel, so kv_len is bounded only by the block table.
+// online softmax each, merged by a second kernel: up to 1,048,576 positions per sequence.
 //
 // Work split: one wave per (query, kv head, block of up to 8 of its q heads, split). Each K
 // row crosses HBM once per (query, kv head) for up to 8 q heads. Per 32-position chunk
@@ -30,8 +30,11 @@ using namespace fhip;
 namespace {
 
 constexpr int kPSplit = 1024;  // positions per split: 64 pages, one per lane of the page cache
-constexpr int kPWaves = 4;     // waves per workgroup (independent work items)
+constexpr int kPWaves = 2;     // waves per workgroup (independent work items)
 constexpr int kHeadsMax = 8;   // q heads per wave
+// Longest context a block table may describe (the combine kernel keeps one weight per
+// split in LDS: 4 KiB at this bound).
+constexpr int64_t kMaxTokens = (int64_t)kPSplit * 1024;
 
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
@@ -303,32 +306,56 @@ paged_attn_split_kernel(const uint16_t* __restrict__ q, PQueries qs, Pages pg, i
     }
 }
 
-// Merge of the splits of one (query, q head) vector per wave:
+// Merge of the splits of one (query, q head) vector per workgroup:
 // out = (sum_s w_s acc_s) / (sum_s w_s l_s), w_s = exp(m_s - max m); zeros when the query
-// attends to no position.
-__global__ __launch_bounds__(64) void paged_attn_combine_kernel(PQueries qs,
-                                                                const float* __restrict__ ml,
-                                                                const float* __restrict__ acc,
-                                                                uint16_t* __restrict__ out,
-                                                                int qh, int hd, int nsplit) {
+// attends to no position. The split weights are computed once, in parallel, into LDS; each
+// thread then sums its output dims over the splits with eight loads in flight at a time.
+constexpr int kCombThreads = 128;
+__global__ __launch_bounds__(kCombThreads) void paged_attn_combine_kernel(
+    PQueries qs, const float* __restrict__ ml, const float* __restrict__ acc,
+    uint16_t* __restrict__ out, int qh, int hd, int nsplit) {
+    extern __shared__ float wts[];  // nsplit weights
+    __shared__ float red[2][kCombThreads / kWave];
     const int64_t vec = blockIdx.x;
     const int qi = (int)(vec / qh);
     const int clen = qs.causal_len(qi);
     const int ns = (clen + kPSplit - 1) / kPSplit;
     const float* m = ml + vec * nsplit * 2;
-    float M = -__builtin_inff();
-    for (int s = 0; s < ns; ++s) M = fmaxf(M, m[2 * s]);
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
+    constexpr int kW = kCombThreads / kWave;
+    float mx = -__builtin_inff();
+    for (int s = tid; s < ns; s += kCombThreads) mx = fmaxf(mx, m[2 * s]);
+    mx = wave_max(mx);
+    if (lane == 0) red[0][wv] = mx;
+    __syncthreads();
+    float M = red[0][0];
+#pragma unroll
+    for (int w = 1; w < kW; ++w) M = fmaxf(M, red[0][w]);
+    float ls = 0.0f;
+    for (int s = tid; s < ns; s += kCombThreads) {
+        const float w = M == -__builtin_inff() ? 0.0f : expf(m[2 * s] - M);
+        wts[s] = w;
+        ls += w * m[2 * s + 1];
+    }
+    ls = wave_sum(ls);
+    if (lane == 0) red[1][wv] = ls;
+    __syncthreads();
     float L = 0.0f;
-    if (M != -__builtin_inff())
-        for (int s = 0; s < ns; ++s) L += expf(m[2 * s] - M) * m[2 * s + 1];
+#pragma unroll
+    for (int w = 0; w < kW; ++w) L += red[1][w];
     const float* a = acc + vec * nsplit * hd;
-    for (int d = threadIdx.x; d < hd; d += 64) {
+    for (int d = tid; d < hd; d += kCombThreads) {
         float o = 0.0f;
-        if (L > 0.0f) {
-            for (int s = 0; s < ns; ++s) o += expf(m[2 * s] - M) * a[(int64_t)s * hd + d];
-            o /= L;
+        int s = 0;
+        for (; s + 8 <= ns; s += 8) {
+            float av[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) av[j] = a[(int64_t)(s + j) * hd + d];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o = fmaf(wts[s + j], av[j], o);
         }
-        out[vec * hd + d] = (uint16_t)f2h(o);
+        for (; s < ns; ++s) o = fmaf(wts[s], a[(int64_t)s * hd + d], o);
+        out[vec * hd + d] = (uint16_t)f2h(L > 0.0f ? o / L : 0.0f);
     }
 }
 
@@ -387,8 +414,9 @@ int launch_paged(void* out, const void* q, const PQueries& qs, int nq, const Pag
         case 128: launch_split_hd<128>(qp, q2, pg, qh, kvh, nhb, ml, acc, nsplit, groups, s); break;
         default: launch_split_hd<256>(qp, q2, pg, qh, kvh, nhb, ml, acc, nsplit, groups, s); break;
     }
-    hipLaunchKernelGGL(paged_attn_combine_kernel, dim3((unsigned)((int64_t)nq * qh)), dim3(64), 0,
-                       s, q2, ml, acc, (uint16_t*)out, qh, hd, nsplit);
+    hipLaunchKernelGGL(paged_attn_combine_kernel, dim3((unsigned)((int64_t)nq * qh)),
+                       dim3(kCombThreads), (size_t)nsplit * sizeof(float), s, q2, ml, acc,
+                       (uint16_t*)out, qh, hd, nsplit);
     return hipGetLastError();
 }
 
@@ -411,7 +439,7 @@ int fhip_launch_attention_paged_decode(void* output, const void* q, const int32_
                                        void* workspace, fhip_stream_t stream) {
     if (batch < 0 || max_blocks <= 0 || num_pages < 0 || page_k_bytes < 0 || page_v_bytes < 0 ||
         !paged_shape_ok(num_q_heads, num_kv_heads, head_dim) ||
-        (int64_t)max_blocks * FHIP_PAGE_TOKENS > 0x7fffffff)
+        (int64_t)max_blocks * FHIP_PAGE_TOKENS > kMaxTokens)
         return hipErrorInvalidValue;
     if (batch == 0) return hipSuccess;
     if (!output || !q || !block_table || !seq_lens || !k_pool || !v_pool || !workspace)
@@ -434,7 +462,7 @@ int fhip_launch_paged_attention(void* output, const void* q, const int* block_ta
                                 fhip_stream_t stream) {
     if (num_tokens < 0 || kv_len < 0 || start_pos < 0 || num_blocks_in_seq < 0 ||
         !paged_shape_ok(num_q_heads, num_kv_heads, head_dim) ||
-        (int64_t)num_blocks_in_seq * FHIP_PAGE_TOKENS > 0x7fffffff)
+        (int64_t)num_blocks_in_seq * FHIP_PAGE_TOKENS > kMaxTokens)
         return hipErrorInvalidValue;
     if (num_tokens == 0) return hipSuccess;
     if (!output || !q) return hipErrorInvalidValue;
