@@ -585,6 +585,8 @@ def pmc_sequence(torch, K, dev):
         seq += [(f"tq_compress_{bits}bit", comp, nbytes), (f"tq_dequant_{bits}bit", deq, nbytes)]
     fn, nb_att, _, _ = attention_inputs(torch, K, dev)
     seq.append(("attention_tq_decode", fn, nb_att))
+    fn, nb_pg, _, _ = paged_inputs(torch, K, dev)
+    seq.append(("attention_paged_decode", fn, nb_pg))
     return seq
 
 
@@ -615,6 +617,8 @@ def pmc_keys():
     pdk, pdv = a["HD"] * a["kb"] // 8, a["HD"] * a["vb"] // 8
     keys.append(("attention_tq_decode", int(lens.sum()) * a["KVH"] * (pdk + pdv + 4) +
                  a["B"] * a["QH"] * a["HD"] * 4 + a["B"] * maxb * 4))
+    keys.append(("attention_paged_decode", int(lens.sum()) * a["KVH"] * a["HD"] * 4 +
+                 2 * a["B"] * a["QH"] * a["HD"] * 2 + a["B"] * maxb * 4))
     return keys
 
 

@@ -102,6 +102,7 @@ SIGNATURES = {
     "fhip_turboquant_compress": (I, [P, TP, TP, TP, C.c_uint8, TP, TP]),
     "fhip_attention_paged_tq": (I, [P, TP, P, SZ, TP, TP, TP, TP, SZ, TP, TP, TP, TP,
                                     C.c_uint8, C.c_uint8, SZ, SZ, SZ, TP]),
+    "fhip_attention_paged": (I, [P, TP, P, SZ, TP, TP, SZ, SZ, SZ, SZ, TP]),
     "fhip_add_rmsnorm": (I, [P, TP, TP, TP, D, TP]),
     "fhip_softmax_rows": (I, [P, TP, F, TP]),
     "fhip_argmax_rows": (I, [P, TP, P, SZ]),

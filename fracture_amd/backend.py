@@ -309,6 +309,22 @@ class HipBackend:
             C.byref(k_centroids._c()), C.byref(v_centroids._c()), key_bits, value_bits,
             num_kv_heads, kv_len, start_pos, C.byref(out._c())))
 
+    def attention_paged(self, q: DeviceTensor, block_table: Sequence[int],
+                        k_blocks: Sequence[DeviceTensor], v_blocks: Sequence[DeviceTensor],
+                        num_kv_heads: int, kv_len: int, start_pos: int,
+                        out: DeviceTensor) -> None:
+        """Backend::attention_paged (backend.rs:74-88): causal GQA attention of q [T, qh, hd]
+        fp16 over the pool's [16, kvh, hd] fp16 block tensors, indexed by physical block id."""
+        bt = np.ascontiguousarray(np.asarray(block_table, dtype=np.int32))
+        n = len(k_blocks)
+        if len(v_blocks) != n:
+            raise InvalidShape("k/v block tensor lists differ in length")
+        arrs = [(_lib.FhipTensor * max(1, n))(*[t._c() for t in lst])
+                for lst in (k_blocks, v_blocks)]
+        _check(self._L.fhip_attention_paged(
+            self._h, C.byref(q._c()), bt.ctypes.data, bt.size, arrs[0], arrs[1], n,
+            num_kv_heads, kv_len, start_pos, C.byref(out._c())))
+
     # -- additive ops ---------------------------------------------------------------------------
     def add_rmsnorm(self, residual: DeviceTensor, delta: DeviceTensor, weight: DeviceTensor,
                     eps: float, normed_out: DeviceTensor) -> None:

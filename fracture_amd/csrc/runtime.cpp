@@ -948,4 +948,69 @@ int fhip_attention_paged_tq(fhip_backend* b, const fhip_tensor* q, const int32_t
     return FHIP_OK;
 }
 
+// Backend::attention_paged (backend.rs:74-88; cuda/src/backend.rs:255-345): q [T, qh, hd]
+// fp16; k_blocks / v_blocks are the pool's per-block tensors, indexed by physical block id
+// (batched.rs:92-97). The block table and the pointer arrays go through the pinned staging
+// ring instead of per-call device allocations.
+int fhip_attention_paged(fhip_backend* b, const fhip_tensor* q, const int32_t* block_table,
+                         size_t num_blocks, const fhip_tensor* k_blocks,
+                         const fhip_tensor* v_blocks, size_t pool_len, size_t num_kv_heads,
+                         size_t kv_len, size_t start_pos, const fhip_tensor* out) {
+    CHECK_B(b);
+    CHECK_T(q);
+    CHECK_T(out);
+    GET_PTR(b, q, pq);
+    GET_PTR(b, out, po);
+    if (q->ndim != 3 || q->dtype != FHIP_FP16 || out->dtype != FHIP_FP16 ||
+        numel(out) != numel(q))
+        return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged q %s out %s",
+                    shape_str(q).c_str(), shape_str(out).c_str());
+    const uint64_t T = q->shape[0], qh = q->shape[1], hd = q->shape[2];
+    if (num_kv_heads == 0 || qh % num_kv_heads != 0 ||
+        !(hd == 32 || hd == 64 || hd == 128 || hd == 256))
+        return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged: %zu q heads, %zu kv heads, "
+                    "head_dim %zu (32, 64, 128 or 256)", (size_t)qh, num_kv_heads, (size_t)hd);
+    if (kv_len > 0x7fffffffu || start_pos > 0x7fffffffu || T > 0x7fffffffu)
+        return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged: sizes beyond int32");
+    const uint64_t needed_blocks = (kv_len + FHIP_PAGE_TOKENS - 1) / FHIP_PAGE_TOKENS;
+    if (num_blocks < needed_blocks)
+        return fail(FHIP_ERR_INVALID_SHAPE, "block table has %zu blocks for kv_len %zu",
+                    num_blocks, kv_len);
+    std::vector<const void*> ptrs(2 * pool_len > 0 ? 2 * pool_len : 1, nullptr);
+    const uint64_t need = FHIP_PAGE_TOKENS * num_kv_heads * hd * 2;
+    for (size_t i = 0; i < pool_len; ++i) {
+        const fhip_tensor* ts[2] = {&k_blocks[i], &v_blocks[i]};
+        for (int k = 0; k < 2; ++k) {
+            void* p;
+            int r = b->get_ptr(ts[k]->id, &p);
+            if (r) return r;
+            if (ts[k]->dtype != FHIP_FP16 || size_bytes(ts[k]) < need)
+                return fail(FHIP_ERR_INVALID_SHAPE, "block tensor %s: need %zu fp16 bytes",
+                            shape_str(ts[k]).c_str(), (size_t)need);
+            ptrs[(size_t)k * pool_len + i] = p;
+        }
+    }
+    for (uint64_t i = 0; i < needed_blocks; ++i)
+        if (block_table[i] < 0 || (uint64_t)block_table[i] >= pool_len)
+            return fail(FHIP_ERR_INVALID_SHAPE, "block id %d outside the pool of %zu",
+                        block_table[i], pool_len);
+    if (T == 0) return FHIP_OK;
+    set_device(b);
+    std::lock_guard<std::mutex> g(b->launch_mu);
+    void *dbt, *dptr;
+    int s1, s2;
+    int r = b->stage(block_table, (needed_blocks ? needed_blocks : 1) * sizeof(int32_t), &dbt, &s1);
+    if (r) return r;
+    r = b->stage(ptrs.data(), ptrs.size() * sizeof(void*), &dptr, &s2);
+    if (r) return r;
+    const void** dp = (const void**)dptr;
+    int e = fhip_launch_paged_attention(po, pq, (const int*)dbt, dp, dp + pool_len, (int)T,
+                                        (int)qh, (int)num_kv_heads, (int)hd, (int)kv_len,
+                                        (int)start_pos, (int)needed_blocks, b->stream);
+    b->stage_done(s1);
+    b->stage_done(s2);
+    if (e != hipSuccess) return hip_fail((hipError_t)e);
+    return FHIP_OK;
+}
+
 }  // extern "C"

@@ -337,6 +337,13 @@ int fhip_attention_paged_tq(fhip_backend* b, const fhip_tensor* q, const int32_t
                             uint8_t key_bits, uint8_t value_bits, size_t num_kv_heads,
                             size_t kv_len, size_t start_pos, const fhip_tensor* out);
 
+/* Backend::attention_paged (backend.rs:74-88): q [T, qh, hd] fp16; the two per-block tensor
+ * lists are arrays of pool_len [16, kvh, hd] fp16 tensors indexed by physical block id. */
+int fhip_attention_paged(fhip_backend* b, const fhip_tensor* q, const int32_t* block_table,
+                         size_t num_blocks, const fhip_tensor* k_blocks,
+                         const fhip_tensor* v_blocks, size_t pool_len, size_t num_kv_heads,
+                         size_t kv_len, size_t start_pos, const fhip_tensor* out);
+
 /* --- additive handle ops --------------------------------------------------------------- */
 
 /* Fused residual add + RMSNorm: residual += delta (in place), normed_out = rmsnorm(residual). */

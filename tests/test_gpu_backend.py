@@ -262,3 +262,33 @@ def test_attention_paged_tq_through_trait(backend):
                                    vb, kvh, kv_len, kv_len - 1, out)
     for t in kps + kns + vps + vns + [tq_, out, tkr, tvr, tkc, tvc]:
         backend.free(t)
+
+
+def test_attention_paged_through_trait(backend):
+    """FP16 pool blocks as PagedKvCacheManager hands them to the backend
+    (crates/fracture-engine/src/batched.rs:92-109): prefill of 5 tokens at start_pos 45."""
+    rng = np.random.default_rng(5)
+    qh, kvh, hd = 8, 2, 64
+    kv_len, T = 50, 5
+    pool = 6
+    table = [4, 0, 5, 2]
+    KP = rng.standard_normal((pool, 16, kvh, hd)).astype(np.float16)
+    VP = rng.standard_normal((pool, 16, kvh, hd)).astype(np.float16)
+    kbs = [backend.upload(KP[i]) for i in range(pool)]
+    vbs = [backend.upload(VP[i]) for i in range(pool)]
+    q = rng.standard_normal((T, qh, hd)).astype(np.float16)
+    tq_ = up16(backend, q)
+    out = backend.alloc([T, qh, hd], DType.FP16)
+    backend.attention_paged(tq_, table, kbs, vbs, kvh, kv_len, kv_len - T, out)
+    got = backend.download(out)
+    for t in range(T):
+        want = oracle.paged_attention(q[t], np.array(table, np.int32), kv_len - T + t + 1, KP,
+                                      VP, kvh)
+        assert_close(got[t].astype(np.float32), want.astype(np.float32), 1e-3, 1e-3,
+                     f"attention_paged token {t}")
+    with pytest.raises(InvalidShape, match="block id"):
+        backend.attention_paged(tq_, [4, 0, 9, 2], kbs, vbs, kvh, kv_len, kv_len - T, out)
+    with pytest.raises(InvalidShape, match="block table"):
+        backend.attention_paged(tq_, [4, 0], kbs, vbs, kvh, kv_len, kv_len - T, out)
+    for t in kbs + vbs + [tq_, out]:
+        backend.free(t)
