@@ -46,6 +46,7 @@ SIGNATURES = {
     "fhip_launch_attention_paged_tq": (I, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I,
                                            I, I, I, I, P]),
     "fhip_launch_paged_attention": (I, [P, P, P, P, P, I, I, I, I, I, I, I, P]),
+    "fhip_launch_matmul": (I, [P, P, P, I, I, I, P]),
     # additive raw launchers
     "fhip_launch_rmsnorm_ex": (I, [P, P, P, F, I, I, I, P]),
     "fhip_launch_add_ex": (I, [P, P, P, I64, I, P]),
@@ -103,6 +104,7 @@ SIGNATURES = {
     "fhip_attention_paged_tq": (I, [P, TP, P, SZ, TP, TP, TP, TP, SZ, TP, TP, TP, TP,
                                     C.c_uint8, C.c_uint8, SZ, SZ, SZ, TP]),
     "fhip_attention_paged": (I, [P, TP, P, SZ, TP, TP, SZ, SZ, SZ, SZ, TP]),
+    "fhip_matmul": (I, [P, TP, TP, TP]),
     "fhip_add_rmsnorm": (I, [P, TP, TP, TP, D, TP]),
     "fhip_softmax_rows": (I, [P, TP, F, TP]),
     "fhip_argmax_rows": (I, [P, TP, P, SZ]),

@@ -208,9 +208,6 @@ class HipBackend:
         _check(self._L.fhip_copy_to_host(self._h, C.byref(src._c()), p, n))
 
     # -- compute (trait) ----------------------------------------------------------------------
-    def matmul(self, a: DeviceTensor, b: DeviceTensor, out: DeviceTensor) -> None:
-        raise BackendError("matmul not supported by this backend")
-
     def rmsnorm(self, input: DeviceTensor, weight: DeviceTensor, eps: float,
                 out: DeviceTensor) -> None:
         _check(self._L.fhip_rmsnorm(self._h, C.byref(input._c()), C.byref(weight._c()), eps,
@@ -224,9 +221,6 @@ class HipBackend:
 
     def attention(self, *args, **kwargs) -> None:
         raise BackendError("attention not supported by this backend")
-
-    def attention_paged(self, *args, **kwargs) -> None:
-        raise BackendError("paged attention not supported by this backend")
 
     def silu_mul(self, gate: DeviceTensor, up: DeviceTensor, out: DeviceTensor) -> None:
         _check(self._L.fhip_silu_mul(self._h, C.byref(gate._c()), C.byref(up._c()),
@@ -308,6 +302,12 @@ class HipBackend:
             arrs[3], n, C.byref(k_rotation._c()), C.byref(v_rotation._c()),
             C.byref(k_centroids._c()), C.byref(v_centroids._c()), key_bits, value_bits,
             num_kv_heads, kv_len, start_pos, C.byref(out._c())))
+
+    def matmul(self, a: DeviceTensor, b: DeviceTensor, out: DeviceTensor) -> None:
+        """Backend::matmul as the CUDA backend implements it (cuda/src/backend.rs:75-128):
+        out[M, N] = a[M, K] @ b[N, K]^T in fp16 with fp32 accumulation."""
+        _check(self._L.fhip_matmul(self._h, C.byref(a._c()), C.byref(b._c()),
+                                   C.byref(out._c())))
 
     def attention_paged(self, q: DeviceTensor, block_table: Sequence[int],
                         k_blocks: Sequence[DeviceTensor], v_blocks: Sequence[DeviceTensor],

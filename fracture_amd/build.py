@@ -37,7 +37,7 @@ PER_FILE = {
     "tq_host.cpp": ["-ffp-contract=off"],
 }
 SOURCES = ["elementwise.hip", "reduce.hip", "turboquant.hip", "attention_tq.hip",
-           "attention_paged.hip",
+           "attention_paged.hip", "matmul.cpp",
            "tq_host.cpp", "runtime.cpp"]
 
 _NOISE = "'-packed-fp32-ops' is not a recognized feature for this target"
@@ -68,7 +68,7 @@ def build(jobs: int | None = None, verbose: bool = True) -> Path:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
-           *map(str, objs), "-ldl"]
+           *map(str, objs), "-lrocblas", "-ldl"]
     p = subprocess.run(cmd, capture_output=True, text=True)
     if p.returncode != 0:
         raise RuntimeError("link failed:\n" + _clean(p.stdout + p.stderr))

@@ -431,6 +431,38 @@ int fhip_rmsnorm(fhip_backend* b, const fhip_tensor* input, const fhip_tensor* w
                                                 input->dtype, b->stream));
 }
 
+// Backend::matmul (cuda/src/backend.rs:75-128): out = a · bᵀ, a [M, K], b [N, K], out [M, N].
+int fhip_matmul(fhip_backend* b, const fhip_tensor* a, const fhip_tensor* bm,
+                const fhip_tensor* out) {
+    CHECK_B(b);
+    CHECK_T(a);
+    CHECK_T(bm);
+    CHECK_T(out);
+    GET_PTR(b, a, pa);
+    GET_PTR(b, bm, pb);
+    GET_PTR(b, out, pc);
+    if (a->ndim != 2 || bm->ndim != 2)
+        return fail(FHIP_ERR_INVALID_SHAPE, "matmul: A %s and B %s must be 2-D",
+                    shape_str(a).c_str(), shape_str(bm).c_str());
+    if (a->shape[1] != bm->shape[1])
+        return fail(FHIP_ERR_INVALID_SHAPE,
+                    "matmul: A inner dim %llu != B inner dim %llu (A is %s, B is %s)",
+                    (unsigned long long)a->shape[1], (unsigned long long)bm->shape[1],
+                    shape_str(a).c_str(), shape_str(bm).c_str());
+    const uint64_t M = a->shape[0], K = a->shape[1], N = bm->shape[0];
+    if (a->dtype != FHIP_FP16 || bm->dtype != FHIP_FP16 || out->dtype != FHIP_FP16)
+        return fail(FHIP_ERR_UNSUPPORTED_DTYPE, "matmul is fp16 (A %s, B %s, out %s)",
+                    dtype_name(a->dtype), dtype_name(bm->dtype), dtype_name(out->dtype));
+    if (numel(out) != M * N)
+        return fail(FHIP_ERR_INVALID_SHAPE, "matmul: out %s for a [%llu, %llu] result",
+                    shape_str(out).c_str(), (unsigned long long)M, (unsigned long long)N);
+    if (M > 0x7fffffffu || N > 0x7fffffffu || K > 0x7fffffffu)
+        return fail(FHIP_ERR_INVALID_SHAPE, "matmul: dimensions beyond int32");
+    if (M == 0 || N == 0) return FHIP_OK;
+    set_device(b);
+    return launch_result(fhip_launch_matmul(pc, pa, pb, (int)M, (int)N, (int)K, b->stream));
+}
+
 int fhip_add_rmsnorm(fhip_backend* b, const fhip_tensor* residual, const fhip_tensor* delta,
                      const fhip_tensor* weight, double eps, const fhip_tensor* normed_out) {
     CHECK_B(b);

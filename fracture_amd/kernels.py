@@ -406,3 +406,14 @@ def paged_attention(out: torch.Tensor, q: torch.Tensor, block_table: torch.Tenso
     _ok(_L().fhip_launch_paged_attention(
         _p(out), _p(q), _p(block_table), _p(k_block_ptrs), _p(v_block_ptrs), T, qh,
         num_kv_heads, hd, kv_len, start_pos, block_table.numel(), _stream()), "paged_attention")
+
+
+def matmul(c: torch.Tensor, a: torch.Tensor, b: torch.Tensor) -> None:
+    """c[M, N] = a[M, K] @ b[N, K]^T, fp16 in and out, fp32 accumulation
+    (CudaBackend::matmul, cuda/src/backend.rs:75-128)."""
+    _dev(c, a, b)
+    _need(a.dtype == b.dtype == c.dtype == torch.float16, "fp16 operands")
+    _need(a.dim() == 2 and b.dim() == 2 and a.shape[1] == b.shape[1] and
+          tuple(c.shape) == (a.shape[0], b.shape[0]), "shapes")
+    _ok(_L().fhip_launch_matmul(_p(c), _p(a), _p(b), a.shape[0], b.shape[0], a.shape[1],
+                                _stream()), "matmul")

@@ -125,6 +125,11 @@ int fhip_launch_paged_attention(void* output, const void* q, const int* block_ta
                                 int kv_len, int start_pos, int num_blocks_in_seq,
                                 fhip_stream_t stream);
 
+/* The GEMM of CudaBackend::matmul (cuda/src/backend.rs:75-128), which calls cuBLAS directly:
+ * C[M, N] = A[M, K] · B[N, K]^T, row-major fp16 operands, fp32 accumulation, on the stream. */
+int fhip_launch_matmul(void* c, const void* a, const void* b, int m, int n, int k,
+                       fhip_stream_t stream);
+
 /* --- additive raw launchers ---------------------------------------------------------- */
 
 /* dtype-generic forms of rmsnorm / add / silu_mul (FHIP_FP16, FHIP_BF16, FHIP_FP32). */
@@ -336,6 +341,11 @@ int fhip_attention_paged_tq(fhip_backend* b, const fhip_tensor* q, const int32_t
                             const fhip_tensor* k_centroids, const fhip_tensor* v_centroids,
                             uint8_t key_bits, uint8_t value_bits, size_t num_kv_heads,
                             size_t kv_len, size_t start_pos, const fhip_tensor* out);
+
+/* Backend::matmul (backend.rs:25-27; cuda/src/backend.rs:75-128): out[M, N] = a[M, K] · b[N, K]^T,
+ * fp16; a.shape[1] != b.shape[1] is InvalidShape. */
+int fhip_matmul(fhip_backend* b, const fhip_tensor* a, const fhip_tensor* bm,
+                const fhip_tensor* out);
 
 /* Backend::attention_paged (backend.rs:74-88): q [T, qh, hd] fp16; the two per-block tensor
  * lists are arrays of pool_len [16, kvh, hd] fp16 tensors indexed by physical block id. */

@@ -4,9 +4,9 @@ Reads (as data, nothing is executed or imported from the reference):
   * tests/reference-fixture/{prompt_0,prompt_1,decode_step_0}/**.bin — PyTorch per-op dumps
     in the reference's tensor format (tests/validation/src/tensor_compare.rs:68-121:
     u32 ndim, u32 shape[ndim], u32 dtype, little-endian data);
-  * tests/fixtures/tiny-llama.gguf — the F16 tiny model; only the norm weights and the
-    token embedding table are extracted (GGUF v3 container: header, metadata, tensor infos,
-    aligned data section).
+  * tests/fixtures/tiny-llama.gguf — the F16 tiny model: every weight tensor (norms, token
+    embedding, attention and FFN projections, output head) is extracted (GGUF v3 container:
+    header, metadata, tensor infos, aligned data section).
 
 The reference tree lives at /root/reference in the build container; pass another path as
 the first argument. The .npz (a few MB at most) is what the tests load.
@@ -23,7 +23,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 OUT = HERE / "tiny_llama_fixture.npz"
 CASES = ["prompt_0", "prompt_1", "decode_step_0"]
-PER_LAYER = ["input_hidden", "post_attn_norm", "q", "k", "q_rope", "k_rope", "attn_output",
+PER_LAYER = ["input_hidden", "post_attn_norm", "q", "k", "v", "q_rope", "k_rope", "attn_output",
              "post_attn_residual", "post_ffn_norm", "gate", "up", "silu_mul", "ffn_output",
              "output_hidden"]
 TOP = ["token_ids", "embeddings", "final_norm", "logits", "greedy_token"]
@@ -123,9 +123,11 @@ def main(ref_root: Path) -> None:
         for layer in range(cfg["num_layers"]):
             for t in PER_LAYER:
                 arrays[f"{case}/layer_{layer:02d}/{t}"] = read_bin(d / f"layer_{layer:02d}" / f"{t}.bin")
-    names = ["token_embd.weight", "output_norm.weight"]
+    names = ["token_embd.weight", "output_norm.weight", "output.weight"]
     for layer in range(cfg["num_layers"]):
-        names += [f"blk.{layer}.attn_norm.weight", f"blk.{layer}.ffn_norm.weight"]
+        names += [f"blk.{layer}.{t}.weight" for t in
+                  ("attn_norm", "ffn_norm", "attn_q", "attn_k", "attn_v", "attn_output",
+                   "ffn_gate", "ffn_up", "ffn_down")]
     w = read_gguf_tensors(ref_root / "tests" / "fixtures" / "tiny-llama.gguf", set(names))
     for n in names:
         arrays[f"weights/{n}"] = w[n]
