@@ -105,6 +105,11 @@ SIGNATURES = {
                                     C.c_uint8, C.c_uint8, SZ, SZ, SZ, TP]),
     "fhip_attention_paged": (I, [P, TP, P, SZ, TP, TP, SZ, SZ, SZ, SZ, TP]),
     "fhip_matmul": (I, [P, TP, TP, TP]),
+    "fhip_page_pool_create": (I, [P, TP, SZ, SZ, C.POINTER(U64)]),
+    "fhip_page_pool_destroy": (I, [P, U64]),
+    "fhip_attention_paged_pool": (I, [P, TP, P, SZ, U64, SZ, SZ, SZ, TP]),
+    "fhip_attention_paged_tq_pool": (I, [P, TP, P, SZ, U64, TP, TP, TP, TP, C.c_uint8,
+                                         C.c_uint8, SZ, SZ, SZ, TP]),
     "fhip_add_rmsnorm": (I, [P, TP, TP, TP, D, TP]),
     "fhip_softmax_rows": (I, [P, TP, F, TP]),
     "fhip_argmax_rows": (I, [P, TP, P, SZ]),

@@ -325,6 +325,42 @@ class HipBackend:
             self._h, C.byref(q._c()), bt.ctypes.data, bt.size, arrs[0], arrs[1], n,
             num_kv_heads, kv_len, start_pos, C.byref(out._c())))
 
+    # -- registered page pools ------------------------------------------------------------------
+    def page_pool_create(self, *block_lists: Sequence[DeviceTensor]) -> int:
+        """Keep a KV pool's block addresses in device memory: lists (K, V) for
+        attention_paged_pool, (K packed, K norms, V packed, V norms) for
+        attention_paged_tq_pool. The tensors must outlive the pool."""
+        n = len(block_lists[0]) if block_lists else 0
+        if not block_lists or any(len(l) != n for l in block_lists):
+            raise InvalidShape("block lists differ in length")
+        flat = [t._c() for lst in block_lists for t in lst]
+        arr = (_lib.FhipTensor * max(1, len(flat)))(*flat)
+        h = C.c_uint64()
+        _check(self._L.fhip_page_pool_create(self._h, arr, len(block_lists), n, C.byref(h)))
+        return h.value
+
+    def page_pool_destroy(self, pool: int) -> None:
+        _check(self._L.fhip_page_pool_destroy(self._h, pool))
+
+    def attention_paged_pool(self, q: DeviceTensor, block_table: Sequence[int], pool: int,
+                             num_kv_heads: int, kv_len: int, start_pos: int,
+                             out: DeviceTensor) -> None:
+        bt = np.ascontiguousarray(np.asarray(block_table, dtype=np.int32))
+        _check(self._L.fhip_attention_paged_pool(self._h, C.byref(q._c()), bt.ctypes.data,
+                                                 bt.size, pool, num_kv_heads, kv_len, start_pos,
+                                                 C.byref(out._c())))
+
+    def attention_paged_tq_pool(self, q: DeviceTensor, block_table: Sequence[int], pool: int,
+                                k_rotation: DeviceTensor, v_rotation: DeviceTensor,
+                                k_centroids: DeviceTensor, v_centroids: DeviceTensor,
+                                key_bits: int, value_bits: int, num_kv_heads: int, kv_len: int,
+                                start_pos: int, out: DeviceTensor) -> None:
+        bt = np.ascontiguousarray(np.asarray(block_table, dtype=np.int32))
+        _check(self._L.fhip_attention_paged_tq_pool(
+            self._h, C.byref(q._c()), bt.ctypes.data, bt.size, pool, C.byref(k_rotation._c()),
+            C.byref(v_rotation._c()), C.byref(k_centroids._c()), C.byref(v_centroids._c()),
+            key_bits, value_bits, num_kv_heads, kv_len, start_pos, C.byref(out._c())))
+
     # -- additive ops ---------------------------------------------------------------------------
     def add_rmsnorm(self, residual: DeviceTensor, delta: DeviceTensor, weight: DeviceTensor,
                     eps: float, normed_out: DeviceTensor) -> None:

@@ -14,6 +14,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+#include <cstdint>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -150,6 +152,16 @@ struct fhip_backend {
     size_t ws_cap = 0;
     hipEvent_t ws_ev = nullptr;
     bool ws_pending = false;
+    // registered KV page pools: device-resident arrays of the pool's per-block addresses
+    struct PagePool {
+        const void** dev = nullptr;          // nlists * pool_len addresses, list-major
+        size_t pool_len = 0;
+        int nlists = 0;
+        std::vector<uint64_t> min_bytes;     // smallest block tensor of each list
+        std::vector<int32_t> dtype;          // each list's dtype (-1: mixed)
+    };
+    std::unordered_map<uint64_t, PagePool> pools;  // under mu
+    uint64_t next_pool = 1;
 
     int get_ptr(uint64_t id, void** out) {
         std::lock_guard<std::mutex> g(mu);
@@ -282,6 +294,7 @@ void fhip_backend_destroy(fhip_backend* b) {
     }
     if (b->workspace) (void)hipFree(b->workspace);
     if (b->ws_ev) (void)hipEventDestroy(b->ws_ev);
+    for (auto& kv : b->pools) (void)hipFree((void*)kv.second.dev);
     if (b->rope_freq) (void)hipFree(b->rope_freq);
     (void)hipStreamDestroy(b->stream);
     delete b;
@@ -976,6 +989,216 @@ int fhip_attention_paged_tq(fhip_backend* b, const fhip_tensor* q, const int32_t
         (int)vpd, b->stream);
     b->stage_done(s1);
     b->stage_done(s2);
+    if (e != hipSuccess) return hip_fail((hipError_t)e);
+    return FHIP_OK;
+}
+
+// ---------------------------------------------------------------------------------------
+// Registered page pools. The cache managers allocate their block pools once
+// (paged_kv_cache.rs, quantized_paged_kv_cache.rs:82-133) and hand every attention call the
+// whole pool's tensor lists; the reference copies pool_len pointers to a fresh device
+// allocation on every call (cuda/src/backend.rs:295-315, 625-671). A registered pool keeps
+// those addresses in device memory, so a call stages only its block table. The pool's
+// tensors must stay allocated until the pool is destroyed.
+// ---------------------------------------------------------------------------------------
+int fhip_page_pool_create(fhip_backend* b, const fhip_tensor* blocks, size_t nlists,
+                          size_t pool_len, uint64_t* pool_out) {
+    CHECK_B(b);
+    if (!pool_out || nlists == 0 || nlists > 8 || pool_len == 0 || !blocks)
+        return fail(FHIP_ERR_INVALID_SHAPE, "page pool: %zu lists of %zu blocks", nlists,
+                    pool_len);
+    *pool_out = 0;
+    fhip_backend::PagePool pp;
+    pp.pool_len = pool_len;
+    pp.nlists = (int)nlists;
+    pp.min_bytes.assign(nlists, UINT64_MAX);
+    pp.dtype.assign(nlists, -2);
+    std::vector<const void*> ptrs(nlists * pool_len);
+    for (size_t l = 0; l < nlists; ++l)
+        for (size_t i = 0; i < pool_len; ++i) {
+            const fhip_tensor* t = &blocks[l * pool_len + i];
+            void* p;
+            int r = b->get_ptr(t->id, &p);
+            if (r) return r;
+            ptrs[l * pool_len + i] = p;
+            pp.min_bytes[l] = std::min<uint64_t>(pp.min_bytes[l], size_bytes(t));
+            pp.dtype[l] = pp.dtype[l] == -2 || pp.dtype[l] == t->dtype ? t->dtype : -1;
+        }
+    set_device(b);
+    void* dev = nullptr;
+    HIP_TRY(hipMalloc(&dev, ptrs.size() * sizeof(void*)));
+    hipError_t e = hipMemcpy(dev, ptrs.data(), ptrs.size() * sizeof(void*),
+                             hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(dev);
+        return hip_fail(e);
+    }
+    pp.dev = (const void**)dev;
+    std::lock_guard<std::mutex> g(b->mu);
+    const uint64_t id = b->next_pool++;
+    b->pools.emplace(id, std::move(pp));
+    *pool_out = id;
+    return FHIP_OK;
+}
+
+int fhip_page_pool_destroy(fhip_backend* b, uint64_t pool) {
+    CHECK_B(b);
+    const void** dev = nullptr;
+    {
+        std::lock_guard<std::mutex> g(b->mu);
+        auto it = b->pools.find(pool);
+        if (it == b->pools.end())
+            return fail(FHIP_ERR_TENSOR_NOT_FOUND, "page pool %llu", (unsigned long long)pool);
+        dev = it->second.dev;
+        b->pools.erase(it);
+    }
+    set_device(b);
+    // calls already enqueued may still read the addresses
+    HIP_TRY(hipStreamSynchronize(b->stream));
+    HIP_TRY(hipFree((void*)dev));
+    return FHIP_OK;
+}
+
+// The pool with `nlists` lists whose list l holds blocks of at least need[l] bytes of dtype
+// dt[l] (dt -1: any), or an error.
+static int find_pool(fhip_backend* b, uint64_t pool, int nlists, const uint64_t* need,
+                     const int32_t* dt, fhip_backend::PagePool* out) {
+    std::lock_guard<std::mutex> g(b->mu);
+    auto it = b->pools.find(pool);
+    if (it == b->pools.end())
+        return fail(FHIP_ERR_TENSOR_NOT_FOUND, "page pool %llu", (unsigned long long)pool);
+    const auto& pp = it->second;
+    if (pp.nlists != nlists)
+        return fail(FHIP_ERR_INVALID_SHAPE, "page pool %llu has %d block lists, need %d",
+                    (unsigned long long)pool, pp.nlists, nlists);
+    for (int l = 0; l < nlists; ++l) {
+        if (pp.min_bytes[l] < need[l])
+            return fail(FHIP_ERR_INVALID_SHAPE,
+                        "page pool list %d: blocks of %llu bytes, need %llu", l,
+                        (unsigned long long)pp.min_bytes[l], (unsigned long long)need[l]);
+        if (dt[l] >= 0 && pp.dtype[l] != dt[l])
+            return fail(FHIP_ERR_INVALID_SHAPE, "page pool list %d: dtype %s", l,
+                        dtype_name(pp.dtype[l] >= 0 ? pp.dtype[l] : -1));
+    }
+    *out = pp;
+    return FHIP_OK;
+}
+
+// Backend::attention_paged over a registered pool of (K blocks, V blocks).
+int fhip_attention_paged_pool(fhip_backend* b, const fhip_tensor* q, const int32_t* block_table,
+                              size_t num_blocks, uint64_t pool, size_t num_kv_heads,
+                              size_t kv_len, size_t start_pos, const fhip_tensor* out) {
+    CHECK_B(b);
+    CHECK_T(q);
+    CHECK_T(out);
+    GET_PTR(b, q, pq);
+    GET_PTR(b, out, po);
+    if (q->ndim != 3 || q->dtype != FHIP_FP16 || out->dtype != FHIP_FP16 ||
+        numel(out) != numel(q))
+        return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged q %s out %s",
+                    shape_str(q).c_str(), shape_str(out).c_str());
+    const uint64_t T = q->shape[0], qh = q->shape[1], hd = q->shape[2];
+    if (num_kv_heads == 0 || qh % num_kv_heads != 0 ||
+        !(hd == 32 || hd == 64 || hd == 128 || hd == 256))
+        return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged: %zu q heads, %zu kv heads, "
+                    "head_dim %zu (32, 64, 128 or 256)", (size_t)qh, num_kv_heads, (size_t)hd);
+    if (kv_len > 0x7fffffffu || start_pos > 0x7fffffffu || T > 0x7fffffffu)
+        return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged: sizes beyond int32");
+    const uint64_t needed_blocks = (kv_len + FHIP_PAGE_TOKENS - 1) / FHIP_PAGE_TOKENS;
+    if (num_blocks < needed_blocks)
+        return fail(FHIP_ERR_INVALID_SHAPE, "block table has %zu blocks for kv_len %zu",
+                    num_blocks, kv_len);
+    const uint64_t need = FHIP_PAGE_TOKENS * num_kv_heads * hd * 2;
+    const uint64_t needs[2] = {need, need};
+    const int32_t dts[2] = {FHIP_FP16, FHIP_FP16};
+    fhip_backend::PagePool pp;
+    int r = find_pool(b, pool, 2, needs, dts, &pp);
+    if (r) return r;
+    for (uint64_t i = 0; i < needed_blocks; ++i)
+        if (block_table[i] < 0 || (uint64_t)block_table[i] >= pp.pool_len)
+            return fail(FHIP_ERR_INVALID_SHAPE, "block id %d outside the pool of %zu",
+                        block_table[i], pp.pool_len);
+    if (T == 0) return FHIP_OK;
+    set_device(b);
+    std::lock_guard<std::mutex> g(b->launch_mu);
+    void* dbt;
+    int s1;
+    r = b->stage(block_table, (needed_blocks ? needed_blocks : 1) * sizeof(int32_t), &dbt, &s1);
+    if (r) return r;
+    int e = fhip_launch_paged_attention(po, pq, (const int*)dbt, pp.dev, pp.dev + pp.pool_len,
+                                        (int)T, (int)qh, (int)num_kv_heads, (int)hd,
+                                        (int)kv_len, (int)start_pos, (int)needed_blocks,
+                                        b->stream);
+    b->stage_done(s1);
+    if (e != hipSuccess) return hip_fail((hipError_t)e);
+    return FHIP_OK;
+}
+
+// Backend::attention_paged_tq over a registered pool of (K packed, K norms, V packed, V norms).
+int fhip_attention_paged_tq_pool(fhip_backend* b, const fhip_tensor* q,
+                                 const int32_t* block_table, size_t num_blocks, uint64_t pool,
+                                 const fhip_tensor* k_rotation, const fhip_tensor* v_rotation,
+                                 const fhip_tensor* k_centroids, const fhip_tensor* v_centroids,
+                                 uint8_t key_bits, uint8_t value_bits, size_t num_kv_heads,
+                                 size_t kv_len, size_t start_pos, const fhip_tensor* out) {
+    CHECK_B(b);
+    CHECK_T(q);
+    CHECK_T(k_rotation);
+    CHECK_T(v_rotation);
+    CHECK_T(k_centroids);
+    CHECK_T(v_centroids);
+    CHECK_T(out);
+    GET_PTR(b, q, pq);
+    GET_PTR(b, out, po);
+    GET_PTR(b, k_rotation, pkr);
+    GET_PTR(b, v_rotation, pvr);
+    GET_PTR(b, k_centroids, pkc);
+    GET_PTR(b, v_centroids, pvc);
+    if (q->ndim != 3 || q->dtype != FHIP_FP16 || out->dtype != FHIP_FP16 ||
+        numel(out) != numel(q))
+        return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged_tq q %s out %s",
+                    shape_str(q).c_str(), shape_str(out).c_str());
+    const uint64_t T = q->shape[0], qh = q->shape[1], hd = q->shape[2];
+    if (num_kv_heads == 0 || qh % num_kv_heads != 0 || key_bits < 1 || key_bits > 8 ||
+        value_bits < 1 || value_bits > 8 || numel(k_rotation) != hd * hd ||
+        numel(v_rotation) != hd * hd || numel(k_centroids) < (1ull << key_bits) ||
+        numel(v_centroids) < (1ull << value_bits))
+        return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged_tq arguments");
+    if (kv_len > 0x7fffffffu || start_pos > 0x7fffffffu || T > 0x7fffffffu)
+        return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged_tq: sizes beyond int32");
+    const uint64_t needed_blocks = (kv_len + FHIP_PAGE_TOKENS - 1) / FHIP_PAGE_TOKENS;
+    if (num_blocks < needed_blocks)
+        return fail(FHIP_ERR_INVALID_SHAPE, "block table has %zu blocks for kv_len %zu",
+                    num_blocks, kv_len);
+    const uint64_t kpd = fhip_tq_packed_dim_per_head(hd, key_bits);
+    const uint64_t vpd = fhip_tq_packed_dim_per_head(hd, value_bits);
+    const uint64_t needs[4] = {FHIP_PAGE_TOKENS * num_kv_heads * kpd,
+                               FHIP_PAGE_TOKENS * num_kv_heads * 2,
+                               FHIP_PAGE_TOKENS * num_kv_heads * vpd,
+                               FHIP_PAGE_TOKENS * num_kv_heads * 2};
+    const int32_t dts[4] = {-1, -1, -1, -1};
+    fhip_backend::PagePool pp;
+    int r = find_pool(b, pool, 4, needs, dts, &pp);
+    if (r) return r;
+    for (uint64_t i = 0; i < needed_blocks; ++i)
+        if (block_table[i] < 0 || (uint64_t)block_table[i] >= pp.pool_len)
+            return fail(FHIP_ERR_INVALID_SHAPE, "block id %d outside the pool of %zu",
+                        block_table[i], pp.pool_len);
+    if (T == 0) return FHIP_OK;
+    set_device(b);
+    std::lock_guard<std::mutex> g(b->launch_mu);
+    void* dbt;
+    int s1;
+    r = b->stage(block_table, (needed_blocks ? needed_blocks : 1) * sizeof(int32_t), &dbt, &s1);
+    if (r) return r;
+    const void** dp = pp.dev;
+    const size_t n = pp.pool_len;
+    int e = fhip_launch_attention_paged_tq(
+        po, pq, (const int*)dbt, dp, dp + n, dp + 2 * n, dp + 3 * n, (const float*)pkr,
+        (const float*)pvr, (const float*)pkc, (const float*)pvc, (int)T, (int)qh,
+        (int)num_kv_heads, (int)hd, (int)kv_len, (int)start_pos, key_bits, value_bits, (int)kpd,
+        (int)vpd, b->stream);
+    b->stage_done(s1);
     if (e != hipSuccess) return hip_fail((hipError_t)e);
     return FHIP_OK;
 }

@@ -354,6 +354,25 @@ int fhip_attention_paged(fhip_backend* b, const fhip_tensor* q, const int32_t* b
                          const fhip_tensor* v_blocks, size_t pool_len, size_t num_kv_heads,
                          size_t kv_len, size_t start_pos, const fhip_tensor* out);
 
+/* Registered KV page pools (no counterpart in the reference, which copies the pool's block
+ * addresses to a fresh device allocation on every attention call, cuda/src/backend.rs:295-315,
+ * 625-671): `blocks` holds nlists lists of pool_len block tensors, list-major — (K, V) for
+ * fhip_attention_paged_pool, (K packed, K norms, V packed, V norms) for
+ * fhip_attention_paged_tq_pool. The addresses stay in device memory, so each call stages only
+ * its block table. The tensors must stay allocated until the pool is destroyed. */
+int fhip_page_pool_create(fhip_backend* b, const fhip_tensor* blocks, size_t nlists,
+                          size_t pool_len, uint64_t* pool_out);
+int fhip_page_pool_destroy(fhip_backend* b, uint64_t pool);
+int fhip_attention_paged_pool(fhip_backend* b, const fhip_tensor* q, const int32_t* block_table,
+                              size_t num_blocks, uint64_t pool, size_t num_kv_heads,
+                              size_t kv_len, size_t start_pos, const fhip_tensor* out);
+int fhip_attention_paged_tq_pool(fhip_backend* b, const fhip_tensor* q,
+                                 const int32_t* block_table, size_t num_blocks, uint64_t pool,
+                                 const fhip_tensor* k_rotation, const fhip_tensor* v_rotation,
+                                 const fhip_tensor* k_centroids, const fhip_tensor* v_centroids,
+                                 uint8_t key_bits, uint8_t value_bits, size_t num_kv_heads,
+                                 size_t kv_len, size_t start_pos, const fhip_tensor* out);
+
 /* --- additive handle ops --------------------------------------------------------------- */
 
 /* Fused residual add + RMSNorm: residual += delta (in place), normed_out = rmsnorm(residual). */

@@ -292,3 +292,57 @@ def test_attention_paged_through_trait(backend):
         backend.attention_paged(tq_, [4, 0], kbs, vbs, kvh, kv_len, kv_len - T, out)
     for t in kbs + vbs + [tq_, out]:
         backend.free(t)
+
+
+def test_registered_page_pools(backend):
+    """fhip_page_pool_create: pooled attention gives the per-call entries' exact outputs and
+    stages only the block table; wrong pools are refused on the host."""
+    rng = np.random.default_rng(6)
+    qh, kvh, hd = 8, 2, 128
+    kv_len, T = 70, 3
+    pool = 7
+    table = [5, 0, 6, 2, 3]
+    KP = rng.standard_normal((pool, 16, kvh, hd)).astype(np.float16)
+    VP = rng.standard_normal((pool, 16, kvh, hd)).astype(np.float16)
+    kbs = [backend.upload(KP[i]) for i in range(pool)]
+    vbs = [backend.upload(VP[i]) for i in range(pool)]
+    q = rng.standard_normal((T, qh, hd)).astype(np.float16)
+    tq_ = up16(backend, q)
+    o1 = backend.alloc([T, qh, hd], DType.FP16)
+    o2 = backend.alloc([T, qh, hd], DType.FP16)
+    backend.attention_paged(tq_, table, kbs, vbs, kvh, kv_len, kv_len - T, o1)
+    h = backend.page_pool_create(kbs, vbs)
+    backend.attention_paged_pool(tq_, table, h, kvh, kv_len, kv_len - T, o2)
+    assert np.array_equal(backend.download(o1), backend.download(o2))
+    with pytest.raises(InvalidShape, match="block id"):
+        backend.attention_paged_pool(tq_, [5, 0, 9, 2, 3], h, kvh, kv_len, kv_len - T, o2)
+
+    # TurboQuant pool: (K packed, K norms, V packed, V norms)
+    kb, vb = 4, 2
+    pdk, pdv = oracle.packed_dim(hd, kb), oracle.packed_dim(hd, vb)
+    lists = [rng.integers(0, 256, (pool, 16, kvh * pdk)).astype(np.uint8),
+             np.full((pool, 16, kvh), np.float16(2.0)),
+             rng.integers(0, 256, (pool, 16, kvh * pdv)).astype(np.uint8),
+             np.full((pool, 16, kvh), np.float16(3.0))]
+    tls = [[backend.upload(a[i]) for i in range(pool)] for a in lists]
+    krot, vrot = tq.rotation_matrix(hd, 42), tq.rotation_matrix(hd, 542)
+    kc, vc = tq.codebook(hd, kb)[0], tq.codebook(hd, vb)[0]
+    tkr, tvr, tkc, tvc = (backend.upload(a) for a in (krot, vrot, kc, vc))
+    with pytest.raises(InvalidShape, match="block lists"):  # the FP16 pool has 2 lists
+        backend.attention_paged_tq_pool(tq_, table, h, tkr, tvr, tkc, tvc, kb, vb, kvh, kv_len,
+                                        kv_len - T, o2)
+    backend.attention_paged_tq(tq_, table, *tls, tkr, tvr, tkc, tvc, kb, vb, kvh, kv_len,
+                               kv_len - T, o1)
+    h4 = backend.page_pool_create(*tls)
+    backend.attention_paged_tq_pool(tq_, table, h4, tkr, tvr, tkc, tvc, kb, vb, kvh, kv_len,
+                                    kv_len - T, o2)
+    assert np.array_equal(backend.download(o1), backend.download(o2))
+    with pytest.raises(InvalidShape, match="need"):  # twice the kv heads: blocks too small
+        backend.attention_paged_tq_pool(tq_, table, h4, tkr, tvr, tkc, tvc, kb, vb, 2 * kvh,
+                                        kv_len, kv_len - T, o2)
+    backend.page_pool_destroy(h)
+    backend.page_pool_destroy(h4)
+    with pytest.raises(TensorNotFound):
+        backend.page_pool_destroy(h)
+    for t in kbs + vbs + [x for l in tls for x in l] + [tq_, o1, o2, tkr, tvr, tkc, tvc]:
+        backend.free(t)
