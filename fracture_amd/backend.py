@@ -329,7 +329,7 @@ class HipBackend:
     def page_pool_create(self, *block_lists: Sequence[DeviceTensor]) -> int:
         """Keep a KV pool's block addresses in device memory: lists (K, V) for
         attention_paged_pool, (K packed, K norms, V packed, V norms) for
-        attention_paged_tq_pool. The tensors must outlive the pool."""
+        attention_paged_tq_pool. free() refuses a tensor while a pool holds it."""
         n = len(block_lists[0]) if block_lists else 0
         if not block_lists or any(len(l) != n for l in block_lists):
             raise InvalidShape("block lists differ in length")

@@ -159,9 +159,11 @@ struct fhip_backend {
         int nlists = 0;
         std::vector<uint64_t> min_bytes;     // smallest block tensor of each list
         std::vector<int32_t> dtype;          // each list's dtype (-1: mixed)
+        std::vector<uint64_t> ids;           // the block tensors
     };
     std::unordered_map<uint64_t, PagePool> pools;  // under mu
     uint64_t next_pool = 1;
+    std::unordered_map<uint64_t, int> pooled;      // tensor id -> pools holding it (under mu)
 
     int get_ptr(uint64_t id, void** out) {
         std::lock_guard<std::mutex> g(mu);
@@ -373,6 +375,10 @@ int fhip_free(fhip_backend* b, const fhip_tensor* t) {
         auto it = b->tensors.find(t->id);
         if (it == b->tensors.end())
             return fail(FHIP_ERR_TENSOR_NOT_FOUND, "tensor id %llu",
+                        (unsigned long long)t->id);
+        // a registered page pool keeps the tensor's address in device memory
+        if (b->pooled.count(t->id))
+            return fail(FHIP_ERR_BACKEND, "tensor id %llu is in a registered page pool",
                         (unsigned long long)t->id);
         p = it->second;
         b->tensors.erase(it);
@@ -999,7 +1005,7 @@ int fhip_attention_paged_tq(fhip_backend* b, const fhip_tensor* q, const int32_t
 // whole pool's tensor lists; the reference copies pool_len pointers to a fresh device
 // allocation on every call (cuda/src/backend.rs:295-315, 625-671). A registered pool keeps
 // those addresses in device memory, so a call stages only its block table. The pool's
-// tensors must stay allocated until the pool is destroyed.
+// tensors cannot be freed until the pool is destroyed (fhip_free refuses them).
 // ---------------------------------------------------------------------------------------
 int fhip_page_pool_create(fhip_backend* b, const fhip_tensor* blocks, size_t nlists,
                           size_t pool_len, uint64_t* pool_out) {
@@ -1021,6 +1027,7 @@ int fhip_page_pool_create(fhip_backend* b, const fhip_tensor* blocks, size_t nli
             int r = b->get_ptr(t->id, &p);
             if (r) return r;
             ptrs[l * pool_len + i] = p;
+            pp.ids.push_back(t->id);
             pp.min_bytes[l] = std::min<uint64_t>(pp.min_bytes[l], size_bytes(t));
             pp.dtype[l] = pp.dtype[l] == -2 || pp.dtype[l] == t->dtype ? t->dtype : -1;
         }
@@ -1035,6 +1042,13 @@ int fhip_page_pool_create(fhip_backend* b, const fhip_tensor* blocks, size_t nli
     }
     pp.dev = (const void**)dev;
     std::lock_guard<std::mutex> g(b->mu);
+    for (uint64_t tid : pp.ids) {
+        if (!b->tensors.count(tid)) {  // freed while the pool was being built
+            (void)hipFree(dev);
+            return fail(FHIP_ERR_TENSOR_NOT_FOUND, "tensor id %llu", (unsigned long long)tid);
+        }
+    }
+    for (uint64_t tid : pp.ids) ++b->pooled[tid];
     const uint64_t id = b->next_pool++;
     b->pools.emplace(id, std::move(pp));
     *pool_out = id;
@@ -1050,6 +1064,8 @@ int fhip_page_pool_destroy(fhip_backend* b, uint64_t pool) {
         if (it == b->pools.end())
             return fail(FHIP_ERR_TENSOR_NOT_FOUND, "page pool %llu", (unsigned long long)pool);
         dev = it->second.dev;
+        for (uint64_t tid : it->second.ids)
+            if (--b->pooled[tid] == 0) b->pooled.erase(tid);
         b->pools.erase(it);
     }
     set_device(b);

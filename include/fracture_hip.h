@@ -359,7 +359,7 @@ int fhip_attention_paged(fhip_backend* b, const fhip_tensor* q, const int32_t* b
  * 625-671): `blocks` holds nlists lists of pool_len block tensors, list-major — (K, V) for
  * fhip_attention_paged_pool, (K packed, K norms, V packed, V norms) for
  * fhip_attention_paged_tq_pool. The addresses stay in device memory, so each call stages only
- * its block table. The tensors must stay allocated until the pool is destroyed. */
+ * its block table. fhip_free refuses a tensor while a registered pool holds it. */
 int fhip_page_pool_create(fhip_backend* b, const fhip_tensor* blocks, size_t nlists,
                           size_t pool_len, uint64_t* pool_out);
 int fhip_page_pool_destroy(fhip_backend* b, uint64_t pool);

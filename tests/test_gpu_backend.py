@@ -340,6 +340,8 @@ def test_registered_page_pools(backend):
     with pytest.raises(InvalidShape, match="need"):  # twice the kv heads: blocks too small
         backend.attention_paged_tq_pool(tq_, table, h4, tkr, tvr, tkc, tvc, kb, vb, 2 * kvh,
                                         kv_len, kv_len - T, o2)
+    with pytest.raises(BackendError, match="registered page pool"):
+        backend.free(kbs[0])  # still referenced by pool h
     backend.page_pool_destroy(h)
     backend.page_pool_destroy(h4)
     with pytest.raises(TensorNotFound):
