@@ -117,6 +117,21 @@ def test_raw_launchers_reject_bad_arguments_on_host():
     # zero-size work is a no-op success
     assert lib.fhip_launch_add(None, None, None, 0, None) == 0
     assert lib.fhip_rows_workspace_bytes(64, 128256) == 64 * 32 * 32
+    # FP16 paged attention: head_dim 32/64/128/256, heads divisible, context bound
+    assert lib.fhip_launch_paged_attention(1, 1, 1, 1, 1, 1, 8, 2, 96, 16, 0, 1, None) == 1
+    assert lib.fhip_launch_paged_attention(1, 1, 1, 1, 1, 1, 6, 4, 128, 16, 0, 1, None) == 1
+    assert lib.fhip_launch_paged_attention(1, 1, 1, 1, 1, -1, 8, 2, 128, 16, 0, 1, None) == 1
+    assert lib.fhip_launch_paged_attention(None, None, None, None, None, 0, 8, 2, 128, 16, 0, 1,
+                                           None) == 0  # no tokens: nothing to do
+    assert lib.fhip_launch_attention_paged_decode(1, 1, 1, 1, 1, 1 << 17, 1, 1, 1, 1, 1, 8, 2, 128,
+                                                  1, None) == 1  # 2M positions > the 1M bound
+    # split partials: (m, l) and hd floats per (query, head, 1024-position split), 256-aligned
+    ml = 4 * 32 * 32 * 2 * 4
+    assert lib.fhip_attention_paged_workspace_bytes(4, 32, 128, 2048) == ml + 4 * 32 * 32 * 128 * 4
+    assert lib.fhip_attention_paged_workspace_bytes(0, 32, 128, 2048) == 0
+    # matmul sizes
+    assert lib.fhip_launch_matmul(None, None, None, -1, 4, 4, None) == 1
+    assert lib.fhip_launch_matmul(None, None, None, 0, 4, 4, None) == 0
 
 
 def test_kernels_module_requires_device_tensors():
