@@ -453,13 +453,14 @@ int fhip_launch_attention_paged_decode(void* output, const void* q, const int32_
 
 // The reference interface: one sequence, num_tokens queries at positions
 // start_pos .. start_pos + num_tokens - 1, per-block pointer arrays indexed by the physical
-// block ids of block_table[0 .. num_blocks_in_seq). The split partials live in a
-// stream-ordered allocation freed on the same stream.
-int fhip_launch_paged_attention(void* output, const void* q, const int* block_table,
-                                const void** k_block_ptrs, const void** v_block_ptrs,
-                                int num_tokens, int num_q_heads, int num_kv_heads, int head_dim,
-                                int kv_len, int start_pos, int num_blocks_in_seq,
-                                fhip_stream_t stream) {
+// block ids of block_table[0 .. num_blocks_in_seq). `ws` holds the split partials
+// (fhip_attention_paged_workspace_bytes(num_tokens, qh, hd, num_blocks_in_seq) bytes); null
+// asks for a stream-ordered allocation freed on the same stream.
+static int paged_attention_ref(void* output, const void* q, const int* block_table,
+                               const void** k_block_ptrs, const void** v_block_ptrs,
+                               int num_tokens, int num_q_heads, int num_kv_heads, int head_dim,
+                               int kv_len, int start_pos, int num_blocks_in_seq, void* ws,
+                               size_t ws_bytes, hipStream_t s) {
     if (num_tokens < 0 || kv_len < 0 || start_pos < 0 || num_blocks_in_seq < 0 ||
         !paged_shape_ok(num_q_heads, num_kv_heads, head_dim) ||
         (int64_t)num_blocks_in_seq * FHIP_PAGE_TOKENS > kMaxTokens)
@@ -468,23 +469,50 @@ int fhip_launch_paged_attention(void* output, const void* q, const int* block_ta
     if (!output || !q) return hipErrorInvalidValue;
     if (num_blocks_in_seq > 0 && (!block_table || !k_block_ptrs || !v_block_ptrs))
         return hipErrorInvalidValue;
-    hipStream_t s = fhip_host::as_stream(stream);
     const int mb = num_blocks_in_seq > 0 ? num_blocks_in_seq : 1;
     // with no blocks every query attends to nothing: the table is never read
     const PQueries qs{(const int32_t*)block_table, 0, num_blocks_in_seq, nullptr, kv_len,
                       start_pos, num_tokens};
     const size_t bytes = paged_ws_layout(num_tokens, num_q_heads, head_dim,
                                          mb * FHIP_PAGE_TOKENS, nullptr, nullptr);
-    void* ws = nullptr;
-    hipError_t e = hipMallocAsync(&ws, bytes, s);
-    if (e != hipSuccess) return e;
+    const bool own = ws == nullptr;
+    if (!own && ws_bytes < bytes) return hipErrorInvalidValue;
+    if (own) {
+        hipError_t e = hipMallocAsync(&ws, bytes, s);
+        if (e != hipSuccess) return e;
+    }
     const F16PtrPages pg{(const uint8_t* const*)k_block_ptrs, (const uint8_t* const*)v_block_ptrs,
                          0x7fffffff};
     int r = launch_paged(output, q, qs, num_tokens, pg, num_q_heads, num_kv_heads, head_dim, ws,
                          s);
-    hipError_t e2 = hipFreeAsync(ws, s);
-    if (r != hipSuccess) return r;
-    return e2;
+    if (own) {
+        hipError_t e2 = hipFreeAsync(ws, s);
+        if (r == hipSuccess) r = e2;
+    }
+    return r;
+}
+
+int fhip_launch_paged_attention(void* output, const void* q, const int* block_table,
+                                const void** k_block_ptrs, const void** v_block_ptrs,
+                                int num_tokens, int num_q_heads, int num_kv_heads, int head_dim,
+                                int kv_len, int start_pos, int num_blocks_in_seq,
+                                fhip_stream_t stream) {
+    return paged_attention_ref(output, q, block_table, k_block_ptrs, v_block_ptrs, num_tokens,
+                               num_q_heads, num_kv_heads, head_dim, kv_len, start_pos,
+                               num_blocks_in_seq, nullptr, 0, fhip_host::as_stream(stream));
+}
+
+int fhip_launch_paged_attention_ws(void* output, const void* q, const int* block_table,
+                                   const void** k_block_ptrs, const void** v_block_ptrs,
+                                   int num_tokens, int num_q_heads, int num_kv_heads,
+                                   int head_dim, int kv_len, int start_pos,
+                                   int num_blocks_in_seq, void* workspace,
+                                   size_t workspace_bytes, fhip_stream_t stream) {
+    if (!workspace) return hipErrorInvalidValue;
+    return paged_attention_ref(output, q, block_table, k_block_ptrs, v_block_ptrs, num_tokens,
+                               num_q_heads, num_kv_heads, head_dim, kv_len, start_pos,
+                               num_blocks_in_seq, workspace, workspace_bytes,
+                               fhip_host::as_stream(stream));
 }
 
 }  // extern "C"

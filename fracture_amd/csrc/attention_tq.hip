@@ -357,14 +357,22 @@ __global__ __launch_bounds__(256) void tq_attn_split_kernel(
 // Merge the splits of kCombHeads consecutive (query, head) vectors per workgroup and apply
 // Pi_v^T: out = Pi_v^T (sum_s w_s acc_s) / (sum_s w_s l_s), w_s = exp(m_s - max m). The work
 // is a few dependent memory round trips, so each phase issues its loads together:
-//   the rotation (hd x hd fp32) is staged in LDS first, overlapping the rest;
+//   the rotation (hd x hd fp32) is staged in LDS first, overlapping the rest (kRotLds; for
+//            head_dim above kRotLdsMaxHd it does not fit LDS and phase 3 reads it from L2);
 //   phase 1: a half-wave per vector loads its splits' (m, l) once and folds them into
 //            weights (LDS) and 1 / L;
 //   phase 2: the weighted split sums, four (vector, coordinate) items per thread, sixteen
 //            splits per step, each item summed in split order;
-//   phase 3: the matvec from LDS, one output coordinate for 4 vectors per thread and step.
-// Dynamic LDS: hd * hd rotation floats, then kCombHeads * nsplit weights.
+//   phase 3: the matvec, one output coordinate for 4 vectors per thread and step.
+// Dynamic LDS: hd * hd rotation floats (kRotLds), then kCombHeads * nsplit weights.
 constexpr int kCombHeads = 8;
+constexpr int kRotLdsMaxHd = 128;
+constexpr int kMaxTokensTq = kSplit * kSplit;  // 1024 splits: 32 KB of combine weights
+size_t combine_lds_bytes(int hd, int nsplit) {
+    return ((hd <= kRotLdsMaxHd ? (size_t)hd * hd : 0) + (size_t)kCombHeads * nsplit) *
+           sizeof(float);
+}
+template <bool kRotLds>
 __global__ __launch_bounds__(256) void tq_attn_combine_kernel(
     Queries qs, const float* __restrict__ part_ml, const float* __restrict__ part_acc,
     const float* __restrict__ vrot, uint16_t* __restrict__ out, int qh, int hd, int nsplit,
@@ -373,11 +381,12 @@ __global__ __launch_bounds__(256) void tq_attn_combine_kernel(
     __shared__ float linv[kCombHeads];
     __shared__ int nsv[kCombHeads];
     extern __shared__ uint32_t dyn[];
-    float* rl = (float*)dyn;              // [hd][hd]
-    float* wts = (float*)dyn + hd * hd;   // [kCombHeads][nsplit]
+    float* rl = (float*)dyn;                                  // [hd][hd] (kRotLds)
+    float* wts = (float*)dyn + (kRotLds ? hd * hd : 0);      // [kCombHeads][nsplit]
+    const float* rot = kRotLds ? (const float*)rl : vrot;
     const int tid = threadIdx.x;
     const int64_t h0 = (int64_t)blockIdx.x * kCombHeads;
-    {   // the rotation into LDS: hd * hd / 4 16-byte chunks, all loads first (hd % 8 == 0)
+    if (kRotLds) {   // the rotation into LDS: hd * hd / 4 16-byte chunks, all loads first
         const int n16 = hd * hd / 4;
         for (int c0 = tid; c0 < n16; c0 += 16 * 256) {
             u32x4 v[16];
@@ -453,7 +462,7 @@ __global__ __launch_bounds__(256) void tq_attn_combine_kernel(
         const int hg = idx / hd, i = idx - hg * hd;
         float dot[kCombHeads / 2] = {};
         for (int j = 0; j < hd; ++j) {
-            const float v = rl[j * hd + i];
+            const float v = rot[j * hd + i];
 #pragma unroll
             for (int k = 0; k < kCombHeads / 2; ++k) dot[k] += v * o[hg + 2 * k][j];
         }
@@ -1022,10 +1031,10 @@ int launch_attention(const AttnArgs& a, const Pages& pg, hipStream_t s) {
         launch_split<4, 2>(a, pg, nsplit, ml, acc, s);
     else
         launch_split<0, 0>(a, pg, nsplit, ml, acc, s);
-    hipLaunchKernelGGL(tq_attn_combine_kernel, dim3((unsigned)ceil_div(nvec, kCombHeads)),
-                       dim3(256), ((size_t)a.hd * a.hd + (size_t)kCombHeads * nsplit) * sizeof(float),
-                       s, a.qs, ml, acc,
-                       a.vrot, (uint16_t*)a.out, a.qh, a.hd, nsplit, (int64_t)nvec);
+    auto comb = a.hd <= kRotLdsMaxHd ? tq_attn_combine_kernel<true> : tq_attn_combine_kernel<false>;
+    hipLaunchKernelGGL(comb, dim3((unsigned)ceil_div(nvec, kCombHeads)), dim3(256),
+                       combine_lds_bytes(a.hd, nsplit), s, a.qs, ml, acc, a.vrot,
+                       (uint16_t*)a.out, a.qh, a.hd, nsplit, (int64_t)nvec);
     return hipGetLastError();
 }
 
@@ -1061,7 +1070,14 @@ int fhip_launch_attention_tq_decode(void* output, const void* q, const int32_t* 
         !attn_shape_ok(num_q_heads, num_kv_heads, head_dim, key_bits, value_bits))
         return hipErrorInvalidValue;
     if ((int64_t)batch * num_q_heads > (int64_t)1 << 30 || batch > 65535 ||
-        max_blocks * (int64_t)FHIP_PAGE_TOKENS > (int64_t)kSplit * kSplit)
+        max_blocks * (int64_t)FHIP_PAGE_TOKENS > kMaxTokensTq)
+        return hipErrorInvalidValue;
+    // each page stride must cover a page: the kernels read rows [0, 16) of every page
+    const int64_t pdk = (head_dim * key_bits + 7) / 8, pdv = (head_dim * value_bits + 7) / 8;
+    if (page_k_packed_bytes < (int64_t)FHIP_PAGE_TOKENS * num_kv_heads * pdk ||
+        page_v_packed_bytes < (int64_t)FHIP_PAGE_TOKENS * num_kv_heads * pdv ||
+        page_k_norm_bytes < (int64_t)FHIP_PAGE_TOKENS * num_kv_heads * 2 ||
+        page_v_norm_bytes < (int64_t)FHIP_PAGE_TOKENS * num_kv_heads * 2)
         return hipErrorInvalidValue;
     if (batch == 0) return hipSuccess;
     if (!output || !q || !block_table || !seq_lens || !k_packed_pool || !k_norms_pool ||
@@ -1091,18 +1107,19 @@ int fhip_launch_attention_tq_decode(void* output, const void* q, const int32_t* 
 }
 
 // The reference interface: one sequence, num_tokens queries at positions
-// start_pos .. start_pos + num_tokens - 1, per-block pointer arrays. The split partials
-// live in a stream-ordered allocation freed on the same stream.
-int fhip_launch_attention_paged_tq(void* output, const void* q, const int* block_table,
-                                   const void** k_packed_ptrs, const void** k_norms_ptrs,
-                                   const void** v_packed_ptrs, const void** v_norms_ptrs,
-                                   const float* k_rotation, const float* v_rotation,
-                                   const float* k_centroids, const float* v_centroids,
-                                   int num_tokens, int num_q_heads, int num_kv_heads,
-                                   int head_dim, int kv_len, int start_pos, int key_bits,
-                                   int value_bits, int k_packed_dim_per_head,
-                                   int v_packed_dim_per_head, fhip_stream_t stream) {
-    if (num_tokens < 0 || kv_len < 0 || start_pos < 0 ||
+// start_pos .. start_pos + num_tokens - 1, per-block pointer arrays. `ws` holds the split
+// partials (fhip_attention_tq_workspace_bytes(num_tokens, qh, hd, ceil(kv_len / 16)) bytes);
+// null asks for a stream-ordered allocation freed on the same stream.
+static int attention_paged_tq_ref(void* output, const void* q, const int* block_table,
+                                  const void** k_packed_ptrs, const void** k_norms_ptrs,
+                                  const void** v_packed_ptrs, const void** v_norms_ptrs,
+                                  const float* k_rotation, const float* v_rotation,
+                                  const float* k_centroids, const float* v_centroids,
+                                  int num_tokens, int num_q_heads, int num_kv_heads, int head_dim,
+                                  int kv_len, int start_pos, int key_bits, int value_bits,
+                                  int k_packed_dim_per_head, int v_packed_dim_per_head,
+                                  void* ws, size_t ws_bytes, hipStream_t s) {
+    if (num_tokens < 0 || kv_len < 0 || start_pos < 0 || kv_len > kMaxTokensTq ||
         !attn_shape_ok(num_q_heads, num_kv_heads, head_dim, key_bits, value_bits) ||
         k_packed_dim_per_head != (head_dim * key_bits + 7) / 8 ||
         v_packed_dim_per_head != (head_dim * value_bits + 7) / 8 || num_tokens > 65535)
@@ -1114,13 +1131,15 @@ int fhip_launch_attention_paged_tq(void* output, const void* q, const int* block
     if (nblocks > 0 && (!block_table || !k_packed_ptrs || !k_norms_ptrs || !v_packed_ptrs ||
                         !v_norms_ptrs))
         return hipErrorInvalidValue;
-    hipStream_t s = fhip_host::as_stream(stream);
     const int mb = nblocks > 0 ? nblocks : 1;
     const size_t bytes = ws_layout(num_tokens, num_q_heads, head_dim, mb * FHIP_PAGE_TOKENS,
                                    nullptr, nullptr, nullptr);
-    void* ws = nullptr;
-    hipError_t e = hipMallocAsync(&ws, bytes, s);
-    if (e != hipSuccess) return e;
+    const bool own = ws == nullptr;
+    if (!own && ws_bytes < bytes) return hipErrorInvalidValue;
+    if (own) {
+        hipError_t e = hipMallocAsync(&ws, bytes, s);
+        if (e != hipSuccess) return e;
+    }
     AttnArgs a;
     a.out = output;
     a.q = q;
@@ -1140,9 +1159,47 @@ int fhip_launch_attention_paged_tq(void* output, const void* q, const int* block
                 (const uint8_t* const*)v_packed_ptrs, (const uint8_t* const*)v_norms_ptrs,
                 0x7fffffff};
     int r = launch_attention(a, pg, s);
-    hipError_t e2 = hipFreeAsync(ws, s);
-    if (r != hipSuccess) return r;
-    return e2;
+    if (own) {
+        hipError_t e2 = hipFreeAsync(ws, s);
+        if (r == hipSuccess) r = e2;
+    }
+    return r;
+}
+
+int fhip_launch_attention_paged_tq(void* output, const void* q, const int* block_table,
+                                   const void** k_packed_ptrs, const void** k_norms_ptrs,
+                                   const void** v_packed_ptrs, const void** v_norms_ptrs,
+                                   const float* k_rotation, const float* v_rotation,
+                                   const float* k_centroids, const float* v_centroids,
+                                   int num_tokens, int num_q_heads, int num_kv_heads,
+                                   int head_dim, int kv_len, int start_pos, int key_bits,
+                                   int value_bits, int k_packed_dim_per_head,
+                                   int v_packed_dim_per_head, fhip_stream_t stream) {
+    return attention_paged_tq_ref(output, q, block_table, k_packed_ptrs, k_norms_ptrs,
+                                  v_packed_ptrs, v_norms_ptrs, k_rotation, v_rotation,
+                                  k_centroids, v_centroids, num_tokens, num_q_heads,
+                                  num_kv_heads, head_dim, kv_len, start_pos, key_bits,
+                                  value_bits, k_packed_dim_per_head, v_packed_dim_per_head,
+                                  nullptr, 0, fhip_host::as_stream(stream));
+}
+
+int fhip_launch_attention_paged_tq_ws(void* output, const void* q, const int* block_table,
+                                      const void** k_packed_ptrs, const void** k_norms_ptrs,
+                                      const void** v_packed_ptrs, const void** v_norms_ptrs,
+                                      const float* k_rotation, const float* v_rotation,
+                                      const float* k_centroids, const float* v_centroids,
+                                      int num_tokens, int num_q_heads, int num_kv_heads,
+                                      int head_dim, int kv_len, int start_pos, int key_bits,
+                                      int value_bits, int k_packed_dim_per_head,
+                                      int v_packed_dim_per_head, void* workspace,
+                                      size_t workspace_bytes, fhip_stream_t stream) {
+    if (!workspace) return hipErrorInvalidValue;
+    return attention_paged_tq_ref(output, q, block_table, k_packed_ptrs, k_norms_ptrs,
+                                  v_packed_ptrs, v_norms_ptrs, k_rotation, v_rotation,
+                                  k_centroids, v_centroids, num_tokens, num_q_heads,
+                                  num_kv_heads, head_dim, kv_len, start_pos, key_bits,
+                                  value_bits, k_packed_dim_per_head, v_packed_dim_per_head,
+                                  workspace, workspace_bytes, fhip_host::as_stream(stream));
 }
 
 }  // extern "C"

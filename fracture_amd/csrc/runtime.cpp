@@ -211,14 +211,17 @@ struct fhip_backend {
         return FHIP_OK;
     }
     // Backend-owned scratch (softmax partials, attention split partials). Callers hold
-    // launch_mu and call ws_done() after enqueuing the kernels that use it.
+    // launch_mu and call ws_done() after enqueuing the kernels that use it. Every user of the
+    // workspace runs on `stream`, so stream order already keeps one call's kernels from
+    // overwriting the previous call's partials; the host waits only before freeing a
+    // workspace that a queued kernel may still use.
     int get_workspace(size_t bytes, void** out) {
-        if (ws_pending) {
-            HIP_TRY(hipEventSynchronize(ws_ev));
-            ws_pending = false;
-        }
         if (!ws_ev) HIP_TRY(hipEventCreateWithFlags(&ws_ev, hipEventDisableTiming));
         if (bytes > ws_cap) {
+            if (ws_pending) {
+                HIP_TRY(hipEventSynchronize(ws_ev));
+                ws_pending = false;
+            }
             if (workspace) HIP_TRY(hipFree(workspace));
             workspace = nullptr;
             ws_cap = 0;
@@ -987,14 +990,20 @@ int fhip_attention_paged_tq(fhip_backend* b, const fhip_tensor* q, const int32_t
     if (r) return r;
     r = b->stage(ptrs.data(), ptrs.size() * sizeof(void*), &dptr, &s2);
     if (r) return r;
+    const size_t wsb = fhip_attention_tq_workspace_bytes(
+        (int)T, (int)qh, (int)hd, needed_blocks ? (int)needed_blocks : 1);
+    void* ws;
+    r = b->get_workspace(wsb, &ws);
+    if (r) return r;
     const void** dp = (const void**)dptr;
-    int e = fhip_launch_attention_paged_tq(
+    int e = fhip_launch_attention_paged_tq_ws(
         po, pq, (const int*)dbt, dp, dp + pool_len, dp + 2 * pool_len, dp + 3 * pool_len,
         (const float*)pkr, (const float*)pvr, (const float*)pkc, (const float*)pvc, (int)T, (int)qh,
         (int)num_kv_heads, (int)hd, (int)kv_len, (int)start_pos, key_bits, value_bits, (int)kpd,
-        (int)vpd, b->stream);
+        (int)vpd, ws, wsb, b->stream);
     b->stage_done(s1);
     b->stage_done(s2);
+    b->ws_done();
     if (e != hipSuccess) return hip_fail((hipError_t)e);
     return FHIP_OK;
 }
@@ -1141,11 +1150,18 @@ int fhip_attention_paged_pool(fhip_backend* b, const fhip_tensor* q, const int32
     int s1;
     r = b->stage(block_table, (needed_blocks ? needed_blocks : 1) * sizeof(int32_t), &dbt, &s1);
     if (r) return r;
-    int e = fhip_launch_paged_attention(po, pq, (const int*)dbt, pp.dev, pp.dev + pp.pool_len,
-                                        (int)T, (int)qh, (int)num_kv_heads, (int)hd,
-                                        (int)kv_len, (int)start_pos, (int)needed_blocks,
-                                        b->stream);
+    const size_t wsb = fhip_attention_paged_workspace_bytes(
+        (int)T, (int)qh, (int)hd, needed_blocks ? (int)needed_blocks : 1);
+    void* ws;
+    r = b->get_workspace(wsb, &ws);
+    if (r) return r;
+    int e = fhip_launch_paged_attention_ws(po, pq, (const int*)dbt, pp.dev,
+                                           pp.dev + pp.pool_len, (int)T, (int)qh,
+                                           (int)num_kv_heads, (int)hd, (int)kv_len,
+                                           (int)start_pos, (int)needed_blocks, ws, wsb,
+                                           b->stream);
     b->stage_done(s1);
+    b->ws_done();
     if (e != hipSuccess) return hip_fail((hipError_t)e);
     return FHIP_OK;
 }
@@ -1207,14 +1223,20 @@ int fhip_attention_paged_tq_pool(fhip_backend* b, const fhip_tensor* q,
     int s1;
     r = b->stage(block_table, (needed_blocks ? needed_blocks : 1) * sizeof(int32_t), &dbt, &s1);
     if (r) return r;
+    const size_t wsb = fhip_attention_tq_workspace_bytes(
+        (int)T, (int)qh, (int)hd, needed_blocks ? (int)needed_blocks : 1);
+    void* ws;
+    r = b->get_workspace(wsb, &ws);
+    if (r) return r;
     const void** dp = pp.dev;
     const size_t n = pp.pool_len;
-    int e = fhip_launch_attention_paged_tq(
+    int e = fhip_launch_attention_paged_tq_ws(
         po, pq, (const int*)dbt, dp, dp + n, dp + 2 * n, dp + 3 * n, (const float*)pkr,
         (const float*)pvr, (const float*)pkc, (const float*)pvc, (int)T, (int)qh,
         (int)num_kv_heads, (int)hd, (int)kv_len, (int)start_pos, key_bits, value_bits, (int)kpd,
-        (int)vpd, b->stream);
+        (int)vpd, ws, wsb, b->stream);
     b->stage_done(s1);
+    b->ws_done();
     if (e != hipSuccess) return hip_fail((hipError_t)e);
     return FHIP_OK;
 }
@@ -1274,12 +1296,19 @@ int fhip_attention_paged(fhip_backend* b, const fhip_tensor* q, const int32_t* b
     if (r) return r;
     r = b->stage(ptrs.data(), ptrs.size() * sizeof(void*), &dptr, &s2);
     if (r) return r;
+    const size_t wsb = fhip_attention_paged_workspace_bytes(
+        (int)T, (int)qh, (int)hd, needed_blocks ? (int)needed_blocks : 1);
+    void* ws;
+    r = b->get_workspace(wsb, &ws);
+    if (r) return r;
     const void** dp = (const void**)dptr;
-    int e = fhip_launch_paged_attention(po, pq, (const int*)dbt, dp, dp + pool_len, (int)T,
-                                        (int)qh, (int)num_kv_heads, (int)hd, (int)kv_len,
-                                        (int)start_pos, (int)needed_blocks, b->stream);
+    int e = fhip_launch_paged_attention_ws(po, pq, (const int*)dbt, dp, dp + pool_len, (int)T,
+                                           (int)qh, (int)num_kv_heads, (int)hd, (int)kv_len,
+                                           (int)start_pos, (int)needed_blocks, ws, wsb,
+                                           b->stream);
     b->stage_done(s1);
     b->stage_done(s2);
+    b->ws_done();
     if (e != hipSuccess) return hip_fail((hipError_t)e);
     return FHIP_OK;
 }

@@ -5,9 +5,13 @@
  * Three groups of entry points:
  *
  *   1. Raw launchers `fhip_launch_*`: device pointers, int32 dims, asynchronous on the
- *      given stream, no allocation, return 0 (hipSuccess) or a HIP error code. The first
- *      eight replace, one for one, the `launch_*` symbols that the reference's Rust code
- *      binds in backends/fracture-cuda/src/ffi.rs:141-274.
+ *      given stream, return 0 (hipSuccess) or a HIP error code. The first eight replace,
+ *      one for one, the `launch_*` symbols that the reference's Rust code binds in
+ *      backends/fracture-cuda/src/ffi.rs:141-274. They allocate nothing, except the two
+ *      paged-attention launchers with the reference's signature, which has no workspace
+ *      argument: those take their split partials from a stream-ordered allocation
+ *      (hipMallocAsync / hipFreeAsync on the given stream); their `_ws` forms take a
+ *      caller-owned workspace instead.
  *   2. A handle runtime `fhip_*` that mirrors the `Backend` trait
  *      (crates/fracture-core/src/backend.rs:8-223) over opaque tensor ids, plus the
  *      inherent `CudaBackend` API (backends/fracture-cuda/src/lib.rs:76-161). Calls return
@@ -103,7 +107,9 @@ int fhip_launch_turboquant_decompress(const void* packed_in, const void* norms_i
 /* ffi.rs:251-274 `launch_attention_paged_tq`: causal GQA attention of q [T, qh, hd] fp16 over
  * TurboQuant pages given as per-block pointer arrays (device memory), with the query
  * pre-rotated by k_rotation and the output unrotated by v_rotation^T. Unlike the reference
- * kernel it keeps no kv_len-sized score row, so kv_len is bounded only by the block table. */
+ * kernel it keeps no kv_len-sized score row: kv_len may be up to 1,048,576 positions.
+ * head_dim is a multiple of 8 up to 256; T up to 65535. The split partials come from a
+ * stream-ordered allocation on `stream` (see fhip_launch_attention_paged_tq_ws). */
 int fhip_launch_attention_paged_tq(void* output, const void* q, const int* block_table,
                                    const void** k_packed_ptrs, const void** k_norms_ptrs,
                                    const void** v_packed_ptrs, const void** v_norms_ptrs,
@@ -118,7 +124,8 @@ int fhip_launch_attention_paged_tq(void* output, const void* q, const int* block
  * of q [T, qh, hd] fp16 over FP16 pages given as per-block pointer arrays (device memory,
  * indexed by the physical block ids of block_table), each block [16, kvh, hd] fp16. head_dim
  * is 32, 64, 128 or 256. Unlike the reference kernel it keeps no kv_len-sized score row: a
- * block table may describe up to 1,048,576 positions. */
+ * block table may describe up to 1,048,576 positions. The split partials come from a
+ * stream-ordered allocation on `stream` (see fhip_launch_paged_attention_ws). */
 int fhip_launch_paged_attention(void* output, const void* q, const int* block_table,
                                 const void** k_block_ptrs, const void** v_block_ptrs,
                                 int num_tokens, int num_q_heads, int num_kv_heads, int head_dim,
@@ -131,6 +138,29 @@ int fhip_launch_matmul(void* c, const void* a, const void* b, int m, int n, int 
                        fhip_stream_t stream);
 
 /* --- additive raw launchers ---------------------------------------------------------- */
+
+/* The two reference-signature paged-attention launchers above with a caller-owned workspace
+ * for the split partials, so that no call allocates: workspace_bytes must be at least
+ * fhip_attention_tq_workspace_bytes(num_tokens, num_q_heads, head_dim, ceil(kv_len / 16))
+ * (TurboQuant; 1 block when kv_len is 0) or fhip_attention_paged_workspace_bytes(num_tokens,
+ * num_q_heads, head_dim, max(num_blocks_in_seq, 1)) (FP16). Calls sharing a workspace must be
+ * ordered on one stream. */
+int fhip_launch_attention_paged_tq_ws(void* output, const void* q, const int* block_table,
+                                      const void** k_packed_ptrs, const void** k_norms_ptrs,
+                                      const void** v_packed_ptrs, const void** v_norms_ptrs,
+                                      const float* k_rotation, const float* v_rotation,
+                                      const float* k_centroids, const float* v_centroids,
+                                      int num_tokens, int num_q_heads, int num_kv_heads,
+                                      int head_dim, int kv_len, int start_pos, int key_bits,
+                                      int value_bits, int k_packed_dim_per_head,
+                                      int v_packed_dim_per_head, void* workspace,
+                                      size_t workspace_bytes, fhip_stream_t stream);
+int fhip_launch_paged_attention_ws(void* output, const void* q, const int* block_table,
+                                   const void** k_block_ptrs, const void** v_block_ptrs,
+                                   int num_tokens, int num_q_heads, int num_kv_heads,
+                                   int head_dim, int kv_len, int start_pos,
+                                   int num_blocks_in_seq, void* workspace,
+                                   size_t workspace_bytes, fhip_stream_t stream);
 
 /* dtype-generic forms of rmsnorm / add / silu_mul (FHIP_FP16, FHIP_BF16, FHIP_FP32). */
 int fhip_launch_rmsnorm_ex(void* output, const void* input, const void* weight, float eps,
@@ -226,9 +256,10 @@ int fhip_launch_tq_dequant_planned(const fhip_tq_plan* plan, const void* packed_
 
 /* Batched decode attention over a TurboQuant page pool: one query token per sequence,
  * q [B, qh, hd] fp16, block_table [B, max_blocks] int32 (physical page ids), seq_lens [B]
- * int32; pages in contiguous pools (strides in bytes between pages); positions whose page
- * id is outside [0, num_pages) are masked out. Output [B, qh, hd] fp16; centroid tables
- * hold 2^bits entries.
+ * int32; pages in contiguous pools (strides in bytes between pages, each at least one page:
+ * 16 * kvh * packed_dim or 16 * kvh * 2 bytes); positions whose page id is outside
+ * [0, num_pages) are masked out. max_blocks * 16 is at most 1,048,576. Output [B, qh, hd]
+ * fp16; centroid tables hold 2^bits entries.
  * The workspace holds split-K partials; size it with fhip_attention_tq_workspace_bytes. */
 size_t fhip_attention_tq_workspace_bytes(int batch, int num_q_heads, int head_dim,
                                          int max_blocks);

@@ -80,6 +80,9 @@ def _declare(L: C.CDLL) -> None:
         "o_tq_dequant": (None, [P, P, I64, C.c_int, P, P, C.c_int, P]),
         "o_tq_attention": (None, [P, P, C.c_int, P, P, P, P, I64, I64, I64, I64, P, P, P, P,
                                   C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, P]),
+        "o_tq_attention_heads": (None, [P, P, C.c_int, P, P, P, P, I64, I64, I64, I64, P, P, P,
+                                        P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                        C.c_int, P]),
         "o_paged_attention": (None, [P, P, C.c_int, P, P, I64, I64, C.c_int, C.c_int, C.c_int,
                                      P]),
     }
@@ -349,19 +352,21 @@ def tq_dequant(packed: np.ndarray, norms: np.ndarray, rot: np.ndarray, centroids
 
 
 def tq_attention(q16, block_table, causal_len, kp, kn, vp, vn, krot, vrot, kc, vc, kbits, vbits,
-                 kvh):
-    """One query token: q16 [qh, hd] float16; pools as uint8 arrays [pages, ...]."""
+                 kvh, heads=None):
+    """One query token: q16 [qh, hd] float16; pools as uint8 arrays [pages, ...].
+    heads=(h0, h1) computes query heads h0..h1-1 only; the other output rows are zero."""
     q = np.ascontiguousarray(q16, dtype=np.float16)
     qh, hd = q.shape
+    h0, h1 = (0, qh) if heads is None else heads
     bt = np.ascontiguousarray(block_table, dtype=np.int32)
     kp, kn, vp, vn = (np.ascontiguousarray(a) for a in (kp, kn, vp, vn))
-    out = np.empty((qh, hd), np.float16)
-    lib().o_tq_attention(
+    out = np.zeros((qh, hd), np.float16)
+    lib().o_tq_attention_heads(
         _p(q), _p(bt), int(causal_len), _p(kp), _p(kn), _p(vp), _p(vn),
         kp[0].nbytes, kn[0].nbytes, vp[0].nbytes, vn[0].nbytes,
         _p(np.ascontiguousarray(krot, np.float32)), _p(np.ascontiguousarray(vrot, np.float32)),
         _p(np.ascontiguousarray(kc, np.float32)), _p(np.ascontiguousarray(vc, np.float32)),
-        kbits, vbits, qh, kvh, hd, _p(out))
+        kbits, vbits, qh, kvh, hd, int(h0), int(h1), _p(out))
     return out
 
 

@@ -566,22 +566,29 @@ void o_tq_dequant(const uint8_t* packed, const uint16_t* norms16, int64_t rows, 
     free(yh);
 }
 
-/* TurboQuant paged attention for one query token (attention_paged_tq.cu:79-257).
+/* TurboQuant paged attention for one query token (attention_paged_tq.cu:79-257), query heads
+ * [h_begin, h_end) only (out16 rows of the other heads are left untouched).
  * Pages live in pools: K packed page p at kp + p*skp bytes, layout [16][kvh][pdk]; norms at
  * kn + p*skn bytes, [16][kvh] fp16; likewise V. q16/out16: [qh][hd] fp16 for this token;
- * causal_len positions are attended through block_table. */
-void o_tq_attention(const uint16_t* q16, const int32_t* block_table, int causal_len,
-                    const uint8_t* kp, const uint8_t* kn, const uint8_t* vp, const uint8_t* vn,
-                    int64_t skp, int64_t skn, int64_t svp, int64_t svn, const float* krot,
-                    const float* vrot, const float* kc, const float* vc, int kbits, int vbits,
-                    int qh, int kvh, int hd, uint16_t* out16) {
+ * causal_len positions are attended through block_table.
+ * The V accumulation visits positions in the outer loop: each coordinate's sum still adds
+ * the positions in increasing order (attention_paged_tq.cu:222-243 sums over t per d), so
+ * the result is the same as with the coordinate loop outside, with one pass over the rows. */
+void o_tq_attention_heads(const uint16_t* q16, const int32_t* block_table, int causal_len,
+                          const uint8_t* kp, const uint8_t* kn, const uint8_t* vp,
+                          const uint8_t* vn, int64_t skp, int64_t skn, int64_t svp, int64_t svn,
+                          const float* krot, const float* vrot, const float* kc, const float* vc,
+                          int kbits, int vbits, int qh, int kvh, int hd, int h_begin, int h_end,
+                          uint16_t* out16) {
     const int G = qh / kvh;
     const int pdk = (hd * kbits + 7) / 8, pdv = (hd * vbits + 7) / 8;
     const float scale = 1.0f / sqrtf((float)hd);
     float* qrot = (float*)malloc(sizeof(float) * (size_t)hd);
     float* acc = (float*)malloc(sizeof(float) * (size_t)hd);
     float* sc = (float*)malloc(sizeof(float) * (size_t)(causal_len > 0 ? causal_len : 1));
-    for (int h = 0; h < qh; ++h) {
+    if (h_begin < 0) h_begin = 0;
+    if (h_end > qh) h_end = qh;
+    for (int h = h_begin; h < h_end; ++h) {
         const int kvhd = h / G;
         for (int i = 0; i < hd; ++i) {
             float dot = 0.0f;
@@ -607,15 +614,12 @@ void o_tq_attention(const uint16_t* q16, const int32_t* block_table, int causal_
         }
         const float inv = 1.0f / sum;
         for (int t = 0; t < causal_len; ++t) sc[t] *= inv;
-        for (int d = 0; d < hd; ++d) {
-            float a = 0.0f;
-            for (int t = 0; t < causal_len; ++t) {
-                const int page = block_table[t / 16], off = t % 16;
-                const uint8_t* row = vp + (int64_t)page * svp + ((int64_t)off * kvh + kvhd) * pdv;
-                const float vn_ = o_f16_to_f32(((const uint16_t*)(vn + (int64_t)page * svn))[off * kvh + kvhd]);
-                a += sc[t] * vc[o_tq_unpack(row, d, vbits)] * vn_;
-            }
-            acc[d] = a;
+        for (int d = 0; d < hd; ++d) acc[d] = 0.0f;
+        for (int t = 0; t < causal_len; ++t) {
+            const int page = block_table[t / 16], off = t % 16;
+            const uint8_t* row = vp + (int64_t)page * svp + ((int64_t)off * kvh + kvhd) * pdv;
+            const float vn_ = o_f16_to_f32(((const uint16_t*)(vn + (int64_t)page * svn))[off * kvh + kvhd]);
+            for (int d = 0; d < hd; ++d) acc[d] += sc[t] * vc[o_tq_unpack(row, d, vbits)] * vn_;
         }
         for (int i = 0; i < hd; ++i) {
             float dot = 0.0f;
@@ -626,6 +630,16 @@ void o_tq_attention(const uint16_t* q16, const int32_t* block_table, int causal_
     free(qrot);
     free(acc);
     free(sc);
+}
+
+/* Every query head of one token. */
+void o_tq_attention(const uint16_t* q16, const int32_t* block_table, int causal_len,
+                    const uint8_t* kp, const uint8_t* kn, const uint8_t* vp, const uint8_t* vn,
+                    int64_t skp, int64_t skn, int64_t svp, int64_t svn, const float* krot,
+                    const float* vrot, const float* kc, const float* vc, int kbits, int vbits,
+                    int qh, int kvh, int hd, uint16_t* out16) {
+    o_tq_attention_heads(q16, block_table, causal_len, kp, kn, vp, vn, skp, skn, svp, svn, krot,
+                         vrot, kc, vc, kbits, vbits, qh, kvh, hd, 0, qh, out16);
 }
 
 /* FP16 paged GQA attention for one query token (attention_paged.cu:36-170).

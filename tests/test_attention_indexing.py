@@ -1,0 +1,210 @@
+"""CPU model of every global-memory address that the MFMA decode-attention kernel
+(tq_attn_mfma_kernel in fracture_amd/csrc/attention_tq.hip) and its combine kernel form,
+checked against the buffers the launcher hands them.
+
+The model restates the kernel's index arithmetic per wave item (query, kv head, 1024-position
+split) and per 64-position chunk, vectorised over lanes with numpy:
+
+  split page cache   table[t_begin / 16 + lane]            (lanes whose page starts < t_end)
+  chunk_pages        page ids of positions t0 + 16k, k = 0..3, kept when in [0, num_pages)
+  load_k             page(k = n / 4) + ((4 (n % 4) + pt) kvh + g) 64 + 16 rg, 16 bytes
+  dma_v              page(i) + ((lane / 4) kvh + g) 64 + 16 ((lane % 4) ^ ((lane / 8) % 4)), 16 bytes
+  load_norms         norm page(lane / 16) + 2 ((lane % 16) kvh + g), 2 bytes
+  Q (rotated)        (qi qh + g G + h) hd + 32 rg + 4 s, 16 bytes
+  partials           ((head0 + h) nsplit + split) (2 | hd) + ...
+
+and asserts that each access stays inside its pool AND inside the page it means to read
+(an access past the page's rows reads a neighbouring page: in bounds, but wrong data).
+Lanes that read no position use `dummy` (the 64-byte K centroid table), which is checked to
+be large enough. No GPU is used.
+"""
+import numpy as np
+import pytest
+
+PAGE = 16
+SPLIT = 1024
+CHUNK = 64
+
+
+def ws_layout(nq, qh, hd, max_tokens):
+    ns = (max_tokens + SPLIT - 1) // SPLIT if max_tokens > 0 else 1
+    al = lambda x: (x + 255) & ~255
+    qrot = nq * qh * hd * 4
+    ml = nq * qh * ns * 2 * 4
+    acc = nq * qh * ns * hd * 4
+    return ns, al(qrot), al(ml), al(acc)
+
+
+def causal_len(seq_len, max_blocks):
+    return max(0, min(int(seq_len), max_blocks * PAGE))
+
+
+class Bounds:
+    """Collects accesses [off, off + width) per buffer and checks them."""
+
+    def __init__(self, sizes):
+        self.sizes = sizes
+        self.count = {k: 0 for k in sizes}
+
+    def check(self, buf, off, width):
+        off = np.asarray(off, dtype=np.int64).ravel()
+        if off.size == 0:
+            return
+        lo, hi = int(off.min()), int(off.max()) + width
+        assert lo >= 0 and hi <= self.sizes[buf], \
+            f"{buf}: access [{lo}, {hi}) outside [0, {self.sizes[buf]})"
+        self.count[buf] += off.size
+
+
+def model_mfma_kernel(lens, table, num_pages, qh, kvh, page_bytes, pool_bytes):
+    """Every access of tq_attn_mfma_kernel<PoolPages> for one launch (hd 128, K4/V4)."""
+    hd, pd = 128, 64
+    B, max_blocks = table.shape
+    G = qh // kvh
+    nsplit, _, ml_bytes, acc_bytes = ws_layout(B, qh, hd, max_blocks * PAGE)
+    bnd = Bounds({"table": table.size * 4, "kp": pool_bytes["kp"], "kn": pool_bytes["kn"],
+                  "vp": pool_bytes["vp"], "vn": pool_bytes["vn"], "qrot": B * qh * hd * 4,
+                  "part_ml": ml_bytes, "part_acc": acc_bytes, "dummy": 64})
+    lane = np.arange(64)
+    n, rg = lane & 15, lane >> 4
+    for qi in range(B):
+        clen = causal_len(lens[qi], max_blocks)
+        for split in range(nsplit):
+            t_begin = split * SPLIT
+            if t_begin >= clen:
+                continue
+            t_end = min(clen, t_begin + SPLIT)
+            # split page cache: one table entry per lane
+            has = t_begin + PAGE * lane < t_end
+            tidx = t_begin // PAGE + lane[has]
+            assert tidx.max() < max_blocks
+            bnd.check("table", (qi * max_blocks + tidx) * 4, 4)
+            split_page = np.full(64, -1, np.int64)
+            split_page[has] = table[qi, tidx]
+            chunks = np.arange(t_begin, t_end, CHUNK)
+            for g in range(kvh):
+                for t0 in chunks:
+                    j0 = ((t0 - t_begin) // PAGE) & 63
+                    pos = t0 + PAGE * np.arange(4)
+                    assert j0 + 3 < 64, "page cache lane index past the wave"
+                    ids = np.where(pos < t_end, split_page[(j0 + np.arange(4)) & 63], -1)
+                    ok_page = (pos < t_end) & (ids >= 0) & (ids < num_pages)
+                    # load_k: lane (n, rg), page k = n / 4, tiles pt = 0..3
+                    k = n >> 2
+                    for pt in range(4):
+                        ok = ok_page[k] & (t0 + 4 * n + pt < t_end)
+                        row = 4 * (n & 3) + pt
+                        inpage = (row * kvh + g) * pd + 16 * rg
+                        assert inpage[ok].max(initial=0) + 16 <= min(PAGE * kvh * pd, page_bytes["kp"])
+                        off = ids[k] * page_bytes["kp"] + inpage
+                        bnd.check("kp", off[ok], 16)
+                        bnd.check("dummy", np.zeros(int((~ok).sum())), 16)
+                    # dma_v: copy i = page i, lane L position 16 i + L / 4
+                    for i in range(4):
+                        ok = ok_page[i] & (t0 + 16 * i + (lane >> 2) < t_end)
+                        inpage = ((lane >> 2) * kvh + g) * pd + 16 * ((lane & 3) ^ ((lane >> 3) & 3))
+                        assert inpage[ok].max(initial=0) + 16 <= min(PAGE * kvh * pd, page_bytes["vp"])
+                        off = ids[i] * page_bytes["vp"] + inpage
+                        bnd.check("vp", np.broadcast_to(off, lane.shape)[ok], 16)
+                    # load_norms: lane -> page lane / 16, row lane % 16 (row 0 when unused)
+                    kk = lane >> 4
+                    ok = ok_page[kk] & (t0 + lane < t_end)
+                    row = np.where(ok, (lane & 15) * kvh + g, 0)
+                    for nm in ("kn", "vn"):
+                        off = ids[kk] * page_bytes[nm] + 2 * row
+                        bnd.check(nm, off[ok_page[kk]], 2)
+                        assert (2 * row + 2).max() <= min(PAGE * kvh * 2, page_bytes[nm])
+                # Q: heads past G read head 0
+                h = n & 7
+                hsrc = np.where(h < G, h, 0)
+                for s8 in range(8):
+                    bnd.check("qrot", ((qi * qh + g * G + hsrc) * hd + 32 * rg + 4 * s8) * 4, 16)
+                head0 = qi * qh + g * G
+                hs = np.arange(G)
+                bnd.check("part_ml", (((head0 + hs) * nsplit + split) * 2) * 4, 8)
+                c = np.arange(8)[:, None, None]
+                e = np.arange(4)[None, :, None]
+                sel = n < G
+                dims = 16 * c + ((4 * rg[sel][None, None, :] + e) ^ 1)
+                bnd.check("part_acc", (((head0 + (n[sel] & 7)) * nsplit + split) * hd + dims) * 4, 4)
+    return bnd, nsplit
+
+
+def model_combine(lens, max_blocks, qh, hd, nsplit, ml_bytes, acc_bytes):
+    """tq_attn_combine_kernel: partial reads (clamped split index), rotation reads, output."""
+    B = len(lens)
+    nvec = B * qh
+    bnd = Bounds({"part_ml": ml_bytes, "part_acc": acc_bytes, "vrot": hd * hd * 4,
+                  "out": nvec * hd * 2})
+    n16 = hd * hd // 4
+    c0 = np.arange(256)[:, None] + 256 * np.arange(16)[None, :]
+    bnd.check("vrot", 4 * np.minimum(c0, n16 - 1) * 4, 16)
+    heads = np.arange(nvec)
+    ns = np.array([(causal_len(lens[h // qh], max_blocks) + SPLIT - 1) // SPLIT for h in heads])
+    assert ns.max() <= nsplit
+    for hh, k in zip(heads, ns):
+        sp = np.arange(k)
+        bnd.check("part_ml", (hh * nsplit * 2 + 2 * sp) * 4, 8)
+        clamp = np.minimum(np.arange(((k + 15) // 16) * 16), max(k - 1, 0))
+        bnd.check("part_acc", ((hh * nsplit + clamp[:, None]) * hd + np.arange(hd)[None, :]) * 4, 4)
+    bnd.check("out", heads * hd * 2, 2 * hd)
+    return bnd
+
+
+def c5_workload():
+    """The decode-attention benchmark's lengths, block table and pool (seeded as bench.py)."""
+    rng = np.random.default_rng(5)
+    lens = rng.integers(1024, 32769, 64).astype(np.int32)
+    nbs = (lens + 15) // 16
+    P = int(nbs.sum())
+    perm = rng.permutation(P).astype(np.int32)
+    table = np.zeros((64, int(nbs.max())), np.int32)
+    at = 0
+    for b in range(64):
+        table[b, :nbs[b]] = perm[at:at + nbs[b]]
+        at += nbs[b]
+    return lens, table, P
+
+
+def pools(P, kvh, pd=64):
+    page = {"kp": PAGE * kvh * pd, "kn": PAGE * kvh * 2, "vp": PAGE * kvh * pd, "vn": PAGE * kvh * 2}
+    return page, {k: v * P for k, v in page.items()}
+
+
+@pytest.mark.parametrize("which", ["c5", "edges"])
+def test_mfma_decode_accesses_in_bounds(which):
+    if which == "c5":
+        lens, table, P = c5_workload()
+        assert lens.max() > 16 * SPLIT, "the workload must reach the combine's second 16-split step"
+    else:
+        # lengths at chunk, page and split edges; unused table slots hold ids outside the pool;
+        # one sequence longer than its block table (clamped to max_blocks * 16)
+        lens = np.array([1, 15, 16, 17, 63, 64, 65, 1023, 1024, 1025, 16384, 16385, 20000, 0,
+                         33000], np.int32)
+        max_blocks = 2048
+        rng = np.random.default_rng(3)
+        P = 2048 * 3
+        table = np.full((len(lens), max_blocks), -7, np.int32)
+        for b, n in enumerate(lens):
+            nb = min((int(n) + 15) // 16, max_blocks)
+            table[b, :nb] = rng.integers(0, P, nb)
+        table[3, 1] = P + 5      # a page id past the pool: masked, never read
+    qh, kvh = 32, 8
+    page, pool = pools(P, kvh)
+    bnd, nsplit = model_mfma_kernel(lens, table, P, qh, kvh, page, pool)
+    assert bnd.count["kp"] > 0 and bnd.count["vp"] > 0
+    _, _, ml, acc = ws_layout(len(lens), qh, 128, table.shape[1] * PAGE)
+    model_combine(lens, table.shape[1], qh, 128, nsplit, ml, acc)
+
+
+def test_page_stride_smaller_than_page_is_caught():
+    """A page stride below the page size makes the model's in-page reads cross into the next
+    page; the launcher rejects such strides (fhip_launch_attention_tq_decode)."""
+    lens, table = np.array([48], np.int32), np.arange(3, dtype=np.int32)[None, :]
+    page, pool = pools(3, 8)
+    model_mfma_kernel(lens, table, 3, 32, 8, page, pool)
+    for key in ("kp", "vn"):
+        small = dict(page)
+        small[key] //= 2
+        with pytest.raises(AssertionError):
+            model_mfma_kernel(lens, table, 3, 32, 8, small, pool)
