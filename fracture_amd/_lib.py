@@ -65,6 +65,8 @@ SIGNATURES = {
     "fhip_launch_tq_rotate": (I, [P, P, P, P, I, I, P]),
     "fhip_launch_tq_compress_pages": (I, [P, P, P, I, I, P, P, I64, I64, P, I, I, I, I, I, P]),
     "fhip_launch_tq_dequant": (I, [P, P, P, P, I, P, I, I, I, I, I, P]),
+    "fhip_launch_tq_compress_page_ptrs": (I, [P, P, P, I, I, P, P, P, I, I, I, I, I, P]),
+    "fhip_launch_tq_compress_page_ptrs_planned": (I, [P, P, P, P, P, I, I, I, I, P]),
     "fhip_tq_plan_create": (I, [P, P, I, I, I, P, C.POINTER(P)]),
     "fhip_tq_plan_destroy": (None, [P]),
     "fhip_launch_tq_compress_planned": (I, [P, P, P, P, I, I, P]),
@@ -73,6 +75,8 @@ SIGNATURES = {
     "fhip_attention_tq_workspace_bytes": (SZ, [I, I, I, I]),
     "fhip_launch_attention_tq_decode": (I, [P, P, P, P, I, I, I, P, P, P, P, I64, I64, I64, I64,
                                             P, P, P, P, I, I, I, I, I, P, P]),
+    "fhip_launch_attention_tq_decode_ptrs": (I, [P, P, P, P, I, I, I, P, P, P, P, P, P, P, P, I,
+                                                 I, I, I, I, P, P]),
     "fhip_attention_paged_workspace_bytes": (SZ, [I, I, I, I]),
     "fhip_launch_attention_paged_decode": (I, [P, P, P, P, I, I, I, P, P, I64, I64, I, I, I, P,
                                                P]),
@@ -113,6 +117,9 @@ SIGNATURES = {
     "fhip_attention_paged_pool": (I, [P, TP, P, SZ, U64, SZ, SZ, SZ, TP]),
     "fhip_attention_paged_tq_pool": (I, [P, TP, P, SZ, U64, TP, TP, TP, TP, C.c_uint8,
                                          C.c_uint8, SZ, SZ, SZ, TP]),
+    "fhip_tq_append_kv": (I, [P, U64, TP, TP, TP, TP, TP, TP, C.c_uint8, C.c_uint8, P, SZ, SZ]),
+    "fhip_attention_paged_tq_batched": (I, [P, TP, P, SZ, P, U64, TP, TP, TP, TP, C.c_uint8,
+                                            C.c_uint8, SZ, TP]),
     "fhip_add_rmsnorm": (I, [P, TP, TP, TP, D, TP]),
     "fhip_softmax_rows": (I, [P, TP, F, TP]),
     "fhip_argmax_rows": (I, [P, TP, P, SZ]),

@@ -361,6 +361,36 @@ class HipBackend:
             C.byref(v_rotation._c()), C.byref(k_centroids._c()), C.byref(v_centroids._c()),
             key_bits, value_bits, num_kv_heads, kv_len, start_pos, C.byref(out._c())))
 
+    def tq_append_kv(self, pool: int, keys: DeviceTensor, values: DeviceTensor,
+                     k_rotation: DeviceTensor, v_rotation: DeviceTensor,
+                     k_centroids: DeviceTensor, v_centroids: DeviceTensor, key_bits: int,
+                     value_bits: int, block_table: Sequence[int], start_pos: int) -> None:
+        """QuantizedKvCacheManager::append_kv for one layer: compress keys / values
+        [N, kv_heads, head_dim] and write token t into slot (start_pos + t) % 16 of block
+        block_table[(start_pos + t) // 16] of a registered TurboQuant pool."""
+        bt = np.ascontiguousarray(np.asarray(block_table, dtype=np.int32))
+        _check(self._L.fhip_tq_append_kv(
+            self._h, pool, C.byref(keys._c()), C.byref(values._c()), C.byref(k_rotation._c()),
+            C.byref(v_rotation._c()), C.byref(k_centroids._c()), C.byref(v_centroids._c()),
+            key_bits, value_bits, bt.ctypes.data, bt.size, start_pos))
+
+    def attention_paged_tq_batched(self, q: DeviceTensor, block_tables: Sequence[Sequence[int]],
+                                   seq_lens: Sequence[int], pool: int, k_rotation: DeviceTensor,
+                                   v_rotation: DeviceTensor, k_centroids: DeviceTensor,
+                                   v_centroids: DeviceTensor, key_bits: int, value_bits: int,
+                                   num_kv_heads: int, out: DeviceTensor) -> None:
+        """Decode attention of q [B, qh, hd] (one query per sequence) over a registered
+        TurboQuant pool in one call; block_tables are padded to a common width."""
+        lens = np.ascontiguousarray(np.asarray(seq_lens, dtype=np.uint32))
+        width = max([len(r) for r in block_tables] + [1])
+        bt = np.full((len(block_tables), width), -1, np.int32)
+        for i, row in enumerate(block_tables):
+            bt[i, :len(row)] = row
+        _check(self._L.fhip_attention_paged_tq_batched(
+            self._h, C.byref(q._c()), bt.ctypes.data, width, lens.ctypes.data, pool,
+            C.byref(k_rotation._c()), C.byref(v_rotation._c()), C.byref(k_centroids._c()),
+            C.byref(v_centroids._c()), key_bits, value_bits, num_kv_heads, C.byref(out._c())))
+
     # -- additive ops ---------------------------------------------------------------------------
     def add_rmsnorm(self, residual: DeviceTensor, delta: DeviceTensor, weight: DeviceTensor,
                     eps: float, normed_out: DeviceTensor) -> None:

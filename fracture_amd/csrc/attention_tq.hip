@@ -1106,6 +1106,48 @@ int fhip_launch_attention_tq_decode(void* output, const void* q, const int32_t* 
     return launch_attention(a, pg, fhip_host::as_stream(stream));
 }
 
+int fhip_launch_attention_tq_decode_ptrs(void* output, const void* q, const int32_t* block_table,
+                                         const int32_t* seq_lens, int batch, int max_blocks,
+                                         int num_pages, const void** k_packed_ptrs,
+                                         const void** k_norms_ptrs, const void** v_packed_ptrs,
+                                         const void** v_norms_ptrs, const float* k_rotation,
+                                         const float* v_rotation, const float* k_centroids,
+                                         const float* v_centroids, int num_q_heads,
+                                         int num_kv_heads, int head_dim, int key_bits,
+                                         int value_bits, void* workspace,
+                                         fhip_stream_t stream) {
+    if (batch < 0 || max_blocks <= 0 || num_pages < 0 ||
+        !attn_shape_ok(num_q_heads, num_kv_heads, head_dim, key_bits, value_bits))
+        return hipErrorInvalidValue;
+    if ((int64_t)batch * num_q_heads > (int64_t)1 << 30 || batch > 65535 ||
+        max_blocks * (int64_t)FHIP_PAGE_TOKENS > kMaxTokensTq)
+        return hipErrorInvalidValue;
+    if (batch == 0) return hipSuccess;
+    if (!output || !q || !block_table || !seq_lens || (num_pages > 0 && (!k_packed_ptrs ||
+        !k_norms_ptrs || !v_packed_ptrs || !v_norms_ptrs)) || !k_rotation || !v_rotation ||
+        !k_centroids || !v_centroids || !workspace)
+        return hipErrorInvalidValue;
+    AttnArgs a;
+    a.out = output;
+    a.q = q;
+    a.qs = Queries{block_table, max_blocks, max_blocks, seq_lens, 0, 0, batch};
+    a.nq = batch;
+    a.krot = k_rotation;
+    a.vrot = v_rotation;
+    a.kcent = k_centroids;
+    a.vcent = v_centroids;
+    a.qh = num_q_heads;
+    a.kvh = num_kv_heads;
+    a.hd = head_dim;
+    a.kbits = key_bits;
+    a.vbits = value_bits;
+    a.ws = workspace;
+    PtrPages pg{(const uint8_t* const*)k_packed_ptrs, (const uint8_t* const*)k_norms_ptrs,
+                (const uint8_t* const*)v_packed_ptrs, (const uint8_t* const*)v_norms_ptrs,
+                num_pages};
+    return launch_attention(a, pg, fhip_host::as_stream(stream));
+}
+
 // The reference interface: one sequence, num_tokens queries at positions
 // start_pos .. start_pos + num_tokens - 1, per-block pointer arrays. `ws` holds the split
 // partials (fhip_attention_tq_workspace_bytes(num_tokens, qh, hd, ceil(kv_len / 16)) bytes);

@@ -164,6 +164,47 @@ struct fhip_backend {
     std::unordered_map<uint64_t, PagePool> pools;  // under mu
     uint64_t next_pool = 1;
     std::unordered_map<uint64_t, int> pooled;      // tensor id -> pools holding it (under mu)
+    // TurboQuant plans, keyed on (rotation id, centroids id, bits, levels): what compress and
+    // dequantize derive from the per-layer tables the cache manager uploads once
+    // (quantized_paged_kv_cache.rs:137-170). A plan is dropped when fhip_free,
+    // fhip_copy_to_device or fhip_copy_rows touches either tensor; callers hold plan_mu from
+    // the lookup until the launch that uses the plan is enqueued.
+    struct PlanEntry {
+        uint64_t rot, cent;
+        int bits, levels;
+        fhip_tq_plan* plan;
+    };
+    std::mutex plan_mu;
+    std::vector<PlanEntry> plans;
+
+    // The plan for these tables (built on first use), or null where the MFMA path does not
+    // apply (head_dim other than 128) or the plan cannot be built: callers then launch the
+    // unplanned kernels, which compute the same bytes.
+    fhip_tq_plan* plan_for(uint64_t rot_id, const void* rot, uint64_t cent_id, const void* cent,
+                           int levels, int bits, int head_dim) {
+        if (head_dim != 128) return nullptr;
+        for (const PlanEntry& e : plans)
+            if (e.rot == rot_id && e.cent == cent_id && e.bits == bits && e.levels == levels)
+                return e.plan;
+        fhip_tq_plan* p = nullptr;
+        if (fhip_tq_plan_create((const float*)rot, (const float*)cent, levels, bits, head_dim,
+                                stream, &p) != hipSuccess)
+            return nullptr;
+        plans.push_back(PlanEntry{rot_id, cent_id, bits, levels, p});
+        return p;
+    }
+    void drop_plans(uint64_t id) {
+        std::lock_guard<std::mutex> g(plan_mu);
+        for (size_t i = 0; i < plans.size();) {
+            if (plans[i].rot == id || plans[i].cent == id) {
+                fhip_tq_plan_destroy(plans[i].plan);  // waits for kernels still using it
+                plans[i] = plans.back();
+                plans.pop_back();
+            } else {
+                ++i;
+            }
+        }
+    }
 
     int get_ptr(uint64_t id, void** out) {
         std::lock_guard<std::mutex> g(mu);
@@ -299,6 +340,7 @@ void fhip_backend_destroy(fhip_backend* b) {
     }
     if (b->workspace) (void)hipFree(b->workspace);
     if (b->ws_ev) (void)hipEventDestroy(b->ws_ev);
+    for (auto& e : b->plans) fhip_tq_plan_destroy(e.plan);
     for (auto& kv : b->pools) (void)hipFree((void*)kv.second.dev);
     if (b->rope_freq) (void)hipFree(b->rope_freq);
     (void)hipStreamDestroy(b->stream);
@@ -387,6 +429,7 @@ int fhip_free(fhip_backend* b, const fhip_tensor* t) {
         b->tensors.erase(it);
     }
     set_device(b);
+    b->drop_plans(t->id);
     // Kernels on the backend's stream may still read the buffer.
     HIP_TRY(hipStreamSynchronize(b->stream));
     HIP_TRY(hipFree(p));
@@ -403,6 +446,7 @@ int fhip_copy_to_device(fhip_backend* b, const fhip_tensor* dst, const void* src
                     src_len, (unsigned long long)size);
     if (size == 0) return FHIP_OK;
     set_device(b);
+    b->drop_plans(dst->id);
     HIP_TRY(hipMemcpyAsync(p, src, size, hipMemcpyHostToDevice, b->stream));
     HIP_TRY(hipStreamSynchronize(b->stream));
     return FHIP_OK;
@@ -655,6 +699,7 @@ int fhip_copy_rows(fhip_backend* b, const fhip_tensor* src, const fhip_tensor* d
     const uint64_t row = row_elems * dtype_size(src->dtype);
     if (count == 0 || row == 0) return FHIP_OK;
     set_device(b);
+    b->drop_plans(dst->id);
     HIP_TRY(hipMemcpyAsync((char*)pdst + dst_offset * row, (const char*)ps + src_offset * row,
                            count * row, hipMemcpyDeviceToDevice, b->stream));
     return FHIP_OK;
@@ -786,6 +831,10 @@ int fhip_turboquant_compress(fhip_backend* b, const fhip_tensor* input, const fh
                     shape_str(rotation).c_str(), shape_str(packed_out).c_str(),
                     shape_str(norms_out).c_str());
     set_device(b);
+    std::lock_guard<std::mutex> g(b->plan_mu);
+    if (fhip_tq_plan* plan = b->plan_for(rotation->id, prot, centroids->id, pc, (int)L, bits, (int)hd))
+        return launch_result(fhip_launch_tq_compress_planned(plan, pin, pp, pn, (int)N, (int)H,
+                                                             b->stream));
     return launch_result(fhip_launch_turboquant_compress(pin, (const float*)prot, (const float*)pc,
                                                          pp, pn, (int)N, (int)H, (int)hd, (int)L,
                                                          bits, (int)pd, b->stream));
@@ -846,6 +895,10 @@ int fhip_tq_dequantize(fhip_backend* b, const fhip_tensor* packed, const fhip_te
         return fail(FHIP_ERR_INVALID_SHAPE, "dequantize packed %s norms %s",
                     shape_str(packed).c_str(), shape_str(norms).c_str());
     set_device(b);
+    std::lock_guard<std::mutex> g(b->plan_mu);
+    if (fhip_tq_plan* plan = b->plan_for(rotation->id, prot, centroids->id, pc, (int)L, bits, (int)hd))
+        return launch_result(fhip_launch_tq_dequant_planned(plan, pp, pn, po, (int)N, (int)H,
+                                                            b->stream));
     return launch_result(fhip_launch_tq_dequant(pp, pn, (const float*)prot, (const float*)pc,
                                                 (int)L, po, (int)N, (int)H, (int)hd, bits,
                                                 (int)pd, b->stream));
@@ -1236,6 +1289,189 @@ int fhip_attention_paged_tq_pool(fhip_backend* b, const fhip_tensor* q,
         (int)num_kv_heads, (int)hd, (int)kv_len, (int)start_pos, key_bits, value_bits, (int)kpd,
         (int)vpd, ws, wsb, b->stream);
     b->stage_done(s1);
+    b->ws_done();
+    if (e != hipSuccess) return hip_fail((hipError_t)e);
+    return FHIP_OK;
+}
+
+// QuantizedKvCacheManager::append_kv (quantized_paged_kv_cache.rs:404-500) for one layer over a
+// registered TurboQuant pool: compress keys and values and write token t straight into page
+// block_table[(start_pos + t) / 16], slot (start_pos + t) % 16 of the pool's per-block
+// tensors. The reference compresses into scratch tensors and copies each page's rows with four
+// copy_rows calls per page span.
+int fhip_tq_append_kv(fhip_backend* b, uint64_t pool, const fhip_tensor* keys,
+                      const fhip_tensor* values, const fhip_tensor* k_rotation,
+                      const fhip_tensor* v_rotation, const fhip_tensor* k_centroids,
+                      const fhip_tensor* v_centroids, uint8_t key_bits, uint8_t value_bits,
+                      const int32_t* block_table, size_t num_blocks, size_t start_pos) {
+    CHECK_B(b);
+    CHECK_T(keys);
+    CHECK_T(values);
+    CHECK_T(k_rotation);
+    CHECK_T(v_rotation);
+    CHECK_T(k_centroids);
+    CHECK_T(v_centroids);
+    GET_PTR(b, keys, pk);
+    GET_PTR(b, values, pv);
+    GET_PTR(b, k_rotation, pkr);
+    GET_PTR(b, v_rotation, pvr);
+    GET_PTR(b, k_centroids, pkc);
+    GET_PTR(b, v_centroids, pvc);
+    if (keys->ndim != 3 || keys->dtype != FHIP_FP16 || !same_shape(keys, values) ||
+        values->dtype != FHIP_FP16)
+        return fail(FHIP_ERR_INVALID_SHAPE,
+                    "append_kv keys %s and values %s must be [N, kv_heads, head_dim] FP16",
+                    shape_str(keys).c_str(), shape_str(values).c_str());
+    const uint64_t N = keys->shape[0], kvh = keys->shape[1], hd = keys->shape[2];
+    const uint64_t KL = numel(k_centroids), VL = numel(v_centroids);
+    if (key_bits < 1 || key_bits > 8 || value_bits < 1 || value_bits > 8 || KL < 1 ||
+        KL > (1ull << key_bits) || VL < 1 || VL > (1ull << value_bits) ||
+        k_centroids->dtype != FHIP_FP32 || v_centroids->dtype != FHIP_FP32 ||
+        numel(k_rotation) != hd * hd || numel(v_rotation) != hd * hd ||
+        k_rotation->dtype != FHIP_FP32 || v_rotation->dtype != FHIP_FP32 || kvh == 0 ||
+        hd == 0 || hd > 8192)
+        return fail(FHIP_ERR_INVALID_SHAPE, "append_kv: tables for %u/%u bits, head_dim %llu",
+                    (unsigned)key_bits, (unsigned)value_bits, (unsigned long long)hd);
+    if (N == 0) return FHIP_OK;
+    if (start_pos + N > 0x7fffffffu || N * kvh > 0x7fffffffu)
+        return fail(FHIP_ERR_INVALID_SHAPE, "append_kv: sizes beyond int32");
+    const uint64_t last_block = (start_pos + N - 1) / FHIP_PAGE_TOKENS;
+    if (num_blocks <= last_block)
+        return fail(FHIP_ERR_INVALID_SHAPE, "block table has %zu blocks for position %llu",
+                    num_blocks, (unsigned long long)(start_pos + N - 1));
+    const uint64_t kpd = fhip_tq_packed_dim_per_head(hd, key_bits);
+    const uint64_t vpd = fhip_tq_packed_dim_per_head(hd, value_bits);
+    const uint64_t needs[4] = {FHIP_PAGE_TOKENS * kvh * kpd, FHIP_PAGE_TOKENS * kvh * 2,
+                               FHIP_PAGE_TOKENS * kvh * vpd, FHIP_PAGE_TOKENS * kvh * 2};
+    const int32_t dts[4] = {-1, FHIP_FP16, -1, FHIP_FP16};
+    fhip_backend::PagePool pp;
+    int r = find_pool(b, pool, 4, needs, dts, &pp);
+    if (r) return r;
+    for (uint64_t i = start_pos / FHIP_PAGE_TOKENS; i <= last_block; ++i)
+        if (block_table[i] < 0 || (uint64_t)block_table[i] >= pp.pool_len)
+            return fail(FHIP_ERR_INVALID_SHAPE, "block id %d outside the pool of %zu",
+                        block_table[i], pp.pool_len);
+    set_device(b);
+    std::lock_guard<std::mutex> g(b->launch_mu);
+    void* dbt;
+    int s1;
+    r = b->stage(block_table, (last_block + 1) * sizeof(int32_t), &dbt, &s1);
+    if (r) return r;
+    void* const* dp = (void* const*)pp.dev;
+    const size_t n = pp.pool_len;
+    int e;
+    {
+        std::lock_guard<std::mutex> gp(b->plan_mu);
+        struct Side {
+            const void* x;
+            uint64_t rot_id, cent_id;
+            void *rot, *cent;
+            int levels, bits, list;
+        } sides[2] = {{pk, k_rotation->id, k_centroids->id, pkr, pkc, (int)KL, key_bits, 0},
+                      {pv, v_rotation->id, v_centroids->id, pvr, pvc, (int)VL, value_bits, 2}};
+        e = hipSuccess;
+        for (const Side& sd : sides) {
+            if (e != hipSuccess) break;
+            fhip_tq_plan* plan = b->plan_for(sd.rot_id, sd.rot, sd.cent_id, sd.cent, sd.levels,
+                                             sd.bits, (int)hd);
+            if (plan)
+                e = (hipError_t)fhip_launch_tq_compress_page_ptrs_planned(
+                    plan, sd.x, dp + sd.list * n, dp + (sd.list + 1) * n, (const int32_t*)dbt,
+                    (int)n, (int)start_pos, (int)N, (int)kvh, b->stream);
+            else
+                e = (hipError_t)fhip_launch_tq_compress_page_ptrs(
+                    sd.x, (const float*)sd.rot, (const float*)sd.cent, sd.levels, sd.bits,
+                    dp + sd.list * n, dp + (sd.list + 1) * n, (const int32_t*)dbt, (int)n,
+                    (int)start_pos, (int)N, (int)kvh, (int)hd, b->stream);
+        }
+    }
+    b->stage_done(s1);
+    if (e != hipSuccess) return hip_fail((hipError_t)e);
+    return FHIP_OK;
+}
+
+// Decode attention for a batch of sequences over a registered TurboQuant pool in one call:
+// sequence i attends seq_lens[i] positions through row i of block_tables [B, max_blocks]. The
+// engine dispatches Backend::attention_paged_tq once per sequence instead
+// (crates/fracture-engine/src/batched.rs:145-194); the kernels here run the whole batch.
+int fhip_attention_paged_tq_batched(fhip_backend* b, const fhip_tensor* q,
+                                    const int32_t* block_tables, size_t max_blocks,
+                                    const uint32_t* seq_lens, uint64_t pool,
+                                    const fhip_tensor* k_rotation, const fhip_tensor* v_rotation,
+                                    const fhip_tensor* k_centroids,
+                                    const fhip_tensor* v_centroids, uint8_t key_bits,
+                                    uint8_t value_bits, size_t num_kv_heads,
+                                    const fhip_tensor* out) {
+    CHECK_B(b);
+    CHECK_T(q);
+    CHECK_T(k_rotation);
+    CHECK_T(v_rotation);
+    CHECK_T(k_centroids);
+    CHECK_T(v_centroids);
+    CHECK_T(out);
+    GET_PTR(b, q, pq);
+    GET_PTR(b, out, po);
+    GET_PTR(b, k_rotation, pkr);
+    GET_PTR(b, v_rotation, pvr);
+    GET_PTR(b, k_centroids, pkc);
+    GET_PTR(b, v_centroids, pvc);
+    if (q->ndim != 3 || q->dtype != FHIP_FP16 || out->dtype != FHIP_FP16 ||
+        numel(out) != numel(q))
+        return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged_tq_batched q %s out %s",
+                    shape_str(q).c_str(), shape_str(out).c_str());
+    const uint64_t B = q->shape[0], qh = q->shape[1], hd = q->shape[2];
+    if (num_kv_heads == 0 || qh % num_kv_heads != 0 || qh / num_kv_heads > 8 || key_bits < 1 ||
+        key_bits > 8 || value_bits < 1 || value_bits > 8 || numel(k_rotation) != hd * hd ||
+        numel(v_rotation) != hd * hd || numel(k_centroids) < (1ull << key_bits) ||
+        numel(v_centroids) < (1ull << value_bits) || hd % 8 != 0 || hd > 256)
+        return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged_tq_batched arguments");
+    if (B > 65535 || max_blocks == 0 || max_blocks > 65536)
+        return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged_tq_batched: %llu sequences of up "
+                    "to %zu blocks (at most 65535 and 65536)", (unsigned long long)B, max_blocks);
+    const uint64_t kpd = fhip_tq_packed_dim_per_head(hd, key_bits);
+    const uint64_t vpd = fhip_tq_packed_dim_per_head(hd, value_bits);
+    const uint64_t needs[4] = {FHIP_PAGE_TOKENS * num_kv_heads * kpd,
+                               FHIP_PAGE_TOKENS * num_kv_heads * 2,
+                               FHIP_PAGE_TOKENS * num_kv_heads * vpd,
+                               FHIP_PAGE_TOKENS * num_kv_heads * 2};
+    const int32_t dts[4] = {-1, -1, -1, -1};
+    fhip_backend::PagePool pp;
+    int r = find_pool(b, pool, 4, needs, dts, &pp);
+    if (r) return r;
+    for (uint64_t i = 0; i < B; ++i) {
+        if (seq_lens[i] > max_blocks * FHIP_PAGE_TOKENS)
+            return fail(FHIP_ERR_INVALID_SHAPE, "sequence %llu: %u positions in %zu blocks",
+                        (unsigned long long)i, seq_lens[i], max_blocks);
+        const uint64_t nb = (seq_lens[i] + FHIP_PAGE_TOKENS - 1) / FHIP_PAGE_TOKENS;
+        for (uint64_t j = 0; j < nb; ++j) {
+            const int32_t id = block_tables[i * max_blocks + j];
+            if (id < 0 || (uint64_t)id >= pp.pool_len)
+                return fail(FHIP_ERR_INVALID_SHAPE, "sequence %llu: block id %d outside the "
+                            "pool of %zu", (unsigned long long)i, id, pp.pool_len);
+        }
+    }
+    if (B == 0) return FHIP_OK;
+    set_device(b);
+    std::lock_guard<std::mutex> g(b->launch_mu);
+    void *dbt, *dlen;
+    int s1, s2;
+    r = b->stage(block_tables, B * max_blocks * sizeof(int32_t), &dbt, &s1);
+    if (r) return r;
+    r = b->stage(seq_lens, B * sizeof(uint32_t), &dlen, &s2);
+    if (r) return r;
+    const size_t wsb = fhip_attention_tq_workspace_bytes((int)B, (int)qh, (int)hd, (int)max_blocks);
+    void* ws;
+    r = b->get_workspace(wsb, &ws);
+    if (r) return r;
+    const void** dp = pp.dev;
+    const size_t n = pp.pool_len;
+    int e = fhip_launch_attention_tq_decode_ptrs(
+        po, pq, (const int32_t*)dbt, (const int32_t*)dlen, (int)B, (int)max_blocks, (int)n, dp,
+        dp + n, dp + 2 * n, dp + 3 * n, (const float*)pkr, (const float*)pvr, (const float*)pkc,
+        (const float*)pvc, (int)qh, (int)num_kv_heads, (int)hd, key_bits, value_bits, ws,
+        b->stream);
+    b->stage_done(s1);
+    b->stage_done(s2);
     b->ws_done();
     if (e != hipSuccess) return hip_fail((hipError_t)e);
     return FHIP_OK;

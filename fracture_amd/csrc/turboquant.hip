@@ -82,6 +82,36 @@ struct PageDst {
     }
 };
 
+// The same page layout with one allocation per page, as QuantizedKvCacheManager allocates
+// them (quantized_paged_kv_cache.rs:82-133): packed_pages[p] / norm_pages[p] are the device
+// addresses of page p's packed rows and norms.
+struct PtrPageDst {
+    uint8_t* const* packed_pages;
+    uint8_t* const* norm_pages;
+    const int32_t* page_ids;
+    int64_t first_pos;
+    int kvh, num_pages;
+    int64_t pd;
+    __device__ bool slot(int64_t m, int64_t& page, int64_t& off) const {
+        const int64_t t = m / kvh;
+        const int64_t hh = m - t * kvh;
+        const int64_t pos = first_pos + t;
+        page = page_ids[pos / FHIP_PAGE_TOKENS];
+        off = (pos % FHIP_PAGE_TOKENS) * kvh + hh;
+        return page >= 0 && page < num_pages;
+    }
+    __device__ uint8_t* prow(int64_t m) const {
+        int64_t page, off;
+        if (!slot(m, page, off)) return nullptr;
+        return packed_pages[page] + off * pd;
+    }
+    __device__ uint16_t* nptr(int64_t m) const {
+        int64_t page, off;
+        if (!slot(m, page, off)) return nullptr;
+        return (uint16_t*)norm_pages[page] + off;
+    }
+};
+
 // The wave's index in its workgroup, as a wave-uniform (scalar) value: the compiler cannot
 // tell that threadIdx.x >> 6 is uniform, and would turn tile loops into divergent ones.
 __device__ __forceinline__ int wave_id() {
@@ -1046,6 +1076,26 @@ int fhip_launch_tq_compress_pages(const void* input, const float* rotation,
                               head_dim, fhip_host::as_stream(stream));
 }
 
+int fhip_launch_tq_compress_page_ptrs(const void* input, const float* rotation,
+                                      const float* centroids, int n_levels, int bits,
+                                      void* const* packed_pages, void* const* norm_pages,
+                                      const int32_t* page_ids, int num_pages, int first_pos,
+                                      int num_tokens, int num_kv_heads, int head_dim,
+                                      fhip_stream_t stream) {
+    if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || head_dim > 8192 ||
+        first_pos < 0 || num_pages < 0 || !tq_args_ok(n_levels, bits))
+        return hipErrorInvalidValue;
+    const int64_t rows = (int64_t)num_tokens * num_kv_heads;
+    if (rows == 0) return hipSuccess;
+    if (!input || !rotation || !centroids || !packed_pages || !norm_pages || !page_ids)
+        return hipErrorInvalidValue;
+    const int64_t pd = ceil_div((int64_t)head_dim * bits, 8);
+    PtrPageDst dst{(uint8_t* const*)packed_pages, (uint8_t* const*)norm_pages, page_ids,
+                   first_pos, num_kv_heads, num_pages, pd};
+    return launch_compress<0>(input, rotation, centroids, n_levels, bits, dst, nullptr, rows,
+                              head_dim, fhip_host::as_stream(stream));
+}
+
 int fhip_launch_tq_quantize_pack(const float* y, const float* centroids, int n_levels, int bits,
                                  void* packed_out, int rows, int head_dim,
                                  int packed_dim_per_head, fhip_stream_t stream) {
@@ -1152,6 +1202,24 @@ int fhip_launch_tq_compress_pages_planned(const fhip_tq_plan* plan, const void* 
     if (!input || !packed_pool || !norms_pool || !page_ids) return hipErrorInvalidValue;
     PageDst dst{(uint8_t*)packed_pool, (uint8_t*)norms_pool, page_packed_bytes, page_norm_bytes,
                 page_ids, first_pos, num_kv_heads, num_pages, pd};
+    const TqPlanDev* p = plan->dev;
+    return launch_compress<0>(input, p->rot, p->cent, plan->n_levels, plan->bits, dst, nullptr,
+                              rows, plan->head_dim, fhip_host::as_stream(stream), p);
+}
+
+int fhip_launch_tq_compress_page_ptrs_planned(const fhip_tq_plan* plan, const void* input,
+                                              void* const* packed_pages,
+                                              void* const* norm_pages, const int32_t* page_ids,
+                                              int num_pages, int first_pos, int num_tokens,
+                                              int num_kv_heads, fhip_stream_t stream) {
+    if (!plan || num_tokens < 0 || num_kv_heads <= 0 || first_pos < 0 || num_pages < 0)
+        return hipErrorInvalidValue;
+    const int64_t rows = (int64_t)num_tokens * num_kv_heads;
+    if (rows == 0) return hipSuccess;
+    if (!input || !packed_pages || !norm_pages || !page_ids) return hipErrorInvalidValue;
+    const int64_t pd = ceil_div((int64_t)plan->head_dim * plan->bits, 8);
+    PtrPageDst dst{(uint8_t* const*)packed_pages, (uint8_t* const*)norm_pages, page_ids,
+                   first_pos, num_kv_heads, num_pages, pd};
     const TqPlanDev* p = plan->dev;
     return launch_compress<0>(input, p->rot, p->cent, plan->n_levels, plan->bits, dst, nullptr,
                               rows, plan->head_dim, fhip_host::as_stream(stream), p);

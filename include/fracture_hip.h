@@ -222,6 +222,18 @@ int fhip_launch_tq_compress_pages(const void* input, const float* rotation,
                                   int first_pos, int num_tokens, int num_kv_heads, int head_dim,
                                   fhip_stream_t stream);
 
+/* The page writer for pages that are separate allocations, as QuantizedKvCacheManager
+ * allocates them (quantized_paged_kv_cache.rs:82-133): packed_pages[p] / norm_pages[p]
+ * (device arrays of num_pages addresses) hold page p's packed rows [16, kvh*pd] and norms
+ * [16, kvh] fp16. Token t goes to page page_ids[(first_pos + t) / 16], slot
+ * (first_pos + t) % 16; rows whose page id is outside [0, num_pages) are not written. */
+int fhip_launch_tq_compress_page_ptrs(const void* input, const float* rotation,
+                                      const float* centroids, int n_levels, int bits,
+                                      void* const* packed_pages, void* const* norm_pages,
+                                      const int32_t* page_ids, int num_pages, int first_pos,
+                                      int num_tokens, int num_kv_heads, int head_dim,
+                                      fhip_stream_t stream);
+
 /* launch_turboquant_decompress with an explicit codebook size (codes index only the first
  * n_levels centroids; the reference form assumes 2^bits). */
 int fhip_launch_tq_dequant(const void* packed_in, const void* norms_in, const float* rotation,
@@ -250,6 +262,11 @@ int fhip_launch_tq_compress_pages_planned(const fhip_tq_plan* plan, const void* 
                                           const int32_t* page_ids, int num_pages, int first_pos,
                                           int num_tokens, int num_kv_heads,
                                           fhip_stream_t stream);
+int fhip_launch_tq_compress_page_ptrs_planned(const fhip_tq_plan* plan, const void* input,
+                                              void* const* packed_pages,
+                                              void* const* norm_pages, const int32_t* page_ids,
+                                              int num_pages, int first_pos, int num_tokens,
+                                              int num_kv_heads, fhip_stream_t stream);
 int fhip_launch_tq_dequant_planned(const fhip_tq_plan* plan, const void* packed_in,
                                    const void* norms_in, void* output, int num_tokens,
                                    int num_kv_heads, fhip_stream_t stream);
@@ -274,6 +291,19 @@ int fhip_launch_attention_tq_decode(void* output, const void* q, const int32_t* 
                                     int num_q_heads, int num_kv_heads, int head_dim,
                                     int key_bits, int value_bits, void* workspace,
                                     fhip_stream_t stream);
+
+/* fhip_launch_attention_tq_decode over pages that are separate allocations: page p's four
+ * parts are at k_packed_ptrs[p], k_norms_ptrs[p], v_packed_ptrs[p], v_norms_ptrs[p] (device
+ * arrays of num_pages addresses). Same workspace as fhip_launch_attention_tq_decode. */
+int fhip_launch_attention_tq_decode_ptrs(void* output, const void* q, const int32_t* block_table,
+                                         const int32_t* seq_lens, int batch, int max_blocks,
+                                         int num_pages, const void** k_packed_ptrs,
+                                         const void** k_norms_ptrs, const void** v_packed_ptrs,
+                                         const void** v_norms_ptrs, const float* k_rotation,
+                                         const float* v_rotation, const float* k_centroids,
+                                         const float* v_centroids, int num_q_heads,
+                                         int num_kv_heads, int head_dim, int key_bits,
+                                         int value_bits, void* workspace, fhip_stream_t stream);
 
 /* Batched decode attention over an FP16 page pool (the FP16 form of the call above, for
  * batched decode): q [B, qh, hd] fp16, block_table [B, max_blocks] int32, seq_lens [B] int32;
@@ -403,6 +433,34 @@ int fhip_attention_paged_tq_pool(fhip_backend* b, const fhip_tensor* q,
                                  const fhip_tensor* k_centroids, const fhip_tensor* v_centroids,
                                  uint8_t key_bits, uint8_t value_bits, size_t num_kv_heads,
                                  size_t kv_len, size_t start_pos, const fhip_tensor* out);
+
+/* QuantizedKvCacheManager::append_kv for one layer (quantized_paged_kv_cache.rs:404-500) over
+ * a registered (K packed, K norms, V packed, V norms) pool: keys / values [N, kvh, hd] FP16 are
+ * compressed with the layer's rotations and codebooks and token t is written straight into
+ * slot (start_pos + t) % 16 of block block_table[(start_pos + t) / 16] (host array of
+ * num_blocks ids). The reference compresses into scratch tensors and then issues four
+ * copy_rows per page span. The backend keeps one TurboQuant plan per (rotation, codebook,
+ * bits) for this and for fhip_turboquant_compress / fhip_tq_dequantize; writing or freeing
+ * either tensor through this API drops the plan. */
+int fhip_tq_append_kv(fhip_backend* b, uint64_t pool, const fhip_tensor* keys,
+                      const fhip_tensor* values, const fhip_tensor* k_rotation,
+                      const fhip_tensor* v_rotation, const fhip_tensor* k_centroids,
+                      const fhip_tensor* v_centroids, uint8_t key_bits, uint8_t value_bits,
+                      const int32_t* block_table, size_t num_blocks, size_t start_pos);
+
+/* Decode attention of a batch over a registered TurboQuant pool in one call (the engine
+ * dispatches Backend::attention_paged_tq per sequence, crates/fracture-engine/src/
+ * batched.rs:145-194): q [B, qh, hd] fp16, one query per sequence at its last position;
+ * sequence i attends seq_lens[i] positions through row i of block_tables (host,
+ * [B, max_blocks]); out [B, qh, hd] fp16. max_blocks is at most 65536. */
+int fhip_attention_paged_tq_batched(fhip_backend* b, const fhip_tensor* q,
+                                    const int32_t* block_tables, size_t max_blocks,
+                                    const uint32_t* seq_lens, uint64_t pool,
+                                    const fhip_tensor* k_rotation, const fhip_tensor* v_rotation,
+                                    const fhip_tensor* k_centroids,
+                                    const fhip_tensor* v_centroids, uint8_t key_bits,
+                                    uint8_t value_bits, size_t num_kv_heads,
+                                    const fhip_tensor* out);
 
 /* --- additive handle ops --------------------------------------------------------------- */
 
