@@ -51,6 +51,8 @@ SIGNATURES = {
     "fhip_launch_attention_paged_tq_ws": (I, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I,
                                               I, I, I, I, P, SZ, P]),
     "fhip_launch_paged_attention_ws": (I, [P, P, P, P, P, I, I, I, I, I, I, I, P, SZ, P]),
+    "fhip_launch_attention_paged_tq_noalloc": (I, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I,
+                                                   I, I, I, I, I, I, P]),
     "fhip_launch_rmsnorm_ex": (I, [P, P, P, F, I, I, I, P]),
     "fhip_launch_add_ex": (I, [P, P, P, I64, I, P]),
     "fhip_launch_silu_mul_ex": (I, [P, P, P, I64, I, P]),

@@ -1038,6 +1038,41 @@ int launch_attention(const AttnArgs& a, const Pages& pg, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Split-partial scratch of fhip_launch_attention_paged_tq_noalloc: one copy per device, held
+// until the process ends. Host code never passes the name `scratch` to a kernel (on the host
+// it is a stand-in, not a device address); it resolves each device's address once with
+// hipGetSymbolAddress and passes that.
+constexpr size_t kNoAllocScratchBytes = FHIP_TQ_ATTN_SCRATCH_BYTES;
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// The scratch address on `dev`, looked up on the first call for that device (made current for
+// the lookup, then restored).
+hipError_t scratch_on_device(int dev, void** out) {
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        int cur = -1;
+        hipError_t e = hipGetDevice(&cur);
+        if (e != hipSuccess) return e;
+        if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return e;
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (cur != dev) {
+            hipError_t e2 = hipSetDevice(cur);
+            if (e == hipSuccess) e = e2;
+        }
+        if (e != hipSuccess) return e;
+        if (!ptr) return hipErrorInvalidSymbol;
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return hipSuccess;
+}
+
 bool attn_shape_ok(int qh, int kvh, int hd, int kbits, int vbits) {
     return kvh > 0 && qh > 0 && qh % kvh == 0 && qh / kvh <= kMaxG && hd % 8 == 0 && hd > 0 &&
            hd <= kMaxHd && kbits >= 1 && kbits <= 8 && vbits >= 1 && vbits <= 8 &&
@@ -1223,6 +1258,37 @@ int fhip_launch_attention_paged_tq(void* output, const void* q, const int* block
                                   num_kv_heads, head_dim, kv_len, start_pos, key_bits,
                                   value_bits, k_packed_dim_per_head, v_packed_dim_per_head,
                                   nullptr, 0, fhip_host::as_stream(stream));
+}
+
+int fhip_launch_attention_paged_tq_noalloc(void* output, const void* q, const int* block_table,
+                                           const void** k_packed_ptrs, const void** k_norms_ptrs,
+                                           const void** v_packed_ptrs, const void** v_norms_ptrs,
+                                           const float* k_rotation, const float* v_rotation,
+                                           const float* k_centroids, const float* v_centroids,
+                                           int num_tokens, int num_q_heads, int num_kv_heads,
+                                           int head_dim, int kv_len, int start_pos, int key_bits,
+                                           int value_bits, int k_packed_dim_per_head,
+                                           int v_packed_dim_per_head, fhip_stream_t stream) {
+    if (num_tokens < 0 || kv_len < 0 || num_q_heads <= 0 || head_dim <= 0)
+        return hipErrorInvalidValue;
+    if (num_tokens == 0) return hipSuccess;
+    const int nblocks = (kv_len + FHIP_PAGE_TOKENS - 1) / FHIP_PAGE_TOKENS;
+    const size_t need = ws_layout(num_tokens, num_q_heads, head_dim,
+                                  (nblocks > 0 ? nblocks : 1) * FHIP_PAGE_TOKENS, nullptr,
+                                  nullptr, nullptr);
+    if (need > kNoAllocScratchBytes) return hipErrorOutOfMemory;
+    hipStream_t s = fhip_host::as_stream(stream);
+    int dev = -1;
+    hipError_t e = hipStreamGetDevice(s, &dev);
+    if (e != hipSuccess) return e;
+    void* ws = nullptr;
+    if ((e = scratch_on_device(dev, &ws)) != hipSuccess) return e;
+    return attention_paged_tq_ref(output, q, block_table, k_packed_ptrs, k_norms_ptrs,
+                                  v_packed_ptrs, v_norms_ptrs, k_rotation, v_rotation,
+                                  k_centroids, v_centroids, num_tokens, num_q_heads,
+                                  num_kv_heads, head_dim, kv_len, start_pos, key_bits,
+                                  value_bits, k_packed_dim_per_head, v_packed_dim_per_head, ws,
+                                  kNoAllocScratchBytes, s);
 }
 
 int fhip_launch_attention_paged_tq_ws(void* output, const void* q, const int* block_table,

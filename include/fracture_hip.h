@@ -162,6 +162,29 @@ int fhip_launch_paged_attention_ws(void* output, const void* q, const int* block
                                    int num_blocks_in_seq, void* workspace,
                                    size_t workspace_bytes, fhip_stream_t stream);
 
+/* fhip_launch_attention_paged_tq that allocates nothing and takes no workspace. It has no
+ * counterpart in the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The split
+ * partials live in a static device array of FHIP_TQ_ATTN_SCRATCH_BYTES per GPU, loaded with
+ * the library and held until the process ends; a call whose partials need more
+ * (fhip_attention_tq_workspace_bytes(num_tokens, num_q_heads, head_dim, ceil(kv_len / 16)),
+ * e.g. one decode token of 32 heads at head_dim 128 up to 1,048,576 positions) returns
+ * hipErrorOutOfMemory and launches nothing. Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (different streams, or host threads enqueueing at once) race
+ * on it and must be ordered by the caller. The kernels write every partial they read, so
+ * nothing in the array needs to start at zero. The stream's device is used; the first call on
+ * each device looks up the array's address there. */
+#define FHIP_TQ_ATTN_SCRATCH_BYTES ((size_t)32 << 20)
+int fhip_launch_attention_paged_tq_noalloc(void* output, const void* q, const int* block_table,
+                                           const void** k_packed_ptrs, const void** k_norms_ptrs,
+                                           const void** v_packed_ptrs, const void** v_norms_ptrs,
+                                           const float* k_rotation, const float* v_rotation,
+                                           const float* k_centroids, const float* v_centroids,
+                                           int num_tokens, int num_q_heads, int num_kv_heads,
+                                           int head_dim, int kv_len, int start_pos, int key_bits,
+                                           int value_bits, int k_packed_dim_per_head,
+                                           int v_packed_dim_per_head, fhip_stream_t stream);
+
 /* dtype-generic forms of rmsnorm / add / silu_mul (FHIP_FP16, FHIP_BF16, FHIP_FP32). */
 int fhip_launch_rmsnorm_ex(void* output, const void* input, const void* weight, float eps,
                            int rows, int cols, int dtype, fhip_stream_t stream);
