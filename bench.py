@@ -3,13 +3,20 @@
 Default workload (the metric's configuration): one Llama-3.1-8B decode step's elementwise
 chain at batch 64, fp16 — embedding gather from a [128256, 4096] table, RoPE on
 Q [64, 32, 128] and K [64, 8, 128] (theta 500000, positions in [0, 8192)), SwiGLU on
-[64, 14336], and two residual adds fused with RMSNorm on [64, 4096] — with inputs resident
-in HBM. A step is the five launches; 20 consecutive steps are captured in one HIP graph
-(`--steps-per-graph`) and replayed (eager timing reported too).
+[64, 14336], and two residual adds fused with RMSNorm on [64, 4096] — with inputs in device
+memory. A step is the five launches; 20 consecutive steps are captured in one HIP graph
+(`--steps-per-graph`) and replayed (eager timing reported too). Replaying one set of inputs
+keeps its 12 MB in L2 / MALL, as activations written by the previous kernel of a real step
+would be; `cold_inputs` repeats the measurement over 40 input sets (more than the 256 MB MALL)
+so that every step reads its inputs from HBM.
 
 Printed: one JSON line with the metric (whole-chain algorithmic GB/s; ms_per_step), per-kernel
-microseconds and GB/s, the roofline object for the dominant kernel (SwiGLU) and the CPU
-baseline (the oracle's restatement of the reference's CPU path, single thread, on this host).
+microseconds and GB/s, the roofline object for the kernel that takes the most time per step,
+compact results of the other configurations (`configs`: prefill-shaped reductions, TurboQuant
+compress / dequantize, TurboQuant decode attention both over contiguous pools and through the
+handle runtime over per-block tensors) and the CPU baseline: the oracle's restatement of the
+reference's CPU formulas on this host, one thread and all host cores (up to 16), for the chain
+and for every configuration (bounded samples, scaled to the full workload).
 
 Other workloads (parity-tested configurations, printed as their own JSON lines):
   --workload prefill      add+RMSNorm [8192,4096], SwiGLU [8192,14336], softmax/argmax [64,128256]
@@ -52,6 +59,8 @@ def parse():
                     help="turn two rocprofv3 --pmc runs of --workload pmc into "
                          "profiles/traffic.json")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="default run: leave out the other configurations' results")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true", help="time the chain without a HIP graph")
     ap.add_argument("--steps-per-graph", type=int, default=20,
@@ -123,13 +132,14 @@ def traffic_of(kernel_key: str):
 # ---------------------------------------------------------------------------------------
 # decode-step chain (the headline)
 # ---------------------------------------------------------------------------------------
-def decode_inputs(torch, dev, seed=0):
+def decode_inputs(torch, dev, seed=0, table=None):
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     B, V, H, QH, KVH, HD, FF = 64, 128256, 4096, 32, 8, 128, 14336
     f16 = torch.float16
     x = {}
-    x["table"] = (torch.randn((V, H), generator=g, device=dev) * 0.02).to(f16)
+    x["table"] = table if table is not None else (
+        torch.randn((V, H), generator=g, device=dev) * 0.02).to(f16)
     x["ids"] = torch.randint(0, V, (B,), generator=g, device=dev, dtype=torch.int32)
     x["emb"] = torch.empty((B, H), dtype=f16, device=dev)
     x["q"] = torch.randn((B, QH, HD), generator=g, device=dev).to(f16)
@@ -149,6 +159,56 @@ def decode_inputs(torch, dev, seed=0):
     x["n1"] = torch.empty((B, H), dtype=f16, device=dev)
     x["n2"] = torch.empty((B, H), dtype=f16, device=dev)
     return x
+
+
+def decode_input_sets(torch, dev, n, base):
+    """n further sets of the chain's activations (ids, positions, q/k, gate/up, h/deltas and
+    outputs), sharing the table, frequencies and norm weights of `base`."""
+    sets = []
+    for i in range(n):
+        x = decode_inputs(torch, dev, seed=100 + i, table=base["table"])
+        for k in ("freqs", "w1", "w2"):
+            x[k] = base[k]
+        sets.append(x)
+    return sets
+
+
+# launches of each kernel per decode step
+DECODE_COUNTS = {"embedding": 1, "rope": 1, "silu_mul": 1, "add_rmsnorm": 2}
+DECODE_KERNELS = {"embedding": "embedding_vec_kernel", "rope": "rope_wave_kernel<fp16>",
+                  "silu_mul": "silu_mul_vec_kernel<fp16>",
+                  "add_rmsnorm": "rmsnorm_vec_kernel<fp16, residual, 1>"}
+
+
+def cpu_threads() -> int:
+    """Host threads for the all-core CPU baseline: the cores this process may run on, at most
+    16 (one GPU's share of the host)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def par_rows(fn, arrays, rows, threads):
+    """fn(*row_slices) over `threads` contiguous row ranges of `arrays` at once (the oracle's C
+    functions release the GIL)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    cuts = [rows * i // threads for i in range(threads + 1)]
+    with ThreadPoolExecutor(threads) as ex:
+        list(ex.map(lambda i: fn(*(a[cuts[i]:cuts[i + 1]] for a in arrays)), range(threads)))
+
+
+def median_time(fn, min_runs=3, seconds=1.0):
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < min_runs or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
 
 
 def decode_bytes():
@@ -176,9 +236,10 @@ def decode_step(ops):
         f()
 
 
-def cpu_decode_baseline(seconds: float):
-    """The oracle's restatement of the reference's CPU formulas for the same chain, one
-    thread, median over as many steps as fit in `seconds` (at least 3)."""
+def cpu_decode_baseline(seconds: float, threads: int = 1):
+    """The oracle's restatement of the reference's CPU formulas for the same chain, on one
+    thread or split by rows over `threads`, median over as many steps as fit in `seconds`
+    (at least 3)."""
     import numpy as np
 
     import oracle
@@ -199,7 +260,7 @@ def cpu_decode_baseline(seconds: float):
     d2 = rng.standard_normal((B, H)).astype(np.float16)
     w = rng.uniform(0.5, 1.5, H).astype(np.float16)
 
-    def step(h):
+    def step1(h):
         oracle.embedding(table, ids)
         oracle.rope(q, pos, fr)
         oracle.rope(k, pos, fr)
@@ -208,15 +269,22 @@ def cpu_decode_baseline(seconds: float):
         h, _ = oracle.add_rmsnorm(h, d2, w, 1e-5)
         return h
 
-    times = []
-    t_end = time.perf_counter() + seconds
-    while len(times) < 3 or time.perf_counter() < t_end:
-        t0 = time.perf_counter()
-        h = step(h)
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
-    return med * 1e6, len(times)
+    def step_par(h):
+        par_rows(lambda i: oracle.embedding(table, i), [ids], B, threads)
+        par_rows(lambda a, p: oracle.rope(a, p, fr), [q, pos], B, threads)
+        par_rows(lambda a, p: oracle.rope(a, p, fr), [k, pos], B, threads)
+        par_rows(oracle.silu_mul, [g, u], B, threads)
+        par_rows(lambda a, b: oracle.add_rmsnorm(a, b, w, 1e-5), [h, d1], B, threads)
+        par_rows(lambda a, b: oracle.add_rmsnorm(a, b, w, 1e-5), [h, d2], B, threads)
+        return h
+
+    state = {"h": h}
+
+    def run():
+        state["h"] = step1(state["h"]) if threads == 1 else step_par(state["h"])
+
+    med, n = median_time(run, 3, seconds)
+    return med * 1e6, n
 
 
 def run_decode(args, torch, K, dev):
@@ -272,6 +340,27 @@ def run_decode(args, torch, K, dev):
     us_step = s_ev.elapsed_time(e_ev) * 1e3 / args.steps
     eager_us = timer.time_us(lambda: decode_step(ops), max(20, args.steps // 4))
 
+    # the same chain with every step on its own inputs (40 sets, ~370 MB: more than the MALL),
+    # so that each step reads its activations from HBM
+    cold_us = None
+    if not args.eager:
+        sets = decode_input_sets(torch, dev, 40, x)
+        cold_ops = [decode_ops(K, xs) for xs in sets]
+        gc = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gc):
+            for o in cold_ops:
+                decode_step(o)
+        gc.replay()
+        torch.cuda.synchronize()
+        reps = max(1, args.steps // len(cold_ops))
+        s_ev.record()
+        for _ in range(reps):
+            gc.replay()
+        e_ev.record()
+        torch.cuda.synchronize()
+        cold_us = s_ev.elapsed_time(e_ev) * 1e3 / (reps * len(cold_ops))
+        del gc, cold_ops, sets
+
     # per-kernel average launch durations (back-to-back launches between two events)
     per = {}
     for name in ("embedding", "rope", "silu_mul", "add_rmsnorm"):
@@ -282,12 +371,22 @@ def run_decode(args, torch, K, dev):
                      "traffic": traffic_of({"embedding": "decode_embedding", "rope": "decode_rope",
                                             "silu_mul": "silu_mul_64x14336",
                                             "add_rmsnorm": "decode_add_rmsnorm"}[name])}
-    dom = "silu_mul"
-    traffic = traffic_of("silu_mul_64x14336")
-    roof = {"kernel": "silu_mul_vec_kernel<fp16> [64,14336]", "bound": "hbm",
+    # the roofline kernel: the one that takes the most time per step (launches x duration)
+    for name, e in per.items():
+        e["launches_per_step"] = DECODE_COUNTS[name]
+        e["us_per_step"] = round(e["us"] * DECODE_COUNTS[name], 3)
+    dom = max(per, key=lambda n: per[n]["us_per_step"])
+    traffic_key = {"embedding": "decode_embedding", "rope": "decode_rope",
+                   "silu_mul": "silu_mul_64x14336", "add_rmsnorm": "decode_add_rmsnorm"}[dom]
+    roof = {"kernel": DECODE_KERNELS[dom], "bound": "hbm",
             "achieved": per[dom]["GB/s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": round(per[dom]["GB/s"] / PEAK_HBM_GBS, 4), "traffic": traffic,
-            "algorithmic_bytes": nbytes[dom], "avg_launch_us": per[dom]["us"]}
+            "frac": round(per[dom]["GB/s"] / PEAK_HBM_GBS, 4),
+            "traffic": traffic_of(traffic_key), "algorithmic_bytes": nbytes[dom],
+            "avg_launch_us": per[dom]["us"],
+            "launches_per_step": DECODE_COUNTS[dom],
+            "note": "average launch duration from a HIP graph of 50 back-to-back launches "
+                    "(HIP events on the launch stream); an empty kernel costs ~1.7 us per "
+                    "launch the same way"}
 
     result = {
         "metric": METRIC,
@@ -309,18 +408,39 @@ def run_decode(args, torch, K, dev):
                    "launch": "eager" if args.eager else f"hip graph, {per_graph} steps per graph",
                    "chain_bytes": chain_bytes},
         "eager_us_per_step": round(eager_us, 3),
+        "cold_inputs": None if cold_us is None else {
+            "us_per_step": round(cold_us, 3), "GB/s": round(gbs(chain_bytes, cold_us), 1),
+            "input_sets": 40},
         "kernels": per,
         "roofline": roof,
     }
     if not args.no_cpu_baseline:
-        cpu_us, n = cpu_decode_baseline(args.cpu_seconds)
+        cpu_us, n = cpu_decode_baseline(args.cpu_seconds / 2)
+        th = cpu_threads()
+        cpu_par, n2 = cpu_decode_baseline(args.cpu_seconds / 2, th)
         result["cpu_baseline"] = {
             "value": round(gbs(chain_bytes, cpu_us), 3), "unit": "GB/s", "cores": 1,
             "kind": "port", "us_per_step": round(cpu_us, 1),
             "sample": f"median of {n} steps of the same chain (same shapes) through the C "
-                      f"restatement of the reference's CPU formulas, one thread, "
-                      f"{os.cpu_count()} host cores visible"}
+                      f"restatement of the reference's CPU formulas, one thread",
+            "all_cores": {"cores": th, "us_per_step": round(cpu_par, 1),
+                          "value": round(gbs(chain_bytes, cpu_par), 3),
+                          "sample": f"median of {n2} steps, each op split by rows over {th} "
+                                    f"threads"},
+            "host": host_cpu()}
     return result
+
+
+def host_cpu():
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"model": model, "logical_cpus": os.cpu_count(), "threads_used": cpu_threads()}
 
 
 # ---------------------------------------------------------------------------------------
@@ -622,6 +742,222 @@ def pmc_keys():
     return keys
 
 
+def runtime_attention_inputs(torch, K, dev):
+    """The decode-attention workload as the engine drives it through the handle runtime: one
+    (K packed, K norms, V packed, V norms) tensor per block, registered as a pool, filled with
+    append_kv per sequence; the call is fhip_attention_paged_tq_batched. Returns (fn, bytes,
+    cleanup)."""
+    import numpy as np
+
+    from fracture_amd import DType, HipBackend
+    from fracture_amd import turboquant as tq
+
+    B, QH, KVH, HD = (ATT_SHAPE[k] for k in ("B", "QH", "KVH", "HD"))
+    lens = attention_lens()
+    rng = np.random.default_rng(5)
+    rng.integers(1024, 32769, B)
+    nbs = (lens + 15) // 16
+    P = int(nbs.sum())
+    perm = rng.permutation(P)
+    tables, at = [], 0
+    for nb in nbs:
+        tables.append(perm[at:at + nb].tolist())
+        at += nb
+    be = HipBackend(0)
+    lists = [[be.alloc(shape, dt) for _ in range(P)] for shape, dt in
+             (([16, KVH * 64], DType.INT8), ([16, KVH], DType.FP16),
+              ([16, KVH * 64], DType.INT8), ([16, KVH], DType.FP16))]
+    pool = be.page_pool_create(*lists)
+    krot, vrot = tq.rotation_matrix(HD, 42), tq.rotation_matrix(HD, 542)
+    cent = tq.codebook(HD, 4)[0]
+    tkr, tvr, tc = (be.upload(a) for a in (krot, vrot, cent))
+    g = torch.Generator(device=dev)
+    g.manual_seed(6)
+    zeros = torch.zeros((int(lens.max()), KVH, HD), dtype=torch.float16, device=dev)
+    for b in range(B):
+        n = int(lens[b])
+        ts = []
+        for _ in range(2):
+            x = torch.randn((n, KVH, HD), generator=g, device=dev).to(torch.float16)
+            t = be.alloc([n, KVH, HD], DType.FP16)
+            # the backend tensor = x + 0 (a device copy, on torch's stream)
+            assert K._L().fhip_launch_add_ex(be.get_ptr(t.id), x.data_ptr(), zeros.data_ptr(),
+                                             x.numel(), 0, K._stream()) == 0
+            torch.cuda.synchronize()
+            ts.append(t)
+        be.tq_append_kv(pool, ts[0], ts[1], tkr, tvr, tc, tc, 4, 4, tables[b], 0)
+        for t in ts:
+            be.free(t)
+    q = be.upload(rng.standard_normal((B, QH, HD)).astype(np.float16))
+    out = be.alloc([B, QH, HD], DType.FP16)
+    table = np.full((B, int(nbs.max())), -1, np.int32)
+    for b, row in enumerate(tables):
+        table[b, :len(row)] = row
+    lens_u = lens.astype(np.uint32)
+    fn = lambda: be.attention_paged_tq_batched(q, table, lens_u, pool, tkr, tvr, tc, tc, 4, 4,
+                                               KVH, out)
+    tok = int(lens.sum())
+    nb = tok * KVH * (64 + 64 + 4) + B * QH * HD * 4 + B * int(nbs.max()) * 4
+
+    def cleanup():
+        be.synchronize()
+        be.page_pool_destroy(pool)
+        be.close()  # frees every tensor at once
+
+    return fn, nb, cleanup, be
+
+
+def kernel_entry(us, nb, **extra):
+    e = {"us": round(us, 2), "GB/s": round(gbs(nb, us), 1),
+         "frac_of_peak": round(gbs(nb, us) / PEAK_HBM_GBS, 4), "bytes": nb}
+    e.update(extra)
+    return e
+
+
+def run_configs(args, torch, K, dev):
+    """Compact results of the other configurations for the default JSON line."""
+    out = {}
+    pre = run_prefill(args, torch, K, dev)["kernels"]
+    out["c3_prefill_reductions"] = {k: {f: v[f] for f in ("us", "GB/s", "frac_of_peak")}
+                                    for k, v in pre.items()}
+    tqr = run_tq(args, torch, K, dev)["kernels"]
+    out["c4_turboquant_kv_32768x8x128"] = {
+        k: {f: v[f] for f in ("us", "GB/s", "frac_of_peak", "rotation_TFLOP/s")}
+        for k, v in tqr.items()}
+    att = run_attention(args, torch, K, dev)["kernels"]["attention_tq_decode"]
+    c5 = {"contiguous_pools": {f: att[f] for f in ("us", "GB/s", "frac_of_peak")}}
+    fn, nb, cleanup, be = runtime_attention_inputs(torch, K, dev)
+    for _ in range(2):
+        fn()
+    be.synchronize()
+    reps = 10
+    t0 = time.perf_counter()
+    tm = be.create_timer()
+    be.start_timer(tm)
+    for _ in range(reps):
+        fn()
+    gpu_us = be.stop_timer(tm) * 1e3 / reps  # HIP events on the backend's stream
+    be.synchronize()
+    us = (time.perf_counter() - t0) * 1e6 / reps
+    be.destroy_timer(tm)
+    c5["handle_runtime_per_block_tensors"] = dict(
+        kernel_entry(gpu_us, nb), host_us_per_call=round(us, 1),
+        note="fhip_attention_paged_tq_batched over a registered pool of per-block tensors "
+             "filled by fhip_tq_append_kv: HIP events on the backend stream; host_us_per_call "
+             "is the wall time per call (block-table staging and checks included)")
+    cleanup()
+    out["c5_tq_decode_attention_B64_K4V4"] = c5
+    return out
+
+
+def cpu_config_baselines(seconds: float):
+    """The oracle on this host for the other configurations: one thread and all cores, each on
+    a bounded sample of the workload, scaled to the full workload's size."""
+    import numpy as np
+
+    import oracle
+    from fracture_amd import turboquant as tq
+
+    th = cpu_threads()
+    rng = np.random.default_rng(0)
+    out = {}
+
+    def both(fn1, fnN, scale, nbytes, sample):
+        t1, _ = median_time(fn1, 3, seconds)
+        tN, _ = median_time(fnN, 3, seconds)
+        return {"us_1core": round(t1 * scale * 1e6, 1), "us_all_cores": round(tN * scale * 1e6, 1),
+                "GB/s_1core": round(gbs(nbytes, t1 * scale * 1e6), 3),
+                "GB/s_all_cores": round(gbs(nbytes, tN * scale * 1e6), 3), "sample": sample}
+
+    R = 512
+    h = rng.standard_normal((R, 4096)).astype(np.float16)
+    d = rng.standard_normal((R, 4096)).astype(np.float16)
+    w = rng.uniform(0.5, 1.5, 4096).astype(np.float16)
+    gt = rng.standard_normal((R, 14336)).astype(np.float16)
+    up = rng.standard_normal((R, 14336)).astype(np.float16)
+    lg = (rng.standard_normal((64, 128256)) * 3).astype(np.float32)
+    lg[np.arange(64), rng.integers(0, 128256, 64)] += 20
+    c3 = {}
+    c3["add_rmsnorm_8192x4096"] = both(
+        lambda: oracle.add_rmsnorm(h, d, w, 1e-5),
+        lambda: par_rows(lambda a, b: oracle.add_rmsnorm(a, b, w, 1e-5), [h, d], R, th),
+        8192 / R, 4 * 8192 * 4096 * 2, f"{R} of 8192 rows")
+    c3["silu_mul_8192x14336"] = both(
+        lambda: oracle.silu_mul(gt, up), lambda: par_rows(oracle.silu_mul, [gt, up], R, th),
+        8192 / R, 3 * 8192 * 14336 * 2, f"{R} of 8192 rows")
+    c3["softmax_64x128256"] = both(
+        lambda: oracle.softmax_rows(lg), lambda: par_rows(oracle.softmax_rows, [lg], 64, th),
+        1.0, 2 * 64 * 128256 * 4, "all 64 rows")
+    c3["argmax_64x128256"] = both(
+        lambda: oracle.argmax_rows(lg), lambda: par_rows(oracle.argmax_rows, [lg], 64, th),
+        1.0, 64 * 128256 * 4, "all 64 rows")
+    out["c3_prefill_reductions"] = c3
+
+    N, H, hd = 512, 8, 128
+    x = (rng.standard_normal((N, H, hd)) * np.exp(rng.normal(0, 0.5, (N, 1, 1)))).astype(np.float16)
+    rot = tq.rotation_matrix(hd, 42)
+    c4 = {}
+    for bits in (4, 3):
+        cent = tq.codebook(hd, bits)[0]
+        pd = (hd * bits + 7) // 8
+        pk, nm, _ = oracle.tq_compress(x, rot, cent, bits)
+        nb = 2 * (32768 * H * hd * 2 + 32768 * H * pd + 32768 * H * 2)
+        scale = 2 * 32768 / N  # K and V of 32768 tokens
+        c4[f"tq_compress_kv_{bits}bit"] = both(
+            lambda: oracle.tq_compress(x, rot, cent, bits),
+            lambda: par_rows(lambda a: oracle.tq_compress(a, rot, cent, bits), [x], N, th),
+            scale, nb, f"{N} tokens x 8 heads, scaled to K and V of 32768 tokens")
+        nmf = nm.reshape(N, H)
+        pkr = pk.reshape(N, H * pd)
+        c4[f"tq_dequant_kv_{bits}bit"] = both(
+            lambda: oracle.tq_dequant(pkr, nmf, rot, cent, bits, hd),
+            lambda: par_rows(lambda a, b: oracle.tq_dequant(a, b, rot, cent, bits, hd),
+                             [pkr, nmf], N, th),
+            scale, nb, f"{N} tokens x 8 heads, scaled to K and V of 32768 tokens")
+    out["c4_turboquant_kv_32768x8x128"] = c4
+
+    # decode attention: 2 sequences x one query head per kv head, per (position, head) time
+    # scaled to the workload's total context x 32 heads
+    lens_s = [16384, 8192]
+    nbs = [n // 16 for n in lens_s]
+    P = sum(nbs)
+    kp = rng.integers(0, 256, (P, 16, 8 * 64)).astype(np.uint8)
+    vp = rng.integers(0, 256, (P, 16, 8 * 64)).astype(np.uint8)
+    kn = rng.uniform(6, 16, (P, 16, 8)).astype(np.float16)
+    vn = rng.uniform(6, 16, (P, 16, 8)).astype(np.float16)
+    perm = rng.permutation(P).astype(np.int32)
+    tabs = [perm[:nbs[0]], perm[nbs[0]:]]
+    q = rng.standard_normal((32, 128)).astype(np.float16)
+    krot, vrot = tq.rotation_matrix(128, 42), tq.rotation_matrix(128, 542)
+    cent = tq.codebook(128, 4)[0]
+    jobs = [(i, 4 * g_) for i in range(2) for g_ in range(8)]
+
+    def one(job):
+        i, h0 = job
+        oracle.tq_attention(q, tabs[i], lens_s[i], kp, kn, vp, vn, krot, vrot, cent, cent, 4, 4,
+                            8, heads=(h0, h0 + 1))
+
+    def serial():
+        for j in jobs:
+            one(j)
+
+    def parallel():
+        from concurrent.futures import ThreadPoolExecutor
+
+        with ThreadPoolExecutor(th) as ex:
+            list(ex.map(one, jobs))
+
+    lens = attention_lens()
+    work = float(lens.sum()) * 32
+    done = float(sum(lens_s)) * 8
+    nb = int(lens.sum()) * 8 * (64 + 64 + 4) + 64 * 32 * 128 * 4 + 64 * int(((lens + 15) // 16).max()) * 4
+    out["c5_tq_decode_attention_B64_K4V4"] = both(
+        serial, parallel, work / done, nb,
+        "2 sequences (16384 and 8192 positions) x 8 query heads, scaled to the workload's "
+        "total context x 32 heads")
+    return out
+
+
 def run_pmc(torch, K, dev):
     seq = pmc_sequence(torch, K, dev)
     assert [(k, nb) for k, _, nb in seq] == pmc_keys(), "pmc_keys() out of step"
@@ -706,7 +1042,14 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
     wl = args.workload
-    if wl in ("decode", "all"):
+    if wl == "decode":
+        res = run_decode(args, torch, K, dev)
+        if not args.no_configs:
+            res["configs"] = run_configs(args, torch, K, dev)
+            if not args.no_cpu_baseline:
+                res["cpu_baseline"]["configs"] = cpu_config_baselines(args.cpu_seconds / 40)
+        print(json.dumps(res), flush=True)
+    if wl == "all":
         print(json.dumps(run_decode(args, torch, K, dev)), flush=True)
     if wl in ("prefill", "all"):
         print(json.dumps(run_prefill(args, torch, K, dev)), flush=True)

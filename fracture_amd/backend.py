@@ -380,12 +380,17 @@ class HipBackend:
                                    v_centroids: DeviceTensor, key_bits: int, value_bits: int,
                                    num_kv_heads: int, out: DeviceTensor) -> None:
         """Decode attention of q [B, qh, hd] (one query per sequence) over a registered
-        TurboQuant pool in one call; block_tables are padded to a common width."""
+        TurboQuant pool in one call. block_tables: an int32 array [B, max_blocks], or rows of
+        block ids (padded here to a common width)."""
         lens = np.ascontiguousarray(np.asarray(seq_lens, dtype=np.uint32))
-        width = max([len(r) for r in block_tables] + [1])
-        bt = np.full((len(block_tables), width), -1, np.int32)
-        for i, row in enumerate(block_tables):
-            bt[i, :len(row)] = row
+        if isinstance(block_tables, np.ndarray) and block_tables.ndim == 2:
+            bt = np.ascontiguousarray(block_tables, dtype=np.int32)
+        else:
+            width = max([len(r) for r in block_tables] + [1])
+            bt = np.full((len(block_tables), width), -1, np.int32)
+            for i, row in enumerate(block_tables):
+                bt[i, :len(row)] = row
+        width = bt.shape[1]
         _check(self._L.fhip_attention_paged_tq_batched(
             self._h, C.byref(q._c()), bt.ctypes.data, width, lens.ctypes.data, pool,
             C.byref(k_rotation._c()), C.byref(v_rotation._c()), C.byref(k_centroids._c()),

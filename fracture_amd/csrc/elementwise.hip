@@ -325,6 +325,44 @@ __global__ __launch_bounds__(256) void rope_kernel(void* __restrict__ q, void* _
     }
 }
 
+// RoPE at head_dim 128 for 16-bit types: one wave per (token, group of 8 heads), so a
+// decode batch of 64 tokens x 40 heads spreads over 320 workgroups instead of 64. Lane l
+// rotates the 8 pairs (8c + e, 64 + 8c + e), c = l % 8, of head 8 group + l / 8, and computes
+// the angle of dim l itself (one accurate sincosf per lane, the same call as rope_kernel);
+// the 8 angles a lane needs come from lanes 8c .. 8c + 7 by shuffles: no LDS, no barrier.
+template <class Tr>
+__global__ __launch_bounds__(64) void rope_wave_kernel(void* __restrict__ q, void* __restrict__ k,
+                                                      const uint32_t* __restrict__ positions,
+                                                      const float* __restrict__ freq, int qh,
+                                                      int kvh) {
+    constexpr int kHalf = 64;
+    using S = typename Tr::S;
+    const int t = blockIdx.x, lane = threadIdx.x;
+    const int head = blockIdx.y * 8 + (lane >> 3), ch = lane & 7;
+    const bool ok = head < qh + kvh;
+    const int hh = ok ? head : 0;  // lanes past the last head reload head 0 and store nothing
+    S* row = hh < qh ? (S*)q + ((int64_t)t * qh + hh) * (2 * kHalf)
+                     : (S*)k + ((int64_t)t * kvh + (hh - qh)) * (2 * kHalf);
+    S* p0 = row + ch * 8;
+    const u32x4 r0 = ld16(p0), r1 = ld16(p0 + kHalf);
+    float sn, cs;
+    sincosf((float)positions[t] * freq[lane], &sn, &cs);
+    float x0[8], x1[8];
+    unpack16<Tr>(r0, x0);
+    unpack16<Tr>(r1, x1);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float c = __shfl(cs, 8 * ch + e), s = __shfl(sn, 8 * ch + e);
+        const float a = x0[e], b = x1[e];
+        x0[e] = a * c - b * s;
+        x1[e] = a * s + b * c;
+    }
+    if (ok) {
+        st16(p0, pack16<Tr>(x0));
+        st16(p0 + kHalf, pack16<Tr>(x1));
+    }
+}
+
 // ---------------------------------------------------------------------------------------
 // Embedding gather (embedding.cu:7-28): out[t,:] = table[id,:], zeros when id >= vocab.
 // Grid (row chunks, tokens); each lane copies 16 bytes.
@@ -409,10 +447,13 @@ int launch_rms_t(void* out, void* resid, const void* in, const void* w, float ep
                         (!kResid || fhip_host::aligned16(resid));
     const int nvec = cols / V;
     if (vec_ok && nvec > 0 && nvec <= 1024 * 8) {
-        // Smallest vectors-per-lane (1, 2, 4, 8) that fits in a <=1024-lane workgroup of
-        // at most 256 lanes when possible; the block is a multiple of the wave.
+        // Smallest vectors-per-lane (1, 2, 4, 8) that fits in a <=1024-lane workgroup of at
+        // most 256 lanes when possible (512 when there are too few rows to fill the chip:
+        // a decode batch of 64 rows then has fewer loads in flight per lane); the block is a
+        // multiple of the wave.
+        const int64_t lanes = rows < 512 ? 512 : 256;
         int vpt = 1;
-        while (vpt < 8 && (int64_t)vpt * 256 < nvec) vpt *= 2;
+        while (vpt < 8 && (int64_t)vpt * lanes < nvec) vpt *= 2;
         int bs = (int)ceil_div(ceil_div(nvec, vpt), kWave) * kWave;
         if (bs > 1024) return hipErrorInvalidValue;
         switch (vpt) {
@@ -438,7 +479,10 @@ int launch_rope_t(void* q, void* k, const uint32_t* pos, const float* freq, int 
                         (kvh == 0 || fhip_host::aligned16(k));
     const int work = (qh + kvh) * (vec_ok ? half / Tr::kVec : half);
     int bs = (int)std::min<int64_t>(256, std::max<int64_t>(kWave, ceil_div(work, kWave) * kWave));
-    if (vec_ok)
+    if (vec_ok && Tr::kVec == 8 && hd == 128 && ceil_div(qh + kvh, 8) <= 65535) {
+        const dim3 grid((unsigned)T, (unsigned)ceil_div(qh + kvh, 8));
+        hipLaunchKernelGGL((rope_wave_kernel<Tr>), grid, dim3(64), 0, s, q, k, pos, freq, qh, kvh);
+    } else if (vec_ok)
         hipLaunchKernelGGL((rope_kernel<Tr, true>), dim3(T), dim3(bs), lds, s, q, k, pos, freq, qh,
                            kvh, hd);
     else
