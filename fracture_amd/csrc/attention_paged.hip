@@ -114,8 +114,12 @@ paged_attn_split_kernel(const uint16_t* __restrict__ q, PQueries qs, Pages pg, i
     constexpr int kPpl = 64 / kDg;               // positions per V load
     constexpr int kVLoads = kChunk / kPpl;
     static_assert(kPpl <= 16 && 16 % kPpl == 0, "a V load stays inside one page");
-    __shared__ __attribute__((aligned(16))) float pbuf[kPWaves][kChunk][kHeadsMax];
-    __shared__ __attribute__((aligned(16))) float abuf[kPWaves][kHeadsMax];
+    // Every lane writes its own slot of these buffers (columns / entries past the wave's
+    // heads are written and never read): a store guarded by the lane index followed by reads
+    // of every lane lets the compiler sink the reads into the guarded block, where they run
+    // with the other lanes switched off (seen in a variant of this loop at head_dim 32).
+    __shared__ __attribute__((aligned(16))) float pbuf[kPWaves][kChunk][16];
+    __shared__ __attribute__((aligned(16))) float abuf[kPWaves][64];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -235,13 +239,13 @@ paged_attn_split_kernel(const uint16_t* __restrict__ q, PQueries qs, Pages pg, i
             for (int e = 0; e < 4; ++e) {
                 const float p = __builtin_amdgcn_exp2f(sc[tt][e] - mref);
                 psum += p;
-                if (n < kHeadsMax) pbuf[wave][16 * tt + 4 * kg + e][n] = p;
+                pbuf[wave][16 * tt + 4 * kg + e][n] = p;
             }
         psum += __shfl_xor(psum, 16);
         psum += __shfl_xor(psum, 32);
         l_run = l_run * alpha + psum;
         m_run = m_new;
-        if (lane < kHeadsMax) abuf[wave][lane] = alpha;
+        abuf[wave][lane] = alpha;
 
         // ---- PV (this wave's LDS writes above complete before its reads below: one wave's
         // LDS instructions execute in order)

@@ -251,6 +251,10 @@ def test_page_writer_equals_flat_compress(dev, first_pos):
                         dev_t(page_ids, dev), first_pos)
     torch.cuda.synchronize()
     flat_p, flat_n = compress(x, rot, cent, bits, dev)
+    # the oracle's quantize-pack of the kernel's own rotated vectors pins the page bytes
+    y, yn = rotate(x, rot, dev)
+    want_p = oracle.tq_quantize_pack(y, cent, bits).reshape(T, H * pd)
+    want_n = yn.reshape(T, H)
     KP, KN = kp.cpu().numpy(), kn.cpu().numpy()
     written = np.zeros((npages, 16), bool)
     for t in range(T):
@@ -259,6 +263,8 @@ def test_page_writer_equals_flat_compress(dev, first_pos):
         if page >= npages:
             continue
         written[page, slot] = True
+        assert np.array_equal(KP[page, slot], want_p[t]), f"token {t} codes"
+        assert np.array_equal(KN[page, slot].view(np.uint16), want_n[t].view(np.uint16))
         assert np.array_equal(KP[page, slot], flat_p[t])
         assert np.array_equal(KN[page, slot].view(np.uint16), flat_n[t].view(np.uint16))
     assert (KP[~written] == 0xAB).all() and (KN[~written] == 7.0).all()
@@ -290,7 +296,13 @@ def test_planned_compress_equals_unplanned(dev, bits, kind):
     norms = torch.empty((301, 8), dtype=torch.float16, device=dev)
     K.tq_compress_planned(plan, dev_t(x, dev), packed, norms)
     torch.cuda.synchronize()
-    assert np.array_equal(packed.cpu().numpy(), want_p)
+    # pinned by the oracle's quantize-pack (first-minimum scan over any codebook) of the
+    # kernel's own rotated vectors, and equal to the unplanned launcher
+    y, yn = rotate(x, rot, dev)
+    got = packed.cpu().numpy()
+    assert np.array_equal(got.reshape(301 * 8, -1), oracle.tq_quantize_pack(y, cent, bits))
+    assert np.array_equal(norms.cpu().numpy().reshape(-1).view(np.uint16), yn.view(np.uint16))
+    assert np.array_equal(got, want_p)
     assert np.array_equal(norms.cpu().numpy().view(np.uint16), want_n.view(np.uint16))
 
 
@@ -309,6 +321,9 @@ def test_planned_dequant_equals_unplanned(dev, bits):
     K.tq_dequant_planned(plan, tp, tn, got)
     torch.cuda.synchronize()
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    ref = oracle.tq_dequant(packed.reshape(200 * 8, -1), norms.reshape(-1), rot, cent, bits, 128)
+    assert_close(got.cpu().numpy().reshape(-1, 128).astype(np.float32), ref.astype(np.float32),
+                 1e-3, 1e-3, "planned dequantize vs oracle")
 
 
 def test_plan_outlives_its_sources(dev):
@@ -330,6 +345,9 @@ def test_plan_outlives_its_sources(dev):
         norms = torch.empty((n, 8), dtype=torch.float16, device=dev)
         K.tq_compress_planned(plan, dev_t(x, dev), packed, norms)
         torch.cuda.synchronize()
+        y, _ = rotate(x, rot, dev)
+        assert np.array_equal(packed.cpu().numpy().reshape(n * 8, -1),
+                              oracle.tq_quantize_pack(y, cent, bits))
         assert np.array_equal(packed.cpu().numpy(), want_p)
         assert np.array_equal(norms.cpu().numpy().view(np.uint16), want_n.view(np.uint16))
 
@@ -355,3 +373,11 @@ def test_planned_page_writer_equals_unplanned(dev):
         torch.cuda.synchronize()
         pools.append((kp.cpu().numpy(), kn.cpu().numpy().view(np.uint16)))
     assert np.array_equal(pools[0][0], pools[1][0]) and np.array_equal(pools[0][1], pools[1][1])
+    # and the planned pages hold the oracle's quantize-pack of the kernel's rotated vectors
+    y, yn = rotate(x, rot, dev)
+    want_p = oracle.tq_quantize_pack(y, cent, bits).reshape(T, H * pd)
+    for t in range(T):
+        pos = first_pos + t
+        page, slot = page_ids[pos // 16], pos % 16
+        assert np.array_equal(pools[1][0][page, slot], want_p[t]), f"token {t}"
+        assert np.array_equal(pools[1][1][page, slot], yn.reshape(T, H)[t].view(np.uint16))
