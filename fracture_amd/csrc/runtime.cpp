@@ -1139,8 +1139,15 @@ int fhip_page_pool_destroy(fhip_backend* b, uint64_t pool) {
 
 // The pool with `nlists` lists whose list l holds blocks of at least need[l] bytes of dtype
 // dt[l] (dt -1: any), or an error.
+// What a launch over a pool needs: the device address table and the pool length (copying the
+// whole PagePool would copy its id list, nlists * pool_len entries, on every call).
+struct PoolView {
+    const void** dev = nullptr;
+    size_t pool_len = 0;
+};
+
 static int find_pool(fhip_backend* b, uint64_t pool, int nlists, const uint64_t* need,
-                     const int32_t* dt, fhip_backend::PagePool* out) {
+                     const int32_t* dt, PoolView* out) {
     std::lock_guard<std::mutex> g(b->mu);
     auto it = b->pools.find(pool);
     if (it == b->pools.end())
@@ -1158,7 +1165,8 @@ static int find_pool(fhip_backend* b, uint64_t pool, int nlists, const uint64_t*
             return fail(FHIP_ERR_INVALID_SHAPE, "page pool list %d: dtype %s", l,
                         dtype_name(pp.dtype[l] >= 0 ? pp.dtype[l] : -1));
     }
-    *out = pp;
+    out->dev = pp.dev;
+    out->pool_len = pp.pool_len;
     return FHIP_OK;
 }
 
@@ -1189,7 +1197,7 @@ int fhip_attention_paged_pool(fhip_backend* b, const fhip_tensor* q, const int32
     const uint64_t need = FHIP_PAGE_TOKENS * num_kv_heads * hd * 2;
     const uint64_t needs[2] = {need, need};
     const int32_t dts[2] = {FHIP_FP16, FHIP_FP16};
-    fhip_backend::PagePool pp;
+    PoolView pp;
     int r = find_pool(b, pool, 2, needs, dts, &pp);
     if (r) return r;
     for (uint64_t i = 0; i < needed_blocks; ++i)
@@ -1262,7 +1270,7 @@ int fhip_attention_paged_tq_pool(fhip_backend* b, const fhip_tensor* q,
                                FHIP_PAGE_TOKENS * num_kv_heads * vpd,
                                FHIP_PAGE_TOKENS * num_kv_heads * 2};
     const int32_t dts[4] = {-1, -1, -1, -1};
-    fhip_backend::PagePool pp;
+    PoolView pp;
     int r = find_pool(b, pool, 4, needs, dts, &pp);
     if (r) return r;
     for (uint64_t i = 0; i < needed_blocks; ++i)
@@ -1344,7 +1352,7 @@ int fhip_tq_append_kv(fhip_backend* b, uint64_t pool, const fhip_tensor* keys,
     const uint64_t needs[4] = {FHIP_PAGE_TOKENS * kvh * kpd, FHIP_PAGE_TOKENS * kvh * 2,
                                FHIP_PAGE_TOKENS * kvh * vpd, FHIP_PAGE_TOKENS * kvh * 2};
     const int32_t dts[4] = {-1, FHIP_FP16, -1, FHIP_FP16};
-    fhip_backend::PagePool pp;
+    PoolView pp;
     int r = find_pool(b, pool, 4, needs, dts, &pp);
     if (r) return r;
     for (uint64_t i = start_pos / FHIP_PAGE_TOKENS; i <= last_block; ++i)
@@ -1435,7 +1443,7 @@ int fhip_attention_paged_tq_batched(fhip_backend* b, const fhip_tensor* q,
                                FHIP_PAGE_TOKENS * num_kv_heads * vpd,
                                FHIP_PAGE_TOKENS * num_kv_heads * 2};
     const int32_t dts[4] = {-1, -1, -1, -1};
-    fhip_backend::PagePool pp;
+    PoolView pp;
     int r = find_pool(b, pool, 4, needs, dts, &pp);
     if (r) return r;
     for (uint64_t i = 0; i < B; ++i) {
