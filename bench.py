@@ -233,6 +233,56 @@ def decode_ops(K, x):
     }
 
 
+def runtime_decode_graph(steps_per_graph: int, replays: int) -> float:
+    """µs per step of the decode chain captured through the handle runtime's graph API
+    (per_graph consecutive steps per graph, as the raw-launcher timing), with its own tensors
+    of the chain's shapes."""
+    import numpy as np
+
+    from fracture_amd import DType, HipBackend
+
+    B, V, H, QH, KVH, HD, FF = 64, 128256, 4096, 32, 8, 128, 14336
+    rng = np.random.default_rng(1)
+    with HipBackend(0) as be:
+        be.precompute_rope_freqs(HD, 500000.0)
+        f16 = DType.FP16
+        # finite fp16 values in [0, 2): bit patterns below 0x4000
+        table = be.upload(rng.integers(0, 0x4000, (V, H), dtype=np.uint16).view(np.float16))
+        ids = be.alloc([B], DType.FP32)
+        be.copy_to_device(ids, rng.integers(0, V, B).astype(np.uint32))
+        pos = be.alloc([B], DType.FP32)
+        be.copy_to_device(pos, rng.integers(0, 8192, B).astype(np.uint32))
+        t = {n: be.upload(rng.standard_normal(shape).astype(np.float16)) for n, shape in
+             (("q", (B, QH, HD)), ("k", (B, KVH, HD)), ("gate", (B, FF)), ("up", (B, FF)),
+              ("h", (B, H)), ("d1", (B, H)), ("d2", (B, H)))}
+        w1 = be.upload(rng.uniform(0.5, 1.5, H).astype(np.float16))
+        w2 = be.upload(rng.uniform(0.5, 1.5, H).astype(np.float16))
+        emb, act = be.alloc([B, H], f16), be.alloc([B, FF], f16)
+        n1, n2 = be.alloc([B, H], f16), be.alloc([B, H], f16)
+
+        def steps():
+            for _ in range(steps_per_graph):
+                be.embedding_dev(ids, B, table, emb)
+                be.rope_dev(t["q"], t["k"], pos, B, HD)
+                be.silu_mul(t["gate"], t["up"], act)
+                be.add_rmsnorm(t["h"], t["d1"], w1, 1e-5, n1)
+                be.add_rmsnorm(t["h"], t["d2"], w2, 1e-5, n2)
+
+        g = be.capture(steps)
+        for _ in range(2):
+            be.graph_launch(g)
+        be.synchronize()
+        tm = be.create_timer()
+        be.start_timer(tm)
+        for _ in range(replays):
+            be.graph_launch(g)
+        ms = be.stop_timer(tm)
+        be.synchronize()
+        be.destroy_timer(tm)
+        be.graph_destroy(g)
+    return ms * 1e3 / (replays * steps_per_graph)
+
+
 def decode_step(ops):
     for f in ops.values():
         f()
@@ -416,6 +466,15 @@ def run_decode(args, torch, K, dev):
         "kernels": per,
         "roofline": roof,
     }
+    if not args.eager:
+        rt_us = runtime_decode_graph(per_graph, max(1, args.steps // per_graph))
+        result["handle_runtime_graph"] = {
+            "us_per_step": round(rt_us, 3), "GB/s": round(gbs(chain_bytes, rt_us), 1),
+            "steps_per_graph": per_graph,
+            "note": "the same chain through the handle runtime: fhip_embedding_dev, "
+                    "fhip_rope_dev, fhip_silu_mul, 2x fhip_add_rmsnorm captured with "
+                    "fhip_graph_begin / fhip_graph_end, replayed with fhip_graph_launch; "
+                    "HIP events on the backend stream"}
     if not args.no_cpu_baseline:
         cpu_us, n = cpu_decode_baseline(args.cpu_seconds / 2)
         th = cpu_threads()

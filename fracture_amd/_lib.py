@@ -46,6 +46,7 @@ SIGNATURES = {
     "fhip_launch_attention_paged_tq": (I, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I,
                                            I, I, I, I, P]),
     "fhip_launch_paged_attention": (I, [P, P, P, P, P, I, I, I, I, I, I, I, P]),
+    "fhip_launch_attention": (I, [P, P, P, P, I, I, I, I, I, I, P]),
     "fhip_launch_matmul": (I, [P, P, P, I, I, I, P]),
     # additive raw launchers
     "fhip_launch_attention_paged_tq_ws": (I, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I,
@@ -99,6 +100,7 @@ SIGNATURES = {
     "fhip_embedding": (I, [P, P, SZ, TP, TP]),
     "fhip_add": (I, [P, TP, TP, TP]),
     "fhip_copy_rows": (I, [P, TP, TP, SZ, SZ, SZ]),
+    "fhip_attention": (I, [P, TP, TP, TP, SZ, SZ, TP]),
     "fhip_device_name": (C.c_char_p, [P]),
     "fhip_total_memory": (SZ, [P]),
     "fhip_available_memory": (SZ, [P]),
@@ -123,6 +125,12 @@ SIGNATURES = {
     "fhip_attention_paged_tq_batched": (I, [P, TP, P, SZ, P, U64, TP, TP, TP, TP, C.c_uint8,
                                             C.c_uint8, SZ, TP]),
     "fhip_add_rmsnorm": (I, [P, TP, TP, TP, D, TP]),
+    "fhip_rope_dev": (I, [P, TP, TP, TP, SZ, SZ]),
+    "fhip_embedding_dev": (I, [P, TP, SZ, TP, TP]),
+    "fhip_graph_begin": (I, [P]),
+    "fhip_graph_end": (I, [P, C.POINTER(U64)]),
+    "fhip_graph_launch": (I, [P, U64]),
+    "fhip_graph_destroy": (I, [P, U64]),
     "fhip_softmax_rows": (I, [P, TP, F, TP]),
     "fhip_argmax_rows": (I, [P, TP, P, SZ]),
     "fhip_tq_dequantize": (I, [P, TP, TP, TP, TP, C.c_uint8, TP]),

@@ -219,8 +219,12 @@ class HipBackend:
         _check(self._L.fhip_rope(self._h, C.byref(q._c()), C.byref(k._c()), pos.ctypes.data,
                                  pos.size, theta, head_dim))
 
-    def attention(self, *args, **kwargs) -> None:
-        raise BackendError("attention not supported by this backend")
+    def attention(self, q: DeviceTensor, k_cache: DeviceTensor, v_cache: DeviceTensor,
+                  num_kv_heads: int, start_pos: int, out: DeviceTensor) -> None:
+        """Backend::attention over contiguous caches: not supported (the caches are paged)."""
+        _check(self._L.fhip_attention(self._h, C.byref(q._c()), C.byref(k_cache._c()),
+                                      C.byref(v_cache._c()), num_kv_heads, start_pos,
+                                      C.byref(out._c())))
 
     def silu_mul(self, gate: DeviceTensor, up: DeviceTensor, out: DeviceTensor) -> None:
         _check(self._L.fhip_silu_mul(self._h, C.byref(gate._c()), C.byref(up._c()),
@@ -231,6 +235,18 @@ class HipBackend:
         ids = np.ascontiguousarray(np.asarray(token_ids, dtype=np.uint32))
         _check(self._L.fhip_embedding(self._h, ids.ctypes.data, ids.size,
                                       C.byref(embedding_table._c()), C.byref(out._c())))
+
+    def rope_dev(self, q: DeviceTensor, k: DeviceTensor, positions: DeviceTensor,
+                 num_positions: int, head_dim: int) -> None:
+        """rope with the positions read as uint32 from a device tensor (capturable)."""
+        _check(self._L.fhip_rope_dev(self._h, C.byref(q._c()), C.byref(k._c()),
+                                     C.byref(positions._c()), num_positions, head_dim))
+
+    def embedding_dev(self, token_ids: DeviceTensor, num_tokens: int,
+                      embedding_table: DeviceTensor, out: DeviceTensor) -> None:
+        """embedding with the token ids read as uint32 from a device tensor (capturable)."""
+        _check(self._L.fhip_embedding_dev(self._h, C.byref(token_ids._c()), num_tokens,
+                                          C.byref(embedding_table._c()), C.byref(out._c())))
 
     def add(self, a: DeviceTensor, b: DeviceTensor, out: DeviceTensor) -> None:
         _check(self._L.fhip_add(self._h, C.byref(a._c()), C.byref(b._c()), C.byref(out._c())))
@@ -252,6 +268,37 @@ class HipBackend:
 
     def synchronize(self) -> None:
         _check(self._L.fhip_synchronize(self._h))
+
+    # -- graph capture ------------------------------------------------------------------------
+    def graph_begin(self) -> None:
+        """Record this thread's following ops into a graph instead of running them."""
+        _check(self._L.fhip_graph_begin(self._h))
+
+    def graph_end(self) -> int:
+        """End the capture; returns the id of the instantiated graph."""
+        g = C.c_uint64()
+        _check(self._L.fhip_graph_end(self._h, C.byref(g)))
+        return g.value
+
+    def graph_launch(self, graph: int) -> None:
+        _check(self._L.fhip_graph_launch(self._h, graph))
+
+    def graph_destroy(self, graph: int) -> None:
+        _check(self._L.fhip_graph_destroy(self._h, graph))
+
+    def capture(self, record) -> int:
+        """Capture the ops `record()` issues into a graph and return its id; a failure inside
+        ends the capture before it propagates."""
+        self.graph_begin()
+        try:
+            record()
+        except BaseException:
+            try:
+                self.graph_destroy(self.graph_end())
+            except FractureError:
+                pass
+            raise
+        return self.graph_end()
 
     # -- profiling ----------------------------------------------------------------------------
     def create_timer(self) -> DeviceTimer:

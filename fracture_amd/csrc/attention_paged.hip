@@ -519,4 +519,16 @@ int fhip_launch_paged_attention_ws(void* output, const void* q, const int* block
                                fhip_host::as_stream(stream));
 }
 
+// ffi.rs:172-184 `launch_attention`, attention over a contiguous KV cache: not supported. The
+// engine's KV caches are paged (engine.rs:671-680 dispatches through the cache manager to the
+// paged forms above), so this backend builds only those; the symbol exists so that a binding of
+// the whole ffi.rs block links, and it launches nothing.
+int fhip_launch_attention(void* output, const void* q, const void* k_cache, const void* v_cache,
+                          int num_tokens, int num_q_heads, int num_kv_heads, int head_dim,
+                          int kv_len, int start_pos, fhip_stream_t stream) {
+    (void)output, (void)q, (void)k_cache, (void)v_cache, (void)num_tokens, (void)num_q_heads;
+    (void)num_kv_heads, (void)head_dim, (void)kv_len, (void)start_pos, (void)stream;
+    return hipErrorNotSupported;
+}
+
 }  // extern "C"

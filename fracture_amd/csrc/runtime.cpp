@@ -16,6 +16,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -143,6 +144,12 @@ struct fhip_backend {
     uint64_t next_timer = 1;
     float* rope_freq = nullptr;
     size_t rope_half = 0;
+    // graph capture (fhip_graph_begin / fhip_graph_end): while set, launches on `stream` are
+    // recorded into a graph instead of running, and only the ops whose arguments are all
+    // device-resident and that never wait on the host are accepted
+    std::atomic<bool> capturing{false};
+    std::unordered_map<uint64_t, hipGraphExec_t> graphs;  // under mu
+    uint64_t next_graph = 1;
     // launch lock: staging ring and workspace are per backend
     std::mutex launch_mu;
     static constexpr int kSlots = 16;
@@ -285,6 +292,10 @@ namespace {
 
 #define CHECK_B(b) \
     if (!(b)) return fail(FHIP_ERR_BACKEND, "null backend handle")
+#define NO_CAPTURE(b, what)                                                                  \
+    if ((b)->capturing)                                                                      \
+    return fail(FHIP_ERR_BACKEND, "%s is not allowed during graph capture (it reads host "  \
+                "memory, waits on the host or allocates)", what)
 #define CHECK_T(t) \
     if (!valid_desc(t)) return fail(FHIP_ERR_INVALID_SHAPE, "invalid tensor descriptor")
 #define GET_PTR(b, t, p)                         \
@@ -327,7 +338,14 @@ int fhip_backend_create(int device_id, fhip_backend** out) {
 void fhip_backend_destroy(fhip_backend* b) {
     if (!b) return;
     (void)hipSetDevice(b->device);
+    if (b->capturing) {
+        hipGraph_t g = nullptr;
+        (void)hipStreamEndCapture(b->stream, &g);
+        if (g) (void)hipGraphDestroy(g);
+        b->capturing = false;
+    }
     (void)hipStreamSynchronize(b->stream);
+    for (auto& kv : b->graphs) (void)hipGraphExecDestroy(kv.second);
     for (auto& kv : b->tensors) (void)hipFree(kv.second);
     for (auto& kv : b->timers) {
         (void)hipEventDestroy(kv.second.first);
@@ -357,6 +375,7 @@ fhip_stream_t fhip_stream(fhip_backend* b) { return b ? (fhip_stream_t)b->stream
 
 int fhip_precompute_rope_freqs(fhip_backend* b, size_t head_dim, double theta) {
     CHECK_B(b);
+    NO_CAPTURE(b, "precompute_rope_freqs");
     if (head_dim < 2 || head_dim % 2 != 0 || head_dim > 4096)
         return fail(FHIP_ERR_INVALID_SHAPE, "rope head_dim must be even and in [2, 4096], got %zu",
                     head_dim);
@@ -383,6 +402,7 @@ int fhip_precompute_rope_freqs(fhip_backend* b, size_t head_dim, double theta) {
 
 int fhip_alloc(fhip_backend* b, const uint64_t* shape, int ndim, int dtype, fhip_tensor* out) {
     CHECK_B(b);
+    NO_CAPTURE(b, "alloc");
     if (!out || ndim < 0 || ndim > FHIP_MAX_DIMS || (ndim > 0 && !shape))
         return fail(FHIP_ERR_INVALID_SHAPE, "invalid shape (ndim %d)", ndim);
     if (dtype_size(dtype) == 0) return fail(FHIP_ERR_UNSUPPORTED_DTYPE, "dtype %d", dtype);
@@ -413,6 +433,7 @@ int fhip_alloc(fhip_backend* b, const uint64_t* shape, int ndim, int dtype, fhip
 
 int fhip_free(fhip_backend* b, const fhip_tensor* t) {
     CHECK_B(b);
+    NO_CAPTURE(b, "free");
     if (!t) return fail(FHIP_ERR_INVALID_SHAPE, "null tensor");
     void* p = nullptr;
     {
@@ -438,6 +459,7 @@ int fhip_free(fhip_backend* b, const fhip_tensor* t) {
 
 int fhip_copy_to_device(fhip_backend* b, const fhip_tensor* dst, const void* src, size_t src_len) {
     CHECK_B(b);
+    NO_CAPTURE(b, "copy_to_device");
     CHECK_T(dst);
     GET_PTR(b, dst, p);
     const uint64_t size = size_bytes(dst);
@@ -454,6 +476,7 @@ int fhip_copy_to_device(fhip_backend* b, const fhip_tensor* dst, const void* src
 
 int fhip_copy_to_host(fhip_backend* b, const fhip_tensor* src, void* dst, size_t dst_len) {
     CHECK_B(b);
+    NO_CAPTURE(b, "copy_to_host");
     CHECK_T(src);
     GET_PTR(b, src, p);
     const uint64_t size = size_bytes(src);
@@ -501,6 +524,7 @@ int fhip_rmsnorm(fhip_backend* b, const fhip_tensor* input, const fhip_tensor* w
 int fhip_matmul(fhip_backend* b, const fhip_tensor* a, const fhip_tensor* bm,
                 const fhip_tensor* out) {
     CHECK_B(b);
+    NO_CAPTURE(b, "matmul");
     CHECK_T(a);
     CHECK_T(bm);
     CHECK_T(out);
@@ -561,10 +585,15 @@ int fhip_add_rmsnorm(fhip_backend* b, const fhip_tensor* residual, const fhip_te
                                                  residual->dtype, b->stream));
 }
 
-int fhip_rope(fhip_backend* b, const fhip_tensor* q, const fhip_tensor* k,
-              const uint32_t* positions, size_t num_positions, double theta, size_t head_dim) {
-    (void)theta;  // the table from precompute_rope_freqs is used (backend.rs:166)
-    CHECK_B(b);
+}  // extern "C"
+
+namespace {
+
+// fhip_rope / fhip_rope_dev: positions from host memory (staged through the pinned ring) or
+// already on the device (dev_pos).
+int rope_common(fhip_backend* b, const fhip_tensor* q, const fhip_tensor* k,
+                const uint32_t* host_pos, const void* dev_pos, size_t num_positions,
+                size_t head_dim) {
     CHECK_T(q);
     CHECK_T(k);
     GET_PTR(b, q, pq);
@@ -585,19 +614,103 @@ int fhip_rope(fhip_backend* b, const fhip_tensor* q, const fhip_tensor* k,
     if (q->dtype != FHIP_FP16 && q->dtype != FHIP_BF16 && q->dtype != FHIP_FP32)
         return fail(FHIP_ERR_UNSUPPORTED_DTYPE, "rope %s", dtype_name(q->dtype));
     if (T == 0) return FHIP_OK;
-    if (!positions) return fail(FHIP_ERR_INVALID_SHAPE, "null positions");
+    if (!host_pos && !dev_pos) return fail(FHIP_ERR_INVALID_SHAPE, "null positions");
     set_device(b);
     std::lock_guard<std::mutex> g(b->launch_mu);
-    void* dpos;
-    int slot;
-    int r = b->stage(positions, T * sizeof(uint32_t), &dpos, &slot);
-    if (r != FHIP_OK) return r;
+    const void* dpos = dev_pos;
+    int slot = -1;
+    if (!dpos) {
+        void* staged;
+        int r = b->stage(host_pos, T * sizeof(uint32_t), &staged, &slot);
+        if (r != FHIP_OK) return r;
+        dpos = staged;
+    }
     int e = fhip_launch_rope_ex(pq, pk, (const uint32_t*)dpos, b->rope_freq, (int)T, (int)qh,
                                 (int)kvh, (int)head_dim, q->dtype, b->stream);
-    r = b->stage_done(slot);
+    int r = slot >= 0 ? b->stage_done(slot) : FHIP_OK;
     if (e != hipSuccess)
         return fail(FHIP_ERR_BACKEND, "RoPE kernel error: %s", hipGetErrorString((hipError_t)e));
     return r;
+}
+
+// fhip_embedding / fhip_embedding_dev: token ids from host memory or already on the device.
+int embedding_common(fhip_backend* b, const uint32_t* host_ids, const void* dev_ids,
+                     size_t num_tokens, const fhip_tensor* table, const fhip_tensor* out) {
+    CHECK_T(table);
+    CHECK_T(out);
+    GET_PTR(b, table, pt);
+    GET_PTR(b, out, po);
+    if (table->ndim != 2 || (dtype_size(table->dtype) != 2 && dtype_size(table->dtype) != 4))
+        return fail(FHIP_ERR_INVALID_SHAPE, "embedding table %s",
+                    shape_str(table).c_str());
+    const uint64_t vocab = table->shape[0], hidden = table->shape[1];
+    if (numel(out) < num_tokens * hidden || out->dtype != table->dtype)
+        return fail(FHIP_ERR_INVALID_SHAPE, "embedding out %s for %zu tokens",
+                    shape_str(out).c_str(), num_tokens);
+    if (num_tokens == 0) return FHIP_OK;
+    if (!host_ids && !dev_ids) return fail(FHIP_ERR_INVALID_SHAPE, "null token ids");
+    set_device(b);
+    std::lock_guard<std::mutex> g(b->launch_mu);
+    const void* dids = dev_ids;
+    int slot = -1;
+    if (!dids) {
+        void* staged;
+        int r = b->stage(host_ids, num_tokens * sizeof(uint32_t), &staged, &slot);
+        if (r != FHIP_OK) return r;
+        dids = staged;
+    }
+    int e = fhip_launch_embedding_ex(po, pt, (const uint32_t*)dids, (int)num_tokens, (int)hidden,
+                                     (int)(vocab > 0x7fffffffull ? 0x7fffffff : vocab),
+                                     (int)dtype_size(table->dtype), b->stream);
+    int r = slot >= 0 ? b->stage_done(slot) : FHIP_OK;
+    if (e != hipSuccess)
+        return fail(FHIP_ERR_BACKEND, "embedding kernel error: %s", hipGetErrorString((hipError_t)e));
+    return r;
+}
+
+// A u32 array of n values held by a backend tensor (any dtype: its bytes are read as uint32).
+int u32_array(fhip_backend* b, const fhip_tensor* t, size_t n, const char* what, void** out) {
+    CHECK_T(t);
+    GET_PTR(b, t, p);
+    if (size_bytes(t) < n * sizeof(uint32_t))
+        return fail(FHIP_ERR_INVALID_SHAPE, "%s: tensor %s holds fewer than %zu uint32 values",
+                    what, shape_str(t).c_str(), n);
+    *out = p;
+    return FHIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fhip_rope(fhip_backend* b, const fhip_tensor* q, const fhip_tensor* k,
+              const uint32_t* positions, size_t num_positions, double theta, size_t head_dim) {
+    (void)theta;  // the table from precompute_rope_freqs is used (backend.rs:166)
+    CHECK_B(b);
+    NO_CAPTURE(b, "rope (host positions; use fhip_rope_dev)");
+    if (num_positions && !positions) return fail(FHIP_ERR_INVALID_SHAPE, "null positions");
+    return rope_common(b, q, k, positions, nullptr, num_positions, head_dim);
+}
+
+int fhip_rope_dev(fhip_backend* b, const fhip_tensor* q, const fhip_tensor* k,
+                  const fhip_tensor* positions, size_t num_positions, size_t head_dim) {
+    CHECK_B(b);
+    if (num_positions == 0) return rope_common(b, q, k, nullptr, nullptr, 0, head_dim);
+    void* dp;
+    int r = u32_array(b, positions, num_positions, "rope positions", &dp);
+    if (r) return r;
+    return rope_common(b, q, k, nullptr, dp, num_positions, head_dim);
+}
+
+// Backend::attention (backend.rs:54-62) over contiguous K / V caches: not supported, as the
+// optional paged methods are on backends without them (backend.rs:74-88); the engine's caches are
+// paged.
+int fhip_attention(fhip_backend* b, const fhip_tensor* q, const fhip_tensor* k_cache,
+                   const fhip_tensor* v_cache, size_t num_kv_heads, size_t start_pos,
+                   const fhip_tensor* out) {
+    (void)q, (void)k_cache, (void)v_cache, (void)num_kv_heads, (void)start_pos, (void)out;
+    CHECK_B(b);
+    return fail(FHIP_ERR_BACKEND, "attention (contiguous KV cache) not supported by this backend");
 }
 
 int fhip_silu_mul(fhip_backend* b, const fhip_tensor* gate, const fhip_tensor* up,
@@ -641,32 +754,93 @@ int fhip_add(fhip_backend* b, const fhip_tensor* a, const fhip_tensor* bt, const
 int fhip_embedding(fhip_backend* b, const uint32_t* token_ids, size_t num_tokens,
                    const fhip_tensor* table, const fhip_tensor* out) {
     CHECK_B(b);
-    CHECK_T(table);
-    CHECK_T(out);
-    GET_PTR(b, table, pt);
-    GET_PTR(b, out, po);
-    if (table->ndim != 2 || (dtype_size(table->dtype) != 2 && dtype_size(table->dtype) != 4))
-        return fail(FHIP_ERR_INVALID_SHAPE, "embedding table %s",
-                    shape_str(table).c_str());
-    const uint64_t vocab = table->shape[0], hidden = table->shape[1];
-    if (numel(out) < num_tokens * hidden || out->dtype != table->dtype)
-        return fail(FHIP_ERR_INVALID_SHAPE, "embedding out %s for %zu tokens",
-                    shape_str(out).c_str(), num_tokens);
-    if (num_tokens == 0) return FHIP_OK;
-    if (!token_ids) return fail(FHIP_ERR_INVALID_SHAPE, "null token ids");
+    NO_CAPTURE(b, "embedding (host token ids; use fhip_embedding_dev)");
+    if (num_tokens && !token_ids) return fail(FHIP_ERR_INVALID_SHAPE, "null token ids");
+    return embedding_common(b, token_ids, nullptr, num_tokens, table, out);
+}
+
+int fhip_embedding_dev(fhip_backend* b, const fhip_tensor* token_ids, size_t num_tokens,
+                       const fhip_tensor* table, const fhip_tensor* out) {
+    CHECK_B(b);
+    if (num_tokens == 0) return embedding_common(b, nullptr, nullptr, 0, table, out);
+    void* dp;
+    int r = u32_array(b, token_ids, num_tokens, "embedding token ids", &dp);
+    if (r) return r;
+    return embedding_common(b, nullptr, dp, num_tokens, table, out);
+}
+
+// Graph capture of the backend's launches (a decode step's elementwise chain, recorded once
+// and replayed per step instead of launched kernel by kernel).
+int fhip_graph_begin(fhip_backend* b) {
+    CHECK_B(b);
     set_device(b);
     std::lock_guard<std::mutex> g(b->launch_mu);
-    void* dids;
-    int slot;
-    int r = b->stage(token_ids, num_tokens * sizeof(uint32_t), &dids, &slot);
-    if (r != FHIP_OK) return r;
-    int e = fhip_launch_embedding_ex(po, pt, (const uint32_t*)dids, (int)num_tokens, (int)hidden,
-                                     (int)(vocab > 0x7fffffffull ? 0x7fffffff : vocab),
-                                     (int)dtype_size(table->dtype), b->stream);
-    r = b->stage_done(slot);
-    if (e != hipSuccess)
-        return fail(FHIP_ERR_BACKEND, "embedding kernel error: %s", hipGetErrorString((hipError_t)e));
-    return r;
+    if (b->capturing) return fail(FHIP_ERR_BACKEND, "graph capture already in progress");
+    HIP_TRY(hipStreamBeginCapture(b->stream, hipStreamCaptureModeThreadLocal));
+    b->capturing = true;
+    return FHIP_OK;
+}
+
+int fhip_graph_end(fhip_backend* b, uint64_t* graph_out) {
+    CHECK_B(b);
+    if (!graph_out) return fail(FHIP_ERR_BACKEND, "null graph output");
+    *graph_out = 0;
+    set_device(b);
+    hipGraph_t graph = nullptr;
+    {
+        std::lock_guard<std::mutex> g(b->launch_mu);
+        if (!b->capturing) return fail(FHIP_ERR_BACKEND, "no graph capture in progress");
+        b->capturing = false;
+        hipError_t e = hipStreamEndCapture(b->stream, &graph);
+        if (e != hipSuccess) {
+            if (graph) (void)hipGraphDestroy(graph);
+            return hip_fail(e);
+        }
+    }
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) return hip_fail(e);
+    std::lock_guard<std::mutex> g(b->mu);
+    const uint64_t id = b->next_graph++;
+    b->graphs[id] = exec;
+    *graph_out = id;
+    return FHIP_OK;
+}
+
+int fhip_graph_launch(fhip_backend* b, uint64_t graph) {
+    CHECK_B(b);
+    NO_CAPTURE(b, "graph_launch");
+    hipGraphExec_t exec;
+    {
+        std::lock_guard<std::mutex> g(b->mu);
+        auto it = b->graphs.find(graph);
+        if (it == b->graphs.end())
+            return fail(FHIP_ERR_BACKEND, "graph %llu not found", (unsigned long long)graph);
+        exec = it->second;
+    }
+    set_device(b);
+    std::lock_guard<std::mutex> g(b->launch_mu);
+    HIP_TRY(hipGraphLaunch(exec, b->stream));
+    return FHIP_OK;
+}
+
+int fhip_graph_destroy(fhip_backend* b, uint64_t graph) {
+    CHECK_B(b);
+    NO_CAPTURE(b, "graph_destroy");
+    hipGraphExec_t exec;
+    {
+        std::lock_guard<std::mutex> g(b->mu);
+        auto it = b->graphs.find(graph);
+        if (it == b->graphs.end())
+            return fail(FHIP_ERR_BACKEND, "graph %llu not found", (unsigned long long)graph);
+        exec = it->second;
+        b->graphs.erase(it);
+    }
+    set_device(b);
+    HIP_TRY(hipStreamSynchronize(b->stream));  // replays queued on the stream finish first
+    HIP_TRY(hipGraphExecDestroy(exec));
+    return FHIP_OK;
 }
 
 int fhip_copy_rows(fhip_backend* b, const fhip_tensor* src, const fhip_tensor* dst,
@@ -717,6 +891,7 @@ size_t fhip_available_memory(fhip_backend* b) {
 
 int fhip_synchronize(fhip_backend* b) {
     CHECK_B(b);
+    NO_CAPTURE(b, "synchronize");
     set_device(b);
     HIP_TRY(hipStreamSynchronize(b->stream));
     return FHIP_OK;
@@ -724,6 +899,7 @@ int fhip_synchronize(fhip_backend* b) {
 
 int fhip_create_timer(fhip_backend* b, uint64_t* timer_id) {
     CHECK_B(b);
+    NO_CAPTURE(b, "create_timer");
     if (!timer_id) return fail(FHIP_ERR_BACKEND, "null timer id");
     set_device(b);
     hipEvent_t s, e;
@@ -750,6 +926,7 @@ static int find_timer(fhip_backend* b, uint64_t id, hipEvent_t* s, hipEvent_t* e
 
 int fhip_start_timer(fhip_backend* b, uint64_t timer_id) {
     CHECK_B(b);
+    NO_CAPTURE(b, "start_timer");
     hipEvent_t s, e;
     int r = find_timer(b, timer_id, &s, &e);
     if (r) return r;
@@ -759,6 +936,7 @@ int fhip_start_timer(fhip_backend* b, uint64_t timer_id) {
 
 int fhip_stop_timer(fhip_backend* b, uint64_t timer_id, float* ms_out) {
     CHECK_B(b);
+    NO_CAPTURE(b, "stop_timer");
     hipEvent_t s, e;
     int r = find_timer(b, timer_id, &s, &e);
     if (r) return r;
@@ -772,6 +950,7 @@ int fhip_stop_timer(fhip_backend* b, uint64_t timer_id, float* ms_out) {
 
 int fhip_destroy_timer(fhip_backend* b, uint64_t timer_id) {
     CHECK_B(b);
+    NO_CAPTURE(b, "destroy_timer");
     std::pair<hipEvent_t, hipEvent_t> ev;
     {
         std::lock_guard<std::mutex> g(b->mu);
@@ -802,6 +981,7 @@ int fhip_turboquant_compress(fhip_backend* b, const fhip_tensor* input, const fh
                              const fhip_tensor* centroids, uint8_t bits,
                              const fhip_tensor* packed_out, const fhip_tensor* norms_out) {
     CHECK_B(b);
+    NO_CAPTURE(b, "turboquant_compress");
     CHECK_T(input);
     CHECK_T(rotation);
     CHECK_T(centroids);
@@ -843,6 +1023,7 @@ int fhip_turboquant_compress(fhip_backend* b, const fhip_tensor* input, const fh
 int fhip_tq_quantize_pack(fhip_backend* b, const fhip_tensor* y, const fhip_tensor* centroids,
                           uint8_t bits, const fhip_tensor* packed_out) {
     CHECK_B(b);
+    NO_CAPTURE(b, "tq_quantize_pack");
     CHECK_T(y);
     CHECK_T(centroids);
     CHECK_T(packed_out);
@@ -872,6 +1053,7 @@ int fhip_tq_dequantize(fhip_backend* b, const fhip_tensor* packed, const fhip_te
                        const fhip_tensor* rotation, const fhip_tensor* centroids, uint8_t bits,
                        const fhip_tensor* out) {
     CHECK_B(b);
+    NO_CAPTURE(b, "tq_dequantize");
     CHECK_T(packed);
     CHECK_T(norms);
     CHECK_T(rotation);
@@ -907,6 +1089,7 @@ int fhip_tq_dequantize(fhip_backend* b, const fhip_tensor* packed, const fhip_te
 int fhip_softmax_rows(fhip_backend* b, const fhip_tensor* logits, float temperature,
                       const fhip_tensor* probs) {
     CHECK_B(b);
+    NO_CAPTURE(b, "softmax_rows");
     CHECK_T(logits);
     CHECK_T(probs);
     GET_PTR(b, logits, pl);
@@ -934,6 +1117,7 @@ int fhip_softmax_rows(fhip_backend* b, const fhip_tensor* logits, float temperat
 int fhip_argmax_rows(fhip_backend* b, const fhip_tensor* logits, uint32_t* tokens_out,
                      size_t rows_out) {
     CHECK_B(b);
+    NO_CAPTURE(b, "argmax_rows");
     CHECK_T(logits);
     GET_PTR(b, logits, pl);
     if (logits->ndim < 1 || logits->dtype != FHIP_FP32)
@@ -983,6 +1167,7 @@ int fhip_attention_paged_tq(fhip_backend* b, const fhip_tensor* q, const int32_t
                             uint8_t key_bits, uint8_t value_bits, size_t num_kv_heads,
                             size_t kv_len, size_t start_pos, const fhip_tensor* out) {
     CHECK_B(b);
+    NO_CAPTURE(b, "attention_paged_tq");
     CHECK_T(q);
     CHECK_T(k_rotation);
     CHECK_T(v_rotation);
@@ -1072,6 +1257,7 @@ int fhip_attention_paged_tq(fhip_backend* b, const fhip_tensor* q, const int32_t
 int fhip_page_pool_create(fhip_backend* b, const fhip_tensor* blocks, size_t nlists,
                           size_t pool_len, uint64_t* pool_out) {
     CHECK_B(b);
+    NO_CAPTURE(b, "page_pool_create");
     if (!pool_out || nlists == 0 || nlists > 8 || pool_len == 0 || !blocks)
         return fail(FHIP_ERR_INVALID_SHAPE, "page pool: %zu lists of %zu blocks", nlists,
                     pool_len);
@@ -1119,6 +1305,7 @@ int fhip_page_pool_create(fhip_backend* b, const fhip_tensor* blocks, size_t nli
 
 int fhip_page_pool_destroy(fhip_backend* b, uint64_t pool) {
     CHECK_B(b);
+    NO_CAPTURE(b, "page_pool_destroy");
     const void** dev = nullptr;
     {
         std::lock_guard<std::mutex> g(b->mu);
@@ -1175,6 +1362,7 @@ int fhip_attention_paged_pool(fhip_backend* b, const fhip_tensor* q, const int32
                               size_t num_blocks, uint64_t pool, size_t num_kv_heads,
                               size_t kv_len, size_t start_pos, const fhip_tensor* out) {
     CHECK_B(b);
+    NO_CAPTURE(b, "attention_paged_pool");
     CHECK_T(q);
     CHECK_T(out);
     GET_PTR(b, q, pq);
@@ -1235,6 +1423,7 @@ int fhip_attention_paged_tq_pool(fhip_backend* b, const fhip_tensor* q,
                                  uint8_t key_bits, uint8_t value_bits, size_t num_kv_heads,
                                  size_t kv_len, size_t start_pos, const fhip_tensor* out) {
     CHECK_B(b);
+    NO_CAPTURE(b, "attention_paged_tq_pool");
     CHECK_T(q);
     CHECK_T(k_rotation);
     CHECK_T(v_rotation);
@@ -1313,6 +1502,7 @@ int fhip_tq_append_kv(fhip_backend* b, uint64_t pool, const fhip_tensor* keys,
                       const fhip_tensor* v_centroids, uint8_t key_bits, uint8_t value_bits,
                       const int32_t* block_table, size_t num_blocks, size_t start_pos) {
     CHECK_B(b);
+    NO_CAPTURE(b, "tq_append_kv");
     CHECK_T(keys);
     CHECK_T(values);
     CHECK_T(k_rotation);
@@ -1411,6 +1601,7 @@ int fhip_attention_paged_tq_batched(fhip_backend* b, const fhip_tensor* q,
                                     uint8_t value_bits, size_t num_kv_heads,
                                     const fhip_tensor* out) {
     CHECK_B(b);
+    NO_CAPTURE(b, "attention_paged_tq_batched");
     CHECK_T(q);
     CHECK_T(k_rotation);
     CHECK_T(v_rotation);
@@ -1494,6 +1685,7 @@ int fhip_attention_paged(fhip_backend* b, const fhip_tensor* q, const int32_t* b
                          const fhip_tensor* v_blocks, size_t pool_len, size_t num_kv_heads,
                          size_t kv_len, size_t start_pos, const fhip_tensor* out) {
     CHECK_B(b);
+    NO_CAPTURE(b, "attention_paged");
     CHECK_T(q);
     CHECK_T(out);
     GET_PTR(b, q, pq);

@@ -132,6 +132,14 @@ int fhip_launch_paged_attention(void* output, const void* q, const int* block_ta
                                 int kv_len, int start_pos, int num_blocks_in_seq,
                                 fhip_stream_t stream);
 
+/* ffi.rs:172-184 `launch_attention` (contiguous KV cache): not supported; returns
+ * hipErrorNotSupported and launches nothing. The engine's caches are paged (engine.rs:671-680
+ * dispatches through the cache manager to the paged launchers above); the symbol lets a
+ * binding of the whole ffi.rs block link. */
+int fhip_launch_attention(void* output, const void* q, const void* k_cache, const void* v_cache,
+                          int num_tokens, int num_q_heads, int num_kv_heads, int head_dim,
+                          int kv_len, int start_pos, fhip_stream_t stream);
+
 /* The GEMM of CudaBackend::matmul (cuda/src/backend.rs:75-128), which calls cuBLAS directly:
  * C[M, N] = A[M, K] · B[N, K]^T, row-major fp16 operands, fp32 accumulation, on the stream. */
 int fhip_launch_matmul(void* c, const void* a, const void* b, int m, int n, int k,
@@ -391,6 +399,12 @@ int fhip_embedding(fhip_backend* b, const uint32_t* token_ids, size_t num_tokens
 int fhip_add(fhip_backend* b, const fhip_tensor* a, const fhip_tensor* bt, const fhip_tensor* out);
 int fhip_copy_rows(fhip_backend* b, const fhip_tensor* src, const fhip_tensor* dst,
                    size_t src_offset, size_t dst_offset, size_t count);
+/* Backend::attention (backend.rs:54-62) over contiguous K / V caches: not supported, returns
+ * FHIP_ERR_BACKEND ("... not supported by this backend"), as the reference's optional methods
+ * do on backends without them (backend.rs:74-88). */
+int fhip_attention(fhip_backend* b, const fhip_tensor* q, const fhip_tensor* k_cache,
+                   const fhip_tensor* v_cache, size_t num_kv_heads, size_t start_pos,
+                   const fhip_tensor* out);
 
 /* Backend::device_name / total_memory / available_memory / synchronize (backend.rs:126-135). */
 const char* fhip_device_name(fhip_backend* b);
@@ -486,6 +500,32 @@ int fhip_attention_paged_tq_batched(fhip_backend* b, const fhip_tensor* q,
                                     const fhip_tensor* out);
 
 /* --- additive handle ops --------------------------------------------------------------- */
+
+/* Backend::rope / Backend::embedding (backend.rs) with the positions / token ids already on
+ * the device: `positions` / `token_ids` is a backend tensor (any dtype) whose first
+ * 4 * num_positions (num_tokens) bytes are read as uint32 values. These are the forms a
+ * captured graph can hold: the caller refreshes the tensor with fhip_copy_to_device before
+ * each replay, where the reference passes a host slice per call (engine.rs:655-656). */
+int fhip_rope_dev(fhip_backend* b, const fhip_tensor* q, const fhip_tensor* k,
+                  const fhip_tensor* positions, size_t num_positions, size_t head_dim);
+int fhip_embedding_dev(fhip_backend* b, const fhip_tensor* token_ids, size_t num_tokens,
+                       const fhip_tensor* table, const fhip_tensor* out);
+
+/* HIP graph capture of the backend's launches. The reference launches every kernel of a
+ * layer's chain one at a time (engine.rs:621-706); here a run of launches is recorded once
+ * and replayed with one launch. Between fhip_graph_begin and fhip_graph_end the ops of the
+ * calling thread are recorded on the backend's stream instead of running; only ops whose
+ * arguments are all device-resident and that never wait on the host are accepted: rmsnorm,
+ * add, add_rmsnorm, silu_mul, copy_rows, fhip_rope_dev, fhip_embedding_dev. Every other op
+ * (host arrays, host waits, allocation, the workspace users, matmul) returns FHIP_ERR_BACKEND
+ * and records nothing. Other threads must keep off the backend during a capture. A graph
+ * holds the tensors' device addresses: they must stay allocated while it exists.
+ * fhip_graph_launch enqueues a replay on the backend's stream (asynchronous);
+ * fhip_graph_destroy waits for the stream first. Graph ids are per backend. */
+int fhip_graph_begin(fhip_backend* b);
+int fhip_graph_end(fhip_backend* b, uint64_t* graph_out);
+int fhip_graph_launch(fhip_backend* b, uint64_t graph);
+int fhip_graph_destroy(fhip_backend* b, uint64_t graph);
 
 /* Fused residual add + RMSNorm: residual += delta (in place), normed_out = rmsnorm(residual). */
 int fhip_add_rmsnorm(fhip_backend* b, const fhip_tensor* residual, const fhip_tensor* delta,

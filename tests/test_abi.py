@@ -30,7 +30,7 @@ def test_library_exports_every_header_symbol():
 def test_reference_launcher_names_are_covered():
     # one fhip_launch_* per launch_* symbol of backends/fracture-cuda/src/ffi.rs:141-274
     ref = ["rmsnorm", "rope", "silu_mul", "embedding", "add", "turboquant_compress",
-           "turboquant_decompress", "attention_paged_tq"]
+           "turboquant_decompress", "attention_paged_tq", "attention", "paged_attention"]
     for name in ref:
         assert f"fhip_launch_{name}" in _lib.header_symbols()
 
@@ -129,6 +129,8 @@ def test_raw_launchers_reject_bad_arguments_on_host():
     ml = 4 * 32 * 32 * 2 * 4
     assert lib.fhip_attention_paged_workspace_bytes(4, 32, 128, 2048) == ml + 4 * 32 * 32 * 128 * 4
     assert lib.fhip_attention_paged_workspace_bytes(0, 32, 128, 2048) == 0
+    # contiguous-cache attention (ffi.rs:172-184) is a stub: hipErrorNotSupported (801)
+    assert lib.fhip_launch_attention(1, 1, 1, 1, 1, 8, 2, 128, 16, 0, None) == 801
     # matmul sizes
     assert lib.fhip_launch_matmul(None, None, None, -1, 4, 4, None) == 1
     assert lib.fhip_launch_matmul(None, None, None, 0, 4, 4, None) == 0
