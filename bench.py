@@ -60,6 +60,8 @@ def parse():
                          "profiles/traffic.json")
     ap.add_argument("--ktrace-from", metavar="TRACE_DIR",
                     help="print a markdown summary of a rocprofv3 --kernel-trace run")
+    ap.add_argument("--counters-from", nargs="+", metavar="PMC_DIR",
+                    help="print per-kernel averages of rocprofv3 --pmc runs (one dir per pass)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-configs", action="store_true",
                     help="default run: leave out the other configurations' results")
@@ -1141,8 +1143,45 @@ def ktrace_summary(directory: str, min_run: int = 50) -> str:
     return "\n".join(lines)
 
 
+def counters_summary(directories) -> str:
+    """Markdown table of rocprofv3 --pmc runs (one directory per pass): each counter's value
+    per dispatch (summed over the hardware instances the profiler reports), averaged over the
+    dispatches of each of this library's kernels."""
+    import re
+    import sqlite3
+
+    per = {}       # kernel -> counter -> [values per dispatch]
+    order = []
+    for d in directories:
+        dbs = sorted(Path(d).rglob("*_results.db"))
+        if not dbs:
+            raise SystemExit(f"no rocpd database under {d}")
+        for db in dbs:
+            c = sqlite3.connect(db)
+            rows = c.execute("select dispatch_id, kernel_name, counter_name, sum(value) from "
+                             "counters_collection group by dispatch_id, counter_name").fetchall()
+            for _, name, counter, value in rows:
+                if "at::" in name or "rocclr" in name or "elementwise_kernel" in name:
+                    continue
+                short = re.sub(r"\(.*", "", name.replace("void ", "")
+                               .replace("(anonymous namespace)::", ""))
+                per.setdefault(short, {}).setdefault(counter, []).append(value)
+                if counter not in order:
+                    order.append(counter)
+    lines = ["| kernel | dispatches | " + " | ".join(order) + " |",
+             "|---|---|" + "---|" * len(order)]
+    for k, cs in sorted(per.items()):
+        n = max(len(v) for v in cs.values())
+        cells = [f"{sum(cs[c]) / len(cs[c]):.4g}" if c in cs else "-" for c in order]
+        lines.append(f"| `{k}` | {n} | " + " | ".join(cells) + " |")
+    return "\n".join(lines)
+
+
 def main():
     args = parse()
+    if args.counters_from:
+        print(counters_summary(args.counters_from))
+        return
     if args.ktrace_from:
         print(ktrace_summary(args.ktrace_from))
         return

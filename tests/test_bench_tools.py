@@ -89,3 +89,27 @@ def test_traffic_from_scales_by_the_calibration_copy(tmp_path):
     assert t["op_a"]["fetch_size_bytes"] == 1536 and t["op_a"]["write_size_bytes"] == 1536
     assert t["op_b"]["bytes_per_dispatch"] == 2 * 3072
     assert t["op_b"]["traffic_over_algorithmic"] == pytest.approx(3.072)
+
+
+def test_counters_summary_averages_per_kernel(tmp_path):
+    a, b = tmp_path / "a", tmp_path / "b"
+    a.mkdir()
+    b.mkdir()
+    c = sqlite3.connect(a / "pmc_results.db")
+    c.execute("create table counters_collection (dispatch_id integer, kernel_name text, "
+              "counter_name text, value real)")
+    # two dispatches of one kernel, each reported by two hardware instances; a torch kernel
+    c.executemany("insert into counters_collection values (?,?,?,?)", [
+        (1, "void fhip::k1<4>(int)", "SQ_INSTS_LDS", 10.0),
+        (1, "void fhip::k1<4>(int)", "SQ_INSTS_LDS", 5.0),
+        (2, "void fhip::k1<4>(int)", "SQ_INSTS_LDS", 20.0),
+        (2, "void fhip::k1<4>(int)", "SQ_INSTS_LDS", 5.0),
+        (3, "void at::native::fill(int)", "SQ_INSTS_LDS", 99.0)])
+    c.commit()
+    c.close()
+    _pmc_db(b / "pmc_results.db", "SQ_INSTS_MFMA", [("void fhip::k1<4>(int)", 7.0)])
+    md = bench.counters_summary([str(a), str(b)]).splitlines()
+    assert md[0] == "| kernel | dispatches | SQ_INSTS_LDS | SQ_INSTS_MFMA |"
+    assert len(md) == 3 and "at::" not in "".join(md)
+    cells = [x.strip() for x in md[2].split("|")[1:-1]]
+    assert cells == ["`fhip::k1<4>`", "2", "20", "7"]
