@@ -483,7 +483,9 @@ __global__ __launch_bounds__(256) void tq_attn_combine_kernel(
 //       B = (q_hi, 0) in column h and (q_lo*2^12, q_hi) in column 8+h, so one MFMA gives
 //       D[h] = sum c_hi q_hi and D[8+h] = 2^12 (sum c_hi q_lo + c_lo q_hi), and the score is
 //       (D[h] + 2^-12 D[8+h]) * norm_k / sqrt(128): fp16 operands, ~fp32 accuracy, no fp16
-//       subnormals. A fragments come from a 16-entry LDS table code -> (c_hi | c_lo' << 16).
+//       subnormals. A fragments come from an LDS table indexed by a code byte (two
+//       coordinates): byte -> the (c_hi | c_lo' << 16) words of its two codes, one
+//       ds_read_b64 and one address op per two codes.
 //   PV  out[h][d] accumulates W[h][pos] V[pos][d] the same way: B = (v_hi, v_lo') of the V
 //       code, A = (w_hi, 0) in row h and (w_lo*2^12, w_hi) in row 8+h, w = p * norm_v.
 //       The B operand needs 4 positions of one coordinate per lane; ds_read_b64_tr_b4 reads
@@ -513,41 +515,33 @@ __device__ __forceinline__ uint32_t hi_lo_pair(float v, float& hi_f) {
 __device__ __forceinline__ float ror8(float v) {  // lane n of each 16-lane row gets lane n^8
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, true));
 }
-// (byte kByte of x) & 0x3C in one v_and_b32_sdwa. Written as asm: the compiler turns the
-// shift-and-mask into two instructions for most byte positions.
+// 8 * (byte kByte of x), the byte offset of a pair-table entry, in one v_lshlrev_b32_sdwa.
+// Written as asm: the compiler turns the extract-and-shift into two instructions for most
+// byte positions.
 template <int kByte>
-__device__ __forceinline__ uint32_t byte_x4(uint32_t x) {
+__device__ __forceinline__ uint32_t byte_x8(uint32_t x) {
     uint32_t r;
     if constexpr (kByte == 0)
-        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0 src1_sel:DWORD"
-            : "=v"(r) : "v"(x), "s"(0x3Cu));
+        asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+            : "=v"(r) : "s"(3u), "v"(x));
     else if constexpr (kByte == 1)
-        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1 src1_sel:DWORD"
-            : "=v"(r) : "v"(x), "s"(0x3Cu));
+        asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
+            : "=v"(r) : "s"(3u), "v"(x));
     else if constexpr (kByte == 2)
-        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2 src1_sel:DWORD"
-            : "=v"(r) : "v"(x), "s"(0x3Cu));
+        asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
+            : "=v"(r) : "s"(3u), "v"(x));
     else
-        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3 src1_sel:DWORD"
-            : "=v"(r) : "v"(x), "s"(0x3Cu));
+        asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+            : "=v"(r) : "s"(3u), "v"(x));
     return r;
 }
-__device__ __forceinline__ uint32_t tab_at(const uint32_t* tab, uint32_t byte_off) {
-    return *(const uint32_t*)((const char*)tab + byte_off);
-}
-// Table entries of the nibbles of bytes kB, kB + 1 of a code word w, given wh = w >> 2 and
-// wl = w << 2 (byte k of wh & 0x3C = 4 x high nibble of byte k; of wl: 4 x low nibble).
-// Returns {hi(kB), lo(kB), hi(kB+1), lo(kB+1)}.
+// Pair-table entries of bytes kB and kB + 1 of a code word w: the (c_hi | c_lo' << 16) words
+// of those bytes' four codes, in the order the table holds each byte's two.
 template <int kB>
-__device__ __forceinline__ u32x4 tab_hl2(const uint32_t* tab, uint32_t wh, uint32_t wl) {
-    return u32x4{tab_at(tab, byte_x4<kB>(wh)), tab_at(tab, byte_x4<kB>(wl)),
-                 tab_at(tab, byte_x4<kB + 1>(wh)), tab_at(tab, byte_x4<kB + 1>(wl))};
-}
-// Same nibbles, low nibble first: {lo(kB), hi(kB), lo(kB+1), hi(kB+1)}.
-template <int kB>
-__device__ __forceinline__ u32x4 tab_lh2(const uint32_t* tab, uint32_t wh, uint32_t wl) {
-    return u32x4{tab_at(tab, byte_x4<kB>(wl)), tab_at(tab, byte_x4<kB>(wh)),
-                 tab_at(tab, byte_x4<kB + 1>(wl)), tab_at(tab, byte_x4<kB + 1>(wh))};
+__device__ __forceinline__ u32x4 pair2(const u32x2* tab, uint32_t w) {
+    const u32x2 e0 = *(const u32x2*)((const char*)tab + byte_x8<kB>(w));
+    const u32x2 e1 = *(const u32x2*)((const char*)tab + byte_x8<kB + 1>(w));
+    return u32x4{e0[0], e0[1], e1[0], e1[1]};
 }
 
 // The 4 pages of the chunk starting at t0 (page k: positions t0 + 16k .. +15; -1 past the end),
@@ -698,23 +692,28 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
                     int kvh, float scale, float* __restrict__ part_ml,
                     float* __restrict__ part_acc, int nsplit) {
     constexpr int hd = 128;
-    // code -> (c_hi | c_lo' << 16); K table in words 0..15, V table in 16..31. Consecutive
-    // words sit in distinct banks, so lookups by any mix of codes are conflict-free. The DMA
+    // Code-byte tables: byte b -> the (c_hi | c_lo' << 16) words of its two codes, K as
+    // {high nibble, low nibble} (the QK A operand's order), V as {low, high} (the PV B
+    // operand's). One ds_read_b64 serves two codes: lookups at random entries of 2 KB tables
+    // cost some bank conflicts, but half the LDS instructions and under half the address
+    // arithmetic of per-code lookups in a 16-word table. The DMA
     // targets are separate objects: table reads never wait for DMA traffic.
-    __shared__ uint32_t tabs[32];
+    __shared__ u32x2 pk[256], pv[256];
     __shared__ __attribute__((aligned(16))) uint8_t vbuf[kWavesM][2][kChunkM * 64];  // by chunk parity
     __shared__ __attribute__((aligned(16))) uint32_t nbuf[kWavesM][kChunkM];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, rg = lane >> 4;  // MFMA column / row group
-    if (threadIdx.x < 32) {
-        const int b = threadIdx.x & 15;
+    static_assert(64 * kWavesM == 256, "one table byte per thread");
+    {
+        const int b = threadIdx.x;
         float hf;
-        tabs[threadIdx.x] = hi_lo_pair(threadIdx.x < 16 ? kcent[b] : vcent[b], hf);
+        const uint32_t kh = hi_lo_pair(kcent[b >> 4], hf), kl = hi_lo_pair(kcent[b & 15], hf);
+        const uint32_t vh = hi_lo_pair(vcent[b >> 4], hf), vl = hi_lo_pair(vcent[b & 15], hf);
+        pk[b] = u32x2{kh, kl};
+        pv[b] = u32x2{vl, vh};
     }
     __syncthreads();
-    const uint32_t* tk = tabs;
-    const uint32_t* tv = tabs + 16;
 
     // items run kv head fastest: the heads of one (query, split) share a workgroup, so the two
     // heads whose 64-byte rows share a 128-byte line read it together
@@ -814,7 +813,7 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
         constexpr int kLookAhead = 2;
         auto qk_a = [&](int t) -> u32x4 {
             const uint32_t w = kcs[t >> 3][(t >> 1) & 3];
-            return (t & 1) ? tab_hl2<2>(tk, w >> 2, w << 2) : tab_hl2<0>(tk, w >> 2, w << 2);
+            return (t & 1) ? pair2<2>(pk, w) : pair2<0>(pk, w);
         };
         {
             u32x4 ahead[kLookAhead + 1];
@@ -921,7 +920,7 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
         auto pv_b = [&](int t) -> u32x4 {
             const int pt = t >> 3, c = t & 7;
             const uint32_t w = (uint32_t)tvs[c][pt >> 1];
-            return (pt & 1) ? tab_lh2<2>(tv, w >> 2, w << 2) : tab_lh2<0>(tv, w >> 2, w << 2);
+            return (pt & 1) ? pair2<2>(pv, w) : pair2<0>(pv, w);
         };
         {
             constexpr int kAheadPv = kLookAhead;
