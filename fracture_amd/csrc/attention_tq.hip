@@ -630,17 +630,19 @@ __device__ __forceinline__ void dma_v(const Pages& pg, const typename Pages::Lan
         dma16(ok ? base + lane_off : dummy, vb + 1024 * i);
     }
 }
-// Norms of position t0 + lane, loaded raw: knorm | vnorm << 16 = pack() once they are
-// needed (0 where there is none). Packing later keeps the wait for them away from the copies
-// issued after them.
+// Norms of position t0 + lane, loaded raw (fp16 bits): pack() gives (knorm, vnorm) in fp32
+// once they are needed (0 where there is none), so each norm is converted once, by the lane
+// that loaded it. Packing later keeps the wait for them away from the copies issued after them.
 struct NormRegs {
     uint32_t k, v;
     bool ok;
-    __device__ uint32_t pack() const {
+    __device__ float2 pack() const {
         uint32_t a = k, b = v;
         // pins the pack here: the compiler would otherwise pack right after the loads
         asm volatile("" : "+v"(a), "+v"(b));
-        return ok ? a | (b << 16) : 0u;
+        const float fk = (float)__builtin_bit_cast(_Float16, (uint16_t)a);
+        const float fv = (float)__builtin_bit_cast(_Float16, (uint16_t)b);
+        return ok ? float2{fk, fv} : float2{0.0f, 0.0f};
     }
 };
 template <class Pages>
@@ -700,7 +702,7 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     // targets are separate objects: table reads never wait for DMA traffic.
     __shared__ u32x2 pk[256], pv[256];
     __shared__ __attribute__((aligned(16))) uint8_t vbuf[kWavesM][2][kChunkM * 64];  // by chunk parity
-    __shared__ __attribute__((aligned(16))) uint32_t nbuf[kWavesM][kChunkM];
+    __shared__ __attribute__((aligned(16))) float2 nbuf[kWavesM][kChunkM];  // (knorm, vnorm)
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, rg = lane >> 4;  // MFMA column / row group
@@ -729,7 +731,7 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     const int G = qh / kvh;
     const int32_t* table = qs.table + (int64_t)qi * qs.table_stride;
     uint8_t* vb = vbuf[wave][0];
-    uint32_t* nb = nbuf[wave];
+    float2* nb = nbuf[wave];
 
     // The split's pages, one per lane (a split is 64 pages), read once: the chunk loop then
     // issues no memory instruction besides its copies.
@@ -775,10 +777,16 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     // Score of head n & 7 in both lanes n and n ^ 8: D[h] + 2^-12 D[8 + h].
     const float ca = n < 8 ? 1.0f : 1.0f / 4096.0f, cb = n < 8 ? 1.0f / 4096.0f : 1.0f;
     // PV A operand of weight w: row h (lanes n < 8) takes (w_hi, 0), row 8 + h takes
-    // (w_lo', w_hi). Both come from r = pkrtz(w, w * wz) followed by
-    // r.lo = f16(r.lo * wb + w * wc): lanes n < 8 keep r.lo = w_hi and have r.hi = 0,
-    // lanes n >= 8 get r.lo = 2^12 (w - w_hi). w_hi is w rounded toward zero.
-    const float wz = n < 8 ? 0.0f : 1.0f, wb = n < 8 ? 1.0f : -4096.0f, wc = n < 8 ? 0.0f : 4096.0f;
+    // (w_lo', w_hi), w_hi = w rounded toward zero. r = pkrtz(w, w) = (w_hi, w_hi), then
+    // r.lo = f16(r.lo * wb + w * wc) in place (lanes n < 8: w_hi; n >= 8: 2^12 (w - w_hi)),
+    // then lanes n < 8 clear r.hi.
+    const float wb = n < 8 ? 1.0f : -4096.0f, wc = n < 8 ? 0.0f : 4096.0f;
+    const uint32_t hmask = n < 8 ? 0xffffu : 0xffffffffu;
+    // cross-row exchanges (lane ^ 16, lane ^ 32) as ds_bpermute byte addresses
+    const int bp16 = (lane ^ 16) << 2, bp32 = (lane ^ 32) << 2;
+    auto xrow = [](int bp, float v) {
+        return __int_as_float(__builtin_amdgcn_ds_bpermute(bp, __float_as_int(v)));
+    };
     // transposed V reads: source lane m of group rg reads position 16rg + 4(m % 4) + m / 4;
     // segment s of that row sits at vrow[s ^ sw]
     const int srow = 16 * rg + 4 * (n & 3) + (n >> 2);
@@ -843,21 +851,19 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
         dma_v(pg, pl, pn, tn, t_end, v_lane_off, vb + (par ^ 1) * (kChunkM * 64), lane, dummy);
         nreg = load_norms(pg, pl, pn, tn, t_end, kvh, g, lane, dummy);
         load_k(pg, pl, pn, tn, t_end, kvh, g, lane, dummy, kreg);
-        f16x2_t nrm[16];  // positions 16rg + j: (knorm, vnorm)
+        float kn[16], vn[16];  // positions 16rg + j
 #pragma unroll
-        for (int j4 = 0; j4 < 4; ++j4) {
-            const u32x4 v = *(const u32x4*)&nb[16 * rg + 4 * j4];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                // through a scalar: bit_cast of a vector element reads element 0 on this clang
-                const uint32_t word = v[t];
-                nrm[4 * j4 + t] = __builtin_bit_cast(f16x2_t, word);
-            }
+        for (int j2 = 0; j2 < 8; ++j2) {
+            const f32x4_t v = *(const f32x4_t*)&nb[16 * rg + 2 * j2];
+            kn[2 * j2] = v[0];
+            vn[2 * j2] = v[1];
+            kn[2 * j2 + 1] = v[2];
+            vn[2 * j2 + 1] = v[3];
         }
 #pragma unroll
         for (int pt = 0; pt < 4; ++pt)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) sc[pt][e] *= (float)nrm[4 * e + pt].x;
+            for (int e = 0; e < 4; ++e) sc[pt][e] *= kn[4 * e + pt];
         if (!full) {
             const bool row_ok = (pc.mask >> rg) & 1u;
 #pragma unroll
@@ -871,8 +877,8 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
         for (int pt = 0; pt < 4; ++pt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) cmax = fmaxf(cmax, sc[pt][e]);
-        cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
-        cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+        cmax = fmaxf(cmax, xrow(bp16, cmax));
+        cmax = fmaxf(cmax, xrow(bp32, cmax));
         const float m_new = fmaxf(m_run, cmax);
         const float alpha =
             m_run == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
@@ -886,14 +892,17 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
             for (int e = 0; e < 4; ++e) {
                 const float pr = __builtin_amdgcn_exp2f(sc[pt][e] - mref);
                 psum += pr;
-                const float w = pr * (float)nrm[4 * e + pt].y;
-                f16x2_t r = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_cvt_pkrtz(w, w * wz));
-                r.x = (_Float16)fmaf((float)r.x, wb, w * wc);
-                aw[pt][e] = __builtin_bit_cast(uint32_t, r);
+                const float w = pr * vn[4 * e + pt];
+                uint32_t r = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(w, w));
+                // in place: written in C, the compiler merges the halves with an extra v_bfi
+                asm("v_fma_mixlo_f16 %0, %0, %1, %2 op_sel_hi:[1,0,0]"
+                    : "+v"(r)
+                    : "v"(wb), "v"(w * wc));
+                aw[pt][e] = r & hmask;
             }
         }
-        psum += __shfl_xor(psum, 16);
-        psum += __shfl_xor(psum, 32);
+        psum += xrow(bp16, psum);
+        psum += xrow(bp32, psum);
         l_run = l_run * alpha + psum;
         // rescale the accumulators when some head's max moved (each lane holds its own head's)
         const bool moved_any = __ballot((n < G) && (rg == 0) && (m_new > m_run)) != 0;
