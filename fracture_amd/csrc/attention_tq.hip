@@ -597,7 +597,9 @@ __device__ __forceinline__ void dma16(const uint8_t* src, uint8_t* lds) {
 // K codes of a chunk, loaded straight into the registers QK uses (LDS DMA streams markedly
 // slower than vector loads, and K needs no LDS stage): tile pt is position 4n + pt, bytes
 // [16rg, 16rg + 16) for lane (n, rg).
-template <class Pages>
+// kAll: every position of the chunk is present and every page valid (the common case), so
+// no lane needs a per-position check or the dummy source.
+template <bool kAll, class Pages>
 __device__ __forceinline__ void load_k(const Pages& pg, const typename Pages::Lane& pl,
                                        const ChunkPages& c, int t0, int t_end, int kvh, int g,
                                        int lane, const uint8_t* dummy, u32x4 (&kc)[4]) {
@@ -605,12 +607,12 @@ __device__ __forceinline__ void load_k(const Pages& pg, const typename Pages::La
     const uint8_t* base[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        base[i] = ((c.mask >> i) & 1u) ? pg.kpage_at(pl, c.j0 + i, c.id[i]) : dummy;
+        base[i] = (kAll || ((c.mask >> i) & 1u)) ? pg.kpage_at(pl, c.j0 + i, c.id[i]) : dummy;
     const bool page_ok = (c.mask >> k) & 1u;
     const uint8_t* src = pick4(base, k) + ((int64_t)(4 * (n & 3)) * kvh + g) * 64 + 16 * rg;
 #pragma unroll
     for (int pt = 0; pt < 4; ++pt) {
-        const bool ok = page_ok && t0 + 4 * n + pt < t_end;
+        const bool ok = kAll || (page_ok && t0 + 4 * n + pt < t_end);
         kc[pt] = ld16(ok ? src + (int64_t)pt * kvh * 64 : dummy);
     }
 }
@@ -618,15 +620,15 @@ __device__ __forceinline__ void load_k(const Pages& pg, const typename Pages::La
 // position p = 16i + L / 4 and stores 16 bytes at 64p + 16(L % 4). The 16-byte segment it
 // copies is (L % 4) ^ ((p / 2) % 4): rows are XOR-swizzled so the transposed reads of one
 // dim range from 16 rows spread over the banks.
-template <class Pages>
+template <bool kAll, class Pages>
 __device__ __forceinline__ void dma_v(const Pages& pg, const typename Pages::Lane& pl,
                                       const ChunkPages& c, int t0, int t_end, int64_t lane_off,
                                       uint8_t* vb, int lane, const uint8_t* dummy) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const bool page_ok = (c.mask >> i) & 1u;
+        const bool page_ok = kAll || ((c.mask >> i) & 1u);
         const uint8_t* base = page_ok ? pg.vpage_at(pl, c.j0 + i, c.id[i]) : dummy;
-        const bool ok = page_ok && t0 + 16 * i + (lane >> 2) < t_end;
+        const bool ok = kAll || (page_ok && t0 + 16 * i + (lane >> 2) < t_end);
         dma16(ok ? base + lane_off : dummy, vb + 1024 * i);
     }
 }
@@ -645,7 +647,7 @@ struct NormRegs {
         return ok ? float2{fk, fv} : float2{0.0f, 0.0f};
     }
 };
-template <class Pages>
+template <bool kAll, class Pages>
 __device__ __forceinline__ NormRegs load_norms(const Pages& pg, const typename Pages::Lane& pl,
                                                const ChunkPages& c, int t0, int t_end, int kvh,
                                                int g, int lane, const uint8_t* dummy) {
@@ -653,12 +655,12 @@ __device__ __forceinline__ NormRegs load_norms(const Pages& pg, const typename P
     const uint8_t* vn[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const bool ok = (c.mask >> i) & 1u;
+        const bool ok = kAll || ((c.mask >> i) & 1u);
         kn[i] = ok ? pg.knorm_at(pl, c.j0 + i, c.id[i]) : dummy;
         vn[i] = ok ? pg.vnorm_at(pl, c.j0 + i, c.id[i]) : dummy;
     }
     const int k = lane >> 4;
-    const bool ok = ((c.mask >> k) & 1u) && t0 + lane < t_end;
+    const bool ok = kAll || (((c.mask >> k) & 1u) && t0 + lane < t_end);
     const int64_t row = ok ? (int64_t)(lane & 15) * kvh + g : 0;
     return NormRegs{((const uint16_t*)pick4(kn, k))[row], ((const uint16_t*)pick4(vn, k))[row], ok};
 }
@@ -745,10 +747,10 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     const int64_t v_lane_off =
         ((int64_t)(lane >> 2) * kvh + g) * 64 + 16 * ((lane & 3) ^ ((lane >> 3) & 3));
     const uint8_t* dummy = (const uint8_t*)kcent;  // 64 readable bytes
-    dma_v(pg, pl, pc, t_begin, t_end, v_lane_off, vb, lane, dummy);  // chunk 0: buffer 0
-    NormRegs nreg = load_norms(pg, pl, pc, t_begin, t_end, kvh, g, lane, dummy);
+    dma_v<false>(pg, pl, pc, t_begin, t_end, v_lane_off, vb, lane, dummy);  // chunk 0: buffer 0
+    NormRegs nreg = load_norms<false>(pg, pl, pc, t_begin, t_end, kvh, g, lane, dummy);
     u32x4 kreg[4];
-    load_k(pg, pl, pc, t_begin, t_end, kvh, g, lane, dummy, kreg);
+    load_k<false>(pg, pl, pc, t_begin, t_end, kvh, g, lane, dummy, kreg);
     ChunkPages pn = chunk_pages(pg, split_page, t_begin, t_begin + kChunkM, t_end);
 
     // Q as the QK B operand, pre-scaled by scale * log2(e) so scores come out in log2 units:
@@ -838,7 +840,15 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
                     d, 0, 0, 0);
                 if ((t & 7) == 7) {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) sc[t >> 3][e] = fmaf(ror8(d[e]), cb, d[e] * ca);
+                    for (int e = 0; e < 4; ++e) {
+                        // fma(ror8(d), cb, d * ca) with the row rotation folded into the fmac
+                        // (the multiply reads d first, after the MFMA result is ready)
+                        float v = d[e] * ca;
+                        asm("v_fmac_f32_dpp %0, %1, %2 row_ror:8 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+                            : "+v"(v)
+                            : "v"(d[e]), "v"(cb));
+                        sc[t >> 3][e] = v;
+                    }
                     d = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
                 }
                 // keeps the scheduler from sinking the look-ahead reads to their MFMAs
@@ -848,9 +858,16 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
         // ---- K norms; then the K and norm registers are free: all loads of the next chunk,
         // its V codes into the other V buffer (after the last chunk: dummy copies)
         nb[lane] = nreg.pack();
-        dma_v(pg, pl, pn, tn, t_end, v_lane_off, vb + (par ^ 1) * (kChunkM * 64), lane, dummy);
-        nreg = load_norms(pg, pl, pn, tn, t_end, kvh, g, lane, dummy);
-        load_k(pg, pl, pn, tn, t_end, kvh, g, lane, dummy, kreg);
+        uint8_t* vnext = vb + (par ^ 1) * (kChunkM * 64);
+        if (pn.mask == 0xfu && tn + kChunkM <= t_end) {
+            dma_v<true>(pg, pl, pn, tn, t_end, v_lane_off, vnext, lane, dummy);
+            nreg = load_norms<true>(pg, pl, pn, tn, t_end, kvh, g, lane, dummy);
+            load_k<true>(pg, pl, pn, tn, t_end, kvh, g, lane, dummy, kreg);
+        } else {
+            dma_v<false>(pg, pl, pn, tn, t_end, v_lane_off, vnext, lane, dummy);
+            nreg = load_norms<false>(pg, pl, pn, tn, t_end, kvh, g, lane, dummy);
+            load_k<false>(pg, pl, pn, tn, t_end, kvh, g, lane, dummy, kreg);
+        }
         float kn[16], vn[16];  // positions 16rg + j
 #pragma unroll
         for (int j2 = 0; j2 < 8; ++j2) {
