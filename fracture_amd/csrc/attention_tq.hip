@@ -38,25 +38,14 @@ struct PtrPages {
     __device__ const uint8_t* knorm(int p) const { return kn[p]; }
     __device__ const uint8_t* vpage(int p) const { return vp[p]; }
     __device__ const uint8_t* vnorm(int p) const { return vn[p]; }
-    // Wave-wide page cache: lane j loads the four pointers of page `p` (its page of the
-    // current split); the `_at` accessors read them back from lane j.
-    struct Lane {
-        const uint8_t *k, *kn, *v, *vn;
-    };
-    __device__ Lane lane_load(int p) const {
-        if (!valid(p)) return Lane{nullptr, nullptr, nullptr, nullptr};
-        return Lane{kp[p], kn[p], vp[p], vn[p]};
+    // The four part addresses of page p (p valid).
+    __device__ void addrs(int p, const uint8_t*& k, const uint8_t*& knp, const uint8_t*& v,
+                          const uint8_t*& vnp) const {
+        k = kp[p];
+        knp = kn[p];
+        v = vp[p];
+        vnp = vn[p];
     }
-    static __device__ const uint8_t* rl(const uint8_t* x, int j) {
-        const uint64_t u = (uint64_t)x;
-        const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)u, j);
-        const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), j);
-        return (const uint8_t*)(((uint64_t)hi << 32) | lo);
-    }
-    __device__ const uint8_t* kpage_at(const Lane& l, int j, int) const { return rl(l.k, j); }
-    __device__ const uint8_t* knorm_at(const Lane& l, int j, int) const { return rl(l.kn, j); }
-    __device__ const uint8_t* vpage_at(const Lane& l, int j, int) const { return rl(l.v, j); }
-    __device__ const uint8_t* vnorm_at(const Lane& l, int j, int) const { return rl(l.vn, j); }
 };
 struct PoolPages {
     const uint8_t* kp;
@@ -70,13 +59,13 @@ struct PoolPages {
     __device__ const uint8_t* knorm(int p) const { return kn + p * skn; }
     __device__ const uint8_t* vpage(int p) const { return vp + p * svp; }
     __device__ const uint8_t* vnorm(int p) const { return vn + p * svn; }
-    // Page addresses are arithmetic on the id: the wave-wide page cache holds nothing.
-    struct Lane {};
-    __device__ Lane lane_load(int) const { return Lane{}; }
-    __device__ const uint8_t* kpage_at(const Lane&, int, int p) const { return kpage(p); }
-    __device__ const uint8_t* knorm_at(const Lane&, int, int p) const { return knorm(p); }
-    __device__ const uint8_t* vpage_at(const Lane&, int, int p) const { return vpage(p); }
-    __device__ const uint8_t* vnorm_at(const Lane&, int, int p) const { return vnorm(p); }
+    __device__ void addrs(int p, const uint8_t*& k, const uint8_t*& knp, const uint8_t*& v,
+                          const uint8_t*& vnp) const {
+        k = kpage(p);
+        knp = knorm(p);
+        v = vpage(p);
+        vnp = vnorm(p);
+    }
 };
 
 // Query q_i reads block-table row i (stride 0: one shared table) and attends to
@@ -496,6 +485,9 @@ __global__ __launch_bounds__(256) void tq_attn_combine_kernel(
 // Online softmax per head (lanes n = h), lazily rescaling the accumulators.
 // ---------------------------------------------------------------------------------------
 constexpr int kChunkM = 64;     // positions per chunk
+constexpr int kSplitMfma = 256;  // positions per wave item (split)
+constexpr int kXcds = 8;         // MI355X: accelerator complex dies, each with its own L2
+constexpr int kSplitPages = kSplitMfma / FHIP_PAGE_TOKENS;
 constexpr int kWavesM = 4;      // waves per workgroup (independent work items)
 
 typedef int v2i_t __attribute__((ext_vector_type(2)));
@@ -544,93 +536,92 @@ __device__ __forceinline__ u32x4 pair2(const u32x2* tab, uint32_t w) {
     return u32x4{e0[0], e0[1], e1[0], e1[1]};
 }
 
-// The 4 pages of the chunk starting at t0 (page k: positions t0 + 16k .. +15; -1 past the end),
-// the mask of those holding positions to read, and the lane of the split's page cache that
-// holds page 0 (lane j caches page j of the split).
-struct ChunkPages {
-    int id[4];
-    uint32_t mask;
-    int j0;
+// The split's pages, read once per split into a per-wave LDS table: entry j holds the four
+// part addresses (K codes, V codes, K norms, V norms) of the split's page j. Where page j holds
+// no position of the split, or its table entry is outside the pool, the entry holds the split's
+// first valid page instead, so every chunk load below reads a real page; the positions of such
+// pages are masked in the scores (bit j of the returned mask clear) and their norms zeroed.
+// With no valid page at all (mask 0) the split reads nothing.
+struct PageAddrs {
+    const uint8_t *k, *v, *kn, *vn;
 };
 template <class Pages>
-__device__ __forceinline__ ChunkPages chunk_pages(const Pages& pg, int split_page, int t_begin,
-                                                  int t0, int t_end) {
-    ChunkPages c;
-    c.mask = 0;
-    c.j0 = ((t0 - t_begin) / FHIP_PAGE_TOKENS) & 63;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int pos = t0 + 16 * k;
-        c.id[k] = pos < t_end ? __builtin_amdgcn_readlane(split_page, c.j0 + k) : -1;
-        if (pos < t_end && pg.valid(c.id[k])) c.mask |= 1u << k;
-    }
-    return c;
+__device__ __forceinline__ uint64_t split_pages(const Pages& pg, const int32_t* table, int t_begin,
+                                                int t_end, int lane, PageAddrs* pages) {
+    const bool in = t_begin + FHIP_PAGE_TOKENS * lane < t_end;
+    const int id = in ? table[t_begin / FHIP_PAGE_TOKENS + lane] : -1;
+    const bool ok = in && pg.valid(id);
+    const uint64_t vmask = __ballot(ok);
+    if (vmask == 0) return 0;
+    const int first = __builtin_amdgcn_readlane(id, (int)__builtin_ctzll(vmask));
+    PageAddrs a;
+    pg.addrs(ok ? id : first, a.k, a.kn, a.v, a.vn);
+    if (lane < kSplitPages) pages[lane] = a;
+    // the wave reads other lanes' entries next: LDS operations of one wave complete in order,
+    // and this keeps the compiler from moving those reads above the write
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    return vmask;
 }
-__device__ __forceinline__ const uint8_t* pick4(const uint8_t* const (&b)[4], int k) {
-    return k == 0 ? b[0] : k == 1 ? b[1] : k == 2 ? b[2] : b[3];
+// Loads through global-address-space pointers: addresses read back from LDS lose their
+// address space, and generic (flat) loads would also count against the LDS counter, so every
+// table-read wait would wait for them too.
+typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
+typedef __attribute__((address_space(1))) const uint16_t g_u16;
+__device__ __forceinline__ u32x4 gld16(const uint8_t* p) { return *(g_u32x4*)p; }
+__device__ __forceinline__ uint32_t gld2(const uint8_t* p) { return *(g_u16*)p; }
+
+// Lane j's address as a wave-uniform value (v_readlane into SGPRs).
+__device__ __forceinline__ const uint8_t* addr_of_lane(const uint8_t* p, int j) {
+    const uint64_t u = (uint64_t)p;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, j);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), j);
+    return (const uint8_t*)(((uint64_t)hi << 32) | lo);
 }
 
-// One 16-byte LDS DMA copy per lane: lane L writes lds + 16 L (lds wave-uniform). Issued as
-// asm so that the compiler, which counts pending LDS DMA against the LDS counter as well,
-// keeps exact LDS waits for the table lookups that run while copies are in flight (the
-// hardware tracks these copies on the vector memory counter only). Every read of the DMA
-// buffers waits for them explicitly.
-__device__ __forceinline__ void dma16(const uint8_t* src, uint8_t* lds) {
+// One 16-byte LDS DMA copy per lane from sbase + voff (sbase wave-uniform, in SGPRs): lane L
+// writes lds + 16 L (lds wave-uniform). Issued as asm so that the compiler, which counts
+// pending LDS DMA against the LDS counter as well, keeps exact LDS waits for the table lookups
+// that run while copies are in flight (the hardware tracks these copies on the vector memory
+// counter only). Every read of the DMA buffers waits for them explicitly.
+__device__ __forceinline__ void dma16(const uint8_t* sbase, uint32_t voff, uint8_t* lds) {
     const uint32_t m = __builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds);
     // m0 is saved and restored around the copy: the compiler may keep a value in it
     uint32_t saved;
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %2\n\t"
-        "global_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
-        : "v"(src), "s"(m)
+        : "v"(voff), "s"(sbase), "s"(m)
         : "memory");
 }
 
-// Every lane issues the same copies whatever the chunk holds, so each chunk adds a fixed
-// number of memory instructions and the compiler's wait counts stay exact. A lane with no
-// position to read copies from `dummy` (16 readable bytes) instead.
+// Chunk loads. The chunk starts at split page j0 (positions t0 .. t0 + 63 = pages j0 .. j0 + 3);
+// every address comes from the split's page lanes, so no load needs a per-position check.
 //
-// K codes of a chunk, loaded straight into the registers QK uses (LDS DMA streams markedly
-// slower than vector loads, and K needs no LDS stage): tile pt is position 4n + pt, bytes
-// [16rg, 16rg + 16) for lane (n, rg).
-// kAll: every position of the chunk is present and every page valid (the common case), so
-// no lane needs a per-position check or the dummy source.
-template <bool kAll, class Pages>
-__device__ __forceinline__ void load_k(const Pages& pg, const typename Pages::Lane& pl,
-                                       const ChunkPages& c, int t0, int t_end, int kvh, int g,
-                                       int lane, const uint8_t* dummy, u32x4 (&kc)[4]) {
-    const int n = lane & 15, rg = lane >> 4, k = n >> 2;
-    const uint8_t* base[4];
+// K codes, straight into the registers QK uses (LDS DMA streams markedly slower than vector
+// loads, and K needs no LDS stage): tile pt is position 4n + pt, bytes [16rg, 16rg + 16) for
+// lane (n, rg); the lane's page is j0 + n / 4 and the four tiles are 4 rows apart.
+__device__ __forceinline__ void load_k(const PageAddrs* pages, int j0, int kvh, int g, int lane,
+                                       u32x4 (&kc)[4]) {
+    const int n = lane & 15, rg = lane >> 4;
+    const uint8_t* src = pages[j0 + (n >> 2)].k + (uint32_t)(((4 * (n & 3)) * kvh + g) * 64 + 16 * rg);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        base[i] = (kAll || ((c.mask >> i) & 1u)) ? pg.kpage_at(pl, c.j0 + i, c.id[i]) : dummy;
-    const bool page_ok = (c.mask >> k) & 1u;
-    const uint8_t* src = pick4(base, k) + ((int64_t)(4 * (n & 3)) * kvh + g) * 64 + 16 * rg;
-#pragma unroll
-    for (int pt = 0; pt < 4; ++pt) {
-        const bool ok = kAll || (page_ok && t0 + 4 * n + pt < t_end);
-        kc[pt] = ld16(ok ? src + (int64_t)pt * kvh * 64 : dummy);
-    }
+    for (int pt = 0; pt < 4; ++pt) kc[pt] = gld16(src + (uint32_t)(pt * kvh * 64));
 }
-// V codes of a chunk by LDS DMA: copy i moves page i (positions 16i .. 16i + 15); lane L takes
+// V codes by LDS DMA: copy i moves page j0 + i (positions 16i .. 16i + 15); lane L takes
 // position p = 16i + L / 4 and stores 16 bytes at 64p + 16(L % 4). The 16-byte segment it
 // copies is (L % 4) ^ ((p / 2) % 4): rows are XOR-swizzled so the transposed reads of one
-// dim range from 16 rows spread over the banks.
-template <bool kAll, class Pages>
-__device__ __forceinline__ void dma_v(const Pages& pg, const typename Pages::Lane& pl,
-                                      const ChunkPages& c, int t0, int t_end, int64_t lane_off,
-                                      uint8_t* vb, int lane, const uint8_t* dummy) {
+// dim range from 16 rows spread over the banks. `voff` is that segment's offset in the page.
+__device__ __forceinline__ void dma_v(const PageAddrs* pages, int j0, uint32_t voff, uint8_t* vb,
+                                      int lane) {
+    const uint8_t* v4 = pages[j0 + (lane & 3)].v;  // lane i < 4: page j0 + i
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const bool page_ok = kAll || ((c.mask >> i) & 1u);
-        const uint8_t* base = page_ok ? pg.vpage_at(pl, c.j0 + i, c.id[i]) : dummy;
-        const bool ok = kAll || (page_ok && t0 + 16 * i + (lane >> 2) < t_end);
-        dma16(ok ? base + lane_off : dummy, vb + 1024 * i);
-    }
+    for (int i = 0; i < 4; ++i) dma16(addr_of_lane(v4, i), voff, vb + 1024 * i);
 }
 // Norms of position t0 + lane, loaded raw (fp16 bits): pack() gives (knorm, vnorm) in fp32
 // once they are needed (0 where there is none), so each norm is converted once, by the lane
@@ -647,22 +638,13 @@ struct NormRegs {
         return ok ? float2{fk, fv} : float2{0.0f, 0.0f};
     }
 };
-template <bool kAll, class Pages>
-__device__ __forceinline__ NormRegs load_norms(const Pages& pg, const typename Pages::Lane& pl,
-                                               const ChunkPages& c, int t0, int t_end, int kvh,
-                                               int g, int lane, const uint8_t* dummy) {
-    const uint8_t* kn[4];
-    const uint8_t* vn[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const bool ok = kAll || ((c.mask >> i) & 1u);
-        kn[i] = ok ? pg.knorm_at(pl, c.j0 + i, c.id[i]) : dummy;
-        vn[i] = ok ? pg.vnorm_at(pl, c.j0 + i, c.id[i]) : dummy;
-    }
+__device__ __forceinline__ NormRegs load_norms(const PageAddrs* pages, int j0, uint32_t pm, int t0,
+                                               int t_end, int kvh, int g, int lane) {
     const int k = lane >> 4;
-    const bool ok = kAll || (((c.mask >> k) & 1u) && t0 + lane < t_end);
-    const int64_t row = ok ? (int64_t)(lane & 15) * kvh + g : 0;
-    return NormRegs{((const uint16_t*)pick4(kn, k))[row], ((const uint16_t*)pick4(vn, k))[row], ok};
+    const uint32_t row = (uint32_t)(((lane & 15) * kvh + g) * 2);
+    const bool ok = ((pm >> k) & 1u) && t0 + lane < t_end;
+    const PageAddrs& pa = pages[j0 + k];
+    return NormRegs{gld2(pa.kn + row), gld2(pa.vn + row), ok};
 }
 
 // Loads of chunk i + 1 (V codes by LDS DMA, then norms and K codes into registers) are issued
@@ -694,7 +676,7 @@ __global__ __launch_bounds__(64 * kWavesM) __attribute__((amdgpu_waves_per_eu(3)
 tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
                     const float* __restrict__ kcent, const float* __restrict__ vcent, int qh,
                     int kvh, float scale, float* __restrict__ part_ml,
-                    float* __restrict__ part_acc, int nsplit) {
+                    float* __restrict__ part_acc, int nsplit, int nblk) {
     constexpr int hd = 128;
     // Code-byte tables: byte b -> the (c_hi | c_lo' << 16) words of its two codes, K as
     // {high nibble, low nibble} (the QK A operand's order), V as {low, high} (the PV B
@@ -705,10 +687,29 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     __shared__ u32x2 pk[256], pv[256];
     __shared__ __attribute__((aligned(16))) uint8_t vbuf[kWavesM][2][kChunkM * 64];  // by chunk parity
     __shared__ __attribute__((aligned(16))) float2 nbuf[kWavesM][kChunkM];  // (knorm, vnorm)
+    __shared__ PageAddrs pagebuf[kWavesM][kSplitPages];  // the wave's split pages
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, rg = lane >> 4;  // MFMA column / row group
     static_assert(64 * kWavesM == 256, "one table byte per thread");
+    static_assert(kWavesM * kSplitMfma == kSplit, "a workgroup's splits make one partial's block");
+
+    // Workgroup (query, kv head, block of kWavesM consecutive splits); wave w takes split
+    // kWavesM * blk + w. Workgroups go to the 8 XCDs round-robin (workgroup b on XCD b % 8),
+    // and the kv heads of one token row share 128-byte lines, so the index puts every kv head
+    // of one (query, block) item on the same XCD: item i = (query, block) and kv head g run
+    // as workgroup (i / 8) (8 kvh) + 8 g + i % 8, and each line is filled into one L2 only.
+    // A workgroup whose block holds no position leaves before the tables are built (the exit
+    // is uniform, so no wave misses the barriers below).
+    const int64_t wg = blockIdx.x;
+    const int64_t per8 = (int64_t)kXcds * kvh;
+    const int64_t item = (wg / per8) * kXcds + wg % kXcds;
+    const int g = (int)((wg % per8) / kXcds);
+    const int qi = (int)(item / nblk);
+    if (qi >= qs.seq_lens_count) return;
+    const int blk = (int)(item % nblk);
+    const int clen = qs.causal_len(qi);
+    if (blk * kSplit >= clen) return;
     {
         const int b = threadIdx.x;
         float hf;
@@ -719,39 +720,36 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     }
     __syncthreads();
 
-    // items run kv head fastest: the heads of one (query, split) share a workgroup, so the two
-    // heads whose 64-byte rows share a 128-byte line read it together
-    const int64_t item = (int64_t)blockIdx.x * kWavesM + wave;
-    const int64_t per_q = (int64_t)kvh * nsplit;
-    const int qi = (int)(item / per_q);
-    if (qi >= qs.seq_lens_count) return;
-    const int g = (int)(item % kvh), split = (int)((item / kvh) % nsplit);
-    const int clen = qs.causal_len(qi);
-    const int t_begin = split * kSplit;
-    if (t_begin >= clen) return;
-    const int t_end = min(clen, t_begin + kSplit);
+    const int split = kWavesM * blk + wave;
+    const int t_begin = split * kSplitMfma;
+    const int t_end = min(clen, t_begin + kSplitMfma);
     const int G = qh / kvh;
     const int32_t* table = qs.table + (int64_t)qi * qs.table_stride;
     uint8_t* vb = vbuf[wave][0];
     float2* nb = nbuf[wave];
+    const int64_t head0 = (int64_t)qi * qh + (int64_t)g * G;
 
-    // The split's pages, one per lane (a split is 64 pages), read once: the chunk loop then
-    // issues no memory instruction besides its copies.
-    static_assert(kSplit == 64 * FHIP_PAGE_TOKENS, "one cached page per lane");
-    const int split_page =
-        t_begin + FHIP_PAGE_TOKENS * lane < t_end ? table[t_begin / FHIP_PAGE_TOKENS + lane] : -1;
-    const typename Pages::Lane pl = pg.lane_load(split_page);
+    float m_run = -__builtin_inff(), l_run = 0.0f;  // log2 units; lanes n, n ^ 8: head n & 7
+    // PV accumulators out^T, dim tile c: lane (n, rg) holds head slot n (n < 8: head n, hi
+    // part; n >= 8: head n - 8, lo' part) at dims 16c + ((4rg + e) ^ 1), e = 0..3
+    f32x4_t acc[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
+    // The split's pages (at most kSplitPages), read once: the chunk loop then issues no memory
+    // instruction besides its loads and copies. A wave with no position to read (its split
+    // starts past the end, or no page is in the pool) keeps the empty state.
+    PageAddrs* pages = pagebuf[wave];
+    const uint64_t vmask = t_begin < clen ? split_pages(pg, table, t_begin, t_end, lane, pages) : 0;
+    if (vmask != 0) {
     // first chunk's copies go out before the Q set-up
-    ChunkPages pc = chunk_pages(pg, split_page, t_begin, t_begin, t_end);
-    const int64_t v_lane_off =
-        ((int64_t)(lane >> 2) * kvh + g) * 64 + 16 * ((lane & 3) ^ ((lane >> 3) & 3));
-    const uint8_t* dummy = (const uint8_t*)kcent;  // 64 readable bytes
-    dma_v<false>(pg, pl, pc, t_begin, t_end, v_lane_off, vb, lane, dummy);  // chunk 0: buffer 0
-    NormRegs nreg = load_norms<false>(pg, pl, pc, t_begin, t_end, kvh, g, lane, dummy);
+    const uint32_t v_lane_off =
+        (uint32_t)(((lane >> 2) * kvh + g) * 64 + 16 * ((lane & 3) ^ ((lane >> 3) & 3)));
+    uint32_t pmask = (uint32_t)vmask & 0xfu;  // pages of the current chunk to read
+    dma_v(pages, 0, v_lane_off, vb, lane);  // chunk 0: buffer 0
+    NormRegs nreg = load_norms(pages, 0, pmask, t_begin, t_end, kvh, g, lane);
     u32x4 kreg[4];
-    load_k<false>(pg, pl, pc, t_begin, t_end, kvh, g, lane, dummy, kreg);
-    ChunkPages pn = chunk_pages(pg, split_page, t_begin, t_begin + kChunkM, t_end);
+    load_k(pages, 0, kvh, g, lane, kreg);
 
     // Q as the QK B operand, pre-scaled by scale * log2(e) so scores come out in log2 units:
     // step s, lane (n, rg) holds coordinates 32rg + 4s + c4.
@@ -799,17 +797,11 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
         vseg[sg] = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)(
             vb + 64 * srow + 16 * (sg ^ sw));
 
-    float m_run = -__builtin_inff(), l_run = 0.0f;  // log2 units; lanes n, n ^ 8: head n & 7
-    // PV accumulators out^T, dim tile c: lane (n, rg) holds head slot n (n < 8: head n, hi
-    // part; n >= 8: head n - 8, lo' part) at dims 16c + ((4rg + e) ^ 1), e = 0..3
-    f32x4_t acc[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) acc[c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-
     for (int t0 = t_begin, par = 0; t0 < t_end; t0 += kChunkM, par ^= 1) {
         const int tn = t0 + kChunkM;  // next chunk
-        const ChunkPages pnn = chunk_pages(pg, split_page, t_begin, tn + kChunkM, t_end);
-        const bool full = pc.mask == 0xfu && tn <= t_end;
+        const int jn = (tn - t_begin) >> 4;  // its first split page
+        const uint32_t pmask_n = tn < t_end ? (uint32_t)(vmask >> jn) & 0xfu : 0u;
+        const bool full = pmask == 0xfu && tn <= t_end;
 
         // ---- QK: 4 tiles x 8 steps, K codes from this wave's DMA buffer
         float sc[4][4];  // [pt][e]: position 16rg + 4e + pt, head n & 7
@@ -856,17 +848,13 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
             }
         }
         // ---- K norms; then the K and norm registers are free: all loads of the next chunk,
-        // its V codes into the other V buffer (after the last chunk: dummy copies)
+        // its V codes into the other V buffer
         nb[lane] = nreg.pack();
         uint8_t* vnext = vb + (par ^ 1) * (kChunkM * 64);
-        if (pn.mask == 0xfu && tn + kChunkM <= t_end) {
-            dma_v<true>(pg, pl, pn, tn, t_end, v_lane_off, vnext, lane, dummy);
-            nreg = load_norms<true>(pg, pl, pn, tn, t_end, kvh, g, lane, dummy);
-            load_k<true>(pg, pl, pn, tn, t_end, kvh, g, lane, dummy, kreg);
-        } else {
-            dma_v<false>(pg, pl, pn, tn, t_end, v_lane_off, vnext, lane, dummy);
-            nreg = load_norms<false>(pg, pl, pn, tn, t_end, kvh, g, lane, dummy);
-            load_k<false>(pg, pl, pn, tn, t_end, kvh, g, lane, dummy, kreg);
+        if (tn < t_end) {
+            dma_v(pages, jn, v_lane_off, vnext, lane);
+            nreg = load_norms(pages, jn, pmask_n, tn, t_end, kvh, g, lane);
+            load_k(pages, jn, kvh, g, lane, kreg);
         }
         float kn[16], vn[16];  // positions 16rg + j
 #pragma unroll
@@ -882,7 +870,7 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
 #pragma unroll
             for (int e = 0; e < 4; ++e) sc[pt][e] *= kn[4 * e + pt];
         if (!full) {
-            const bool row_ok = (pc.mask >> rg) & 1u;
+            const bool row_ok = (pmask >> rg) & 1u;
 #pragma unroll
             for (int pt = 0; pt < 4; ++pt)
 #pragma unroll
@@ -964,27 +952,56 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        pc = pn;
-        pn = pnn;
+        pmask = pmask_n;
     }
 
-    // no copy may land in LDS after the wave has left
+    }  // vmask != 0
+
+    // no copy may land in LDS after this point: the V buffers hold the merge state next
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-    // ---- partials (m back in natural units): head slot h (hi) + 2^-12 slot 8 + h (lo'),
-    // lanes n and n ^ 8
-    const int64_t head0 = (int64_t)qi * qh + (int64_t)g * G;
-    if (n < G && rg == 0) {
-        part_ml[((head0 + n) * nsplit + split) * 2 + 0] = m_run * 0.6931471805599453f;
-        part_ml[((head0 + n) * nsplit + split) * 2 + 1] = l_run;
-    }
-    float* pacc = part_acc + ((head0 + (n & 7)) * nsplit + split) * hd;
+    // ---- merge the workgroup's splits into the block's partial. Each wave leaves its state
+    // in its own V buffer: acc[h][d] = slot h (hi) + 2^-12 slot 8 + h (lo'), lanes n and n ^ 8,
+    // then m (log2 units) and l per head. Each output (h, d) then sums the waves in wave order,
+    // weighted by exp2(m_w - max m) (0 for a wave with m = -inf).
+    float* st = (float*)vbuf[wave][0];
+    static_assert(sizeof(vbuf[0]) >= (kMaxG * hd + 2 * kMaxG) * sizeof(float), "merge state");
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const float v = fmaf(ror8(acc[c][e]), 1.0f / 4096.0f, acc[c][e]);
-            if (n < G) pacc[16 * c + ((4 * rg + e) ^ 1)] = v;
+            if (n < G) st[n * hd + 16 * c + ((4 * rg + e) ^ 1)] = v;
+        }
+    }
+    if (n < G && rg == 0) {
+        st[kMaxG * hd + n] = m_run;
+        st[kMaxG * hd + kMaxG + n] = l_run;
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < G * hd; idx += 64 * kWavesM) {
+        const int h = idx / hd, d = idx - h * hd;
+        float mw[kWavesM], M = -__builtin_inff();
+#pragma unroll
+        for (int w = 0; w < kWavesM; ++w) {
+            mw[w] = ((const float*)vbuf[w][0])[kMaxG * hd + h];
+            M = fmaxf(M, mw[w]);
+        }
+        float L = 0.0f, A = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWavesM; ++w) {
+            const float* sw = (const float*)vbuf[w][0];
+            if (mw[w] != -__builtin_inff()) {
+                const float wt = __builtin_amdgcn_exp2f(mw[w] - M);
+                L = fmaf(wt, sw[kMaxG * hd + kMaxG + h], L);
+                A = fmaf(wt, sw[h * hd + d], A);
+            }
+        }
+        part_acc[((head0 + h) * nsplit + blk) * hd + d] = A;
+        if (d == 0) {  // m back in natural units
+            part_ml[((head0 + h) * nsplit + blk) * 2 + 0] =
+                M == -__builtin_inff() ? M : M * 0.6931471805599453f;
+            part_ml[((head0 + h) * nsplit + blk) * 2 + 1] = L;
         }
     }
 }
@@ -993,12 +1010,15 @@ template <class Pages>
 void launch_mfma_split(const float* qrot, const Queries& qsv, const Pages& pg,
                        const float* kcent, const float* vcent, int nq, int qh, int kvh,
                        int nsplit, float* ml, float* acc, hipStream_t s) {
-    const int64_t items = (int64_t)nq * kvh * nsplit;
+    // one workgroup per (query, kv head, kSplit-position block): the block count is the
+    // partial layout's split count; the (query, block) items are padded to a multiple of the
+    // XCD count (the kernel's index spreads items, not heads, over the XCDs)
+    const int64_t wgs = ceil_div((int64_t)nq * nsplit, kXcds) * kXcds * kvh;
     Queries q2 = qsv;
     q2.seq_lens_count = nq;
-    hipLaunchKernelGGL((tq_attn_mfma_kernel<Pages>), dim3((unsigned)ceil_div(items, kWavesM)),
-                       dim3(64 * kWavesM), 0, s, qrot, q2, pg, kcent, vcent, qh, kvh,
-                       1.0f / sqrtf(128.0f), ml, acc, nsplit);
+    hipLaunchKernelGGL((tq_attn_mfma_kernel<Pages>), dim3((unsigned)wgs), dim3(64 * kWavesM), 0, s,
+                       qrot, q2, pg, kcent, vcent, qh, kvh, 1.0f / sqrtf(128.0f), ml, acc, nsplit,
+                       nsplit);
 }
 
 struct AttnArgs {

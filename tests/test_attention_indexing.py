@@ -2,28 +2,30 @@
 (tq_attn_mfma_kernel in fracture_amd/csrc/attention_tq.hip) and its combine kernel form,
 checked against the buffers the launcher hands them.
 
-The model restates the kernel's index arithmetic per wave item (query, kv head, 1024-position
-split) and per 64-position chunk, vectorised over lanes with numpy:
+The model restates the kernel's index arithmetic per workgroup (query, kv head, 1024-position
+block), per wave (one 256-position split of the block) and per 64-position chunk, vectorised
+over lanes with numpy:
 
-  split page cache   table[t_begin / 16 + lane]            (lanes whose page starts < t_end)
-  chunk_pages        page ids of positions t0 + 16k, k = 0..3, kept when in [0, num_pages)
-  load_k             page(k = n / 4) + ((4 (n % 4) + pt) kvh + g) 64 + 16 rg, 16 bytes
-  dma_v              page(i) + ((lane / 4) kvh + g) 64 + 16 ((lane % 4) ^ ((lane / 8) % 4)), 16 bytes
-  load_norms         norm page(lane / 16) + 2 ((lane % 16) kvh + g), 2 bytes
+  split pages        entry j = table[t_begin / 16 + j] for pages holding positions of the split,
+                     in the pool; every other entry is the split's first valid page (no valid
+                     page: the wave reads nothing)
+  load_k             entry(j0 + n / 4) + ((4 (n % 4) + pt) kvh + g) 64 + 16 rg, 16 bytes
+  dma_v              entry(j0 + i) + ((lane / 4) kvh + g) 64 + 16 ((lane % 4) ^ ((lane / 8) % 4)), 16 bytes
+  load_norms         norm entry(j0 + lane / 16) + 2 ((lane % 16) kvh + g), 2 bytes
   Q (rotated)        (qi qh + g G + h) hd + 32 rg + 4 s, 16 bytes
-  partials           ((head0 + h) nsplit + split) (2 | hd) + ...
+  partials           ((head0 + h) nsplit + block) (2 | hd) + ..., written by the workgroup's merge
 
 and asserts that each access stays inside its pool AND inside the page it means to read
 (an access past the page's rows reads a neighbouring page: in bounds, but wrong data).
-Lanes that read no position use `dummy` (the 64-byte K centroid table), which is checked to
-be large enough. No GPU is used.
+The next chunk's loads are issued only while it starts before the split's end. No GPU is used.
 """
 import numpy as np
 import pytest
 
 PAGE = 16
-SPLIT = 1024
 CHUNK = 64
+SPLIT = 1024       # positions per partial (the MFMA kernel's workgroup block, the VALU kernel's split)
+WAVE_SPLIT = 256   # positions per MFMA wave
 
 
 def ws_layout(nq, qh, hd, max_tokens):
@@ -64,69 +66,63 @@ def model_mfma_kernel(lens, table, num_pages, qh, kvh, page_bytes, pool_bytes):
     nsplit, _, ml_bytes, acc_bytes = ws_layout(B, qh, hd, max_blocks * PAGE)
     bnd = Bounds({"table": table.size * 4, "kp": pool_bytes["kp"], "kn": pool_bytes["kn"],
                   "vp": pool_bytes["vp"], "vn": pool_bytes["vn"], "qrot": B * qh * hd * 4,
-                  "part_ml": ml_bytes, "part_acc": acc_bytes, "dummy": 64})
+                  "part_ml": ml_bytes, "part_acc": acc_bytes})
     lane = np.arange(64)
     n, rg = lane & 15, lane >> 4
     for qi in range(B):
         clen = causal_len(lens[qi], max_blocks)
-        for split in range(nsplit):
-            t_begin = split * SPLIT
-            if t_begin >= clen:
-                continue
-            t_end = min(clen, t_begin + SPLIT)
-            # split page cache: one table entry per lane
-            has = t_begin + PAGE * lane < t_end
-            tidx = t_begin // PAGE + lane[has]
-            assert tidx.max() < max_blocks
-            bnd.check("table", (qi * max_blocks + tidx) * 4, 4)
-            split_page = np.full(64, -1, np.int64)
-            split_page[has] = table[qi, tidx]
-            chunks = np.arange(t_begin, t_end, CHUNK)
+        for blk in range(nsplit):
+            if blk * SPLIT >= clen:
+                continue  # the workgroup leaves before building its tables
             for g in range(kvh):
-                for t0 in chunks:
-                    j0 = ((t0 - t_begin) // PAGE) & 63
-                    pos = t0 + PAGE * np.arange(4)
-                    assert j0 + 3 < 64, "page cache lane index past the wave"
-                    ids = np.where(pos < t_end, split_page[(j0 + np.arange(4)) & 63], -1)
-                    ok_page = (pos < t_end) & (ids >= 0) & (ids < num_pages)
-                    # load_k: lane (n, rg), page k = n / 4, tiles pt = 0..3
-                    k = n >> 2
-                    for pt in range(4):
-                        ok = ok_page[k] & (t0 + 4 * n + pt < t_end)
-                        row = 4 * (n & 3) + pt
-                        inpage = (row * kvh + g) * pd + 16 * rg
-                        assert inpage[ok].max(initial=0) + 16 <= min(PAGE * kvh * pd, page_bytes["kp"])
-                        off = ids[k] * page_bytes["kp"] + inpage
-                        bnd.check("kp", off[ok], 16)
-                        bnd.check("dummy", np.zeros(int((~ok).sum())), 16)
-                    # dma_v: copy i = page i, lane L position 16 i + L / 4
-                    for i in range(4):
-                        ok = ok_page[i] & (t0 + 16 * i + (lane >> 2) < t_end)
-                        inpage = ((lane >> 2) * kvh + g) * pd + 16 * ((lane & 3) ^ ((lane >> 3) & 3))
-                        assert inpage[ok].max(initial=0) + 16 <= min(PAGE * kvh * pd, page_bytes["vp"])
-                        off = ids[i] * page_bytes["vp"] + inpage
-                        bnd.check("vp", np.broadcast_to(off, lane.shape)[ok], 16)
-                    # load_norms: lane -> page lane / 16, row lane % 16 (row 0 when unused)
-                    kk = lane >> 4
-                    ok = ok_page[kk] & (t0 + lane < t_end)
-                    row = np.where(ok, (lane & 15) * kvh + g, 0)
-                    for nm in ("kn", "vn"):
-                        off = ids[kk] * page_bytes[nm] + 2 * row
-                        bnd.check(nm, off[ok_page[kk]], 2)
-                        assert (2 * row + 2).max() <= min(PAGE * kvh * 2, page_bytes[nm])
-                # Q: heads past G read head 0
-                h = n & 7
-                hsrc = np.where(h < G, h, 0)
-                for s8 in range(8):
-                    bnd.check("qrot", ((qi * qh + g * G + hsrc) * hd + 32 * rg + 4 * s8) * 4, 16)
-                head0 = qi * qh + g * G
+                for w in range(SPLIT // WAVE_SPLIT):
+                    t_begin = (4 * blk + w) * WAVE_SPLIT
+                    if t_begin >= clen:
+                        continue  # empty state, nothing read
+                    t_end = min(clen, t_begin + WAVE_SPLIT)
+                    has = t_begin + PAGE * lane < t_end
+                    tidx = t_begin // PAGE + lane[has]
+                    assert tidx.max() < max_blocks
+                    bnd.check("table", (qi * max_blocks + tidx) * 4, 4)
+                    ids = np.full(64, -1, np.int64)
+                    ids[has] = table[qi, tidx]
+                    ok = has & (ids >= 0) & (ids < num_pages)
+                    if not ok.any():
+                        continue
+                    entry = np.where(ok, ids, ids[np.flatnonzero(ok)[0]])[:WAVE_SPLIT // PAGE]
+                    assert ((entry >= 0) & (entry < num_pages)).all()
+                    for t0 in range(t_begin, t_end, CHUNK):
+                        j0 = (t0 - t_begin) // PAGE
+                        assert j0 + 3 < len(entry), "page entry index past the wave's table"
+                        # load_k: lane (n, rg), entry j0 + n / 4, tiles pt = 0..3
+                        e = entry[j0 + (n >> 2)]
+                        for pt in range(4):
+                            row = 4 * (n & 3) + pt
+                            inpage = (row * kvh + g) * pd + 16 * rg
+                            assert inpage.max() + 16 <= min(PAGE * kvh * pd, page_bytes["kp"])
+                            bnd.check("kp", e * page_bytes["kp"] + inpage, 16)
+                        # dma_v: copy i = entry j0 + i, lane L position 16 i + L / 4
+                        for i in range(4):
+                            inpage = ((lane >> 2) * kvh + g) * pd + 16 * ((lane & 3) ^ ((lane >> 3) & 3))
+                            assert inpage.max() + 16 <= min(PAGE * kvh * pd, page_bytes["vp"])
+                            bnd.check("vp", entry[j0 + i] * page_bytes["vp"] + inpage, 16)
+                        # load_norms: lane -> entry j0 + lane / 16, row lane % 16
+                        e = entry[j0 + (lane >> 4)]
+                        row = (lane & 15) * kvh + g
+                        for nm in ("kn", "vn"):
+                            assert (2 * row + 2).max() <= min(PAGE * kvh * 2, page_bytes[nm])
+                            bnd.check(nm, e * page_bytes[nm] + 2 * row, 2)
+                    # Q: heads past G read head 0
+                    h = n & 7
+                    hsrc = np.where(h < G, h, 0)
+                    for s8 in range(8):
+                        bnd.check("qrot", ((qi * qh + g * G + hsrc) * hd + 32 * rg + 4 * s8) * 4, 16)
+                # the workgroup's merge: one partial per head of the group
+                hg0 = qi * qh + g * G
                 hs = np.arange(G)
-                bnd.check("part_ml", (((head0 + hs) * nsplit + split) * 2) * 4, 8)
-                c = np.arange(8)[:, None, None]
-                e = np.arange(4)[None, :, None]
-                sel = n < G
-                dims = 16 * c + ((4 * rg[sel][None, None, :] + e) ^ 1)
-                bnd.check("part_acc", (((head0 + (n[sel] & 7)) * nsplit + split) * hd + dims) * 4, 4)
+                bnd.check("part_ml", (((hg0 + hs) * nsplit + blk) * 2) * 4, 8)
+                bnd.check("part_acc", (((hg0 + hs[:, None]) * nsplit + blk) * hd
+                                       + np.arange(hd)[None, :]) * 4, 4)
     return bnd, nsplit
 
 
@@ -171,9 +167,18 @@ def pools(P, kvh, pd=64):
     return page, {k: v * P for k, v in page.items()}
 
 
-@pytest.mark.parametrize("which", ["c5", "edges"])
+@pytest.mark.parametrize("which", ["c5", "edges", "long"])
 def test_mfma_decode_accesses_in_bounds(which):
-    if which == "c5":
+    if which == "long":
+        # a context of 270,000 positions (264 partial blocks) over a permuted table
+        lens = np.array([270000, 5], np.int32)
+        max_blocks = 270000 // 16
+        rng = np.random.default_rng(4)
+        P = max_blocks + 100
+        table = np.full((len(lens), max_blocks), -1, np.int32)
+        table[0] = rng.permutation(P)[:max_blocks]
+        table[1, 0] = 7
+    elif which == "c5":
         lens, table, P = c5_workload()
         assert lens.max() > 16 * SPLIT, "the workload must reach the combine's second 16-split step"
     else:
