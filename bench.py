@@ -591,11 +591,19 @@ def run_tq(args, torch, K, dev):
         # codebooks once) and the reference-signature entries that rebuild them per call
         kplan, vplan = K.TqPlan(krot, cent, bits), K.TqPlan(vrot, cent, bits)
 
+        # the layer's keys and values in one launch (as append_kv compresses them)
         def comp():
+            K.tq_compress_kv_planned(kplan, vplan, k, v, kp, kn, vp, vn)
+
+        def deq():
+            K.tq_dequant_kv_planned(kplan, vplan, kp, kn, vp, vn, kd, vd)
+
+        # one launch per tensor (the trait's turboquant_compress per tensor, with a plan)
+        def comp_split():
             K.tq_compress_planned(kplan, k, kp, kn)
             K.tq_compress_planned(vplan, v, vp, vn)
 
-        def deq():
+        def deq_split():
             K.tq_dequant_planned(kplan, kp, kn, kd)
             K.tq_dequant_planned(vplan, vp, vn, vd)
 
@@ -610,6 +618,8 @@ def run_tq(args, torch, K, dev):
         nb = 2 * (N * H * hd * 2 + N * H * pd + N * H * 2)  # K and V: read fp16, write codes+norms
         flops = 2 * 2 * N * H * hd * hd
         for name, fn, tkey in (("compress", comp, "compress"), ("dequant", deq, "dequant"),
+                               ("compress_per_tensor", comp_split, None),
+                               ("dequant_per_tensor", deq_split, None),
                                ("compress_unplanned", comp_unplanned, None),
                                ("dequant_unplanned", deq_unplanned, None)):
             us = timer.time_us(fn, 20, warmup=3)
@@ -772,13 +782,11 @@ def pmc_sequence(torch, K, dev):
 
         plans = [K.TqPlan(rots[i], cent, bits) for i in range(2)]
 
-        def comp(plans=plans, pk=pk, nm=nm):
-            for i in range(2):
-                K.tq_compress_planned(plans[i], kv[i], pk[i], nm[i])
+        def comp(plans=plans, pk=pk, nm=nm):  # keys and values in one launch
+            K.tq_compress_kv_planned(plans[0], plans[1], kv[0], kv[1], pk[0], nm[0], pk[1], nm[1])
 
         def deq(plans=plans, pk=pk, nm=nm, dq=dq):
-            for i in range(2):
-                K.tq_dequant_planned(plans[i], pk[i], nm[i], dq[i])
+            K.tq_dequant_kv_planned(plans[0], plans[1], pk[0], nm[0], pk[1], nm[1], dq[0], dq[1])
 
         seq += [(f"tq_compress_{bits}bit", comp, nbytes), (f"tq_dequant_{bits}bit", deq, nbytes)]
     fn, nb_att, _, _ = attention_inputs(torch, K, dev)

@@ -75,6 +75,10 @@ SIGNATURES = {
     "fhip_launch_tq_compress_planned": (I, [P, P, P, P, I, I, P]),
     "fhip_launch_tq_compress_pages_planned": (I, [P, P, P, P, I64, I64, P, I, I, I, I, P]),
     "fhip_launch_tq_dequant_planned": (I, [P, P, P, P, I, I, P]),
+    "fhip_launch_tq_compress_kv_planned": (I, [P, P, P, P, P, P, P, P, I, I, P]),
+    "fhip_launch_tq_compress_kv_page_ptrs_planned": (I, [P, P, P, P, P, P, P, P, P, I, I, I, I,
+                                                         P]),
+    "fhip_launch_tq_dequant_kv_planned": (I, [P, P, P, P, P, P, P, P, I, I, P]),
     "fhip_attention_tq_workspace_bytes": (SZ, [I, I, I, I]),
     "fhip_launch_attention_tq_decode": (I, [P, P, P, P, I, I, I, P, P, P, P, I64, I64, I64, I64,
                                             P, P, P, P, I, I, I, I, I, P, P]),

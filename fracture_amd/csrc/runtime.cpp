@@ -1568,10 +1568,20 @@ int fhip_tq_append_kv(fhip_backend* b, uint64_t pool, const fhip_tensor* keys,
         } sides[2] = {{pk, k_rotation->id, k_centroids->id, pkr, pkc, (int)KL, key_bits, 0},
                       {pv, v_rotation->id, v_centroids->id, pvr, pvc, (int)VL, value_bits, 2}};
         e = hipSuccess;
-        for (const Side& sd : sides) {
+        fhip_tq_plan* plans[2];
+        for (int i = 0; i < 2; ++i)
+            plans[i] = b->plan_for(sides[i].rot_id, sides[i].rot, sides[i].cent_id, sides[i].cent,
+                                   sides[i].levels, sides[i].bits, (int)hd);
+        // both plans: keys and values in one launch
+        const bool kv = plans[0] && plans[1];
+        if (kv)
+            e = (hipError_t)fhip_launch_tq_compress_kv_page_ptrs_planned(
+                plans[0], plans[1], pk, pv, dp, dp + n, dp + 2 * n, dp + 3 * n,
+                (const int32_t*)dbt, (int)n, (int)start_pos, (int)N, (int)kvh, b->stream);
+        for (int i = 0; i < 2 && !kv; ++i) {
+            const Side& sd = sides[i];
             if (e != hipSuccess) break;
-            fhip_tq_plan* plan = b->plan_for(sd.rot_id, sd.rot, sd.cent_id, sd.cent, sd.levels,
-                                             sd.bits, (int)hd);
+            fhip_tq_plan* plan = plans[i];
             if (plan)
                 e = (hipError_t)fhip_launch_tq_compress_page_ptrs_planned(
                     plan, sd.x, dp + sd.list * n, dp + (sd.list + 1) * n, (const int32_t*)dbt,

@@ -412,10 +412,11 @@ template <int kMode, int kBits, bool kUnitFast, class Dst>
 __device__ __forceinline__ void compress_waves(const Quantizer& qz, const RotLds& L,
                                                const uint16_t* __restrict__ in, const Dst& dst,
                                                float* __restrict__ y_out, int64_t rows,
-                                               f16x8 (&xa)[8], f16x8 (&xb)[8]) {
+                                               f16x8 (&xa)[8], f16x8 (&xb)[8], int64_t blk,
+                                               int64_t nblk) {
     const int64_t ntiles = ceil_div(rows, kTile);
-    const int64_t stride = (int64_t)gridDim.x * kWavesC;
-    int64_t tile = (int64_t)blockIdx.x * kWavesC + wave_id();
+    const int64_t stride = nblk * kWavesC;
+    int64_t tile = blk * kWavesC + wave_id();
     f16x8 xc[8];
     // Three register buffers in rotation, one tile per step: while a tile computes, the
     // loads of the next two are in flight.
@@ -444,13 +445,14 @@ __device__ __forceinline__ void compress_waves(const Quantizer& qz, const RotLds
 template <int kMode, int kBits, class Dst>
 __device__ __noinline__ void compress_waves_general(const Quantizer& qz, const RotLds& L,
                                                     const uint16_t* __restrict__ in, Dst dst,
-                                                    float* __restrict__ y_out, int64_t rows) {
-    const int64_t first = (int64_t)blockIdx.x * kWavesC + wave_id();
+                                                    float* __restrict__ y_out, int64_t rows,
+                                                    int64_t blk, int64_t nblk) {
+    const int64_t first = blk * kWavesC + wave_id();
     const int64_t ntiles = ceil_div(rows, kTile);
     f16x8 xa[8], xb[8];
     load_x_half(in, first, ntiles, rows, xa);
-    load_x_half(in, first + (int64_t)gridDim.x * kWavesC, ntiles, rows, xb);
-    compress_waves<kMode, kBits, false>(qz, L, in, dst, y_out, rows, xa, xb);
+    load_x_half(in, first + nblk * kWavesC, ntiles, rows, xb);
+    compress_waves<kMode, kBits, false>(qz, L, in, dst, y_out, rows, xa, xb, blk, nblk);
 }
 
 // Copy of kBytes (a multiple of 16) from global memory into LDS by the whole block, in two
@@ -479,8 +481,37 @@ struct TqPlanDev;
 __device__ __forceinline__ const Quantizer& plan_quantizer(const TqPlanDev* p);
 __device__ __forceinline__ const RotLds& plan_compress_frags(const TqPlanDev* p);
 
-// kPlanned: the quantizer and the rotation fragments come ready-made from a plan (built once
-// per rotation and codebook by tq_plan_kernel) and are only copied into LDS; otherwise the
+// The planned compress of one tensor by workgroup blk of nblk: the quantizer and the rotation
+// fragments come ready-made from the plan (built once per rotation and codebook by
+// tq_plan_kernel) and are only copied into LDS.
+template <int kMode, int kBits, class Dst>
+__device__ __forceinline__ void compress_planned(Quantizer& qz, RotLds& rl,
+                                                 const uint16_t* __restrict__ in,
+                                                 const TqPlanDev* __restrict__ plan,
+                                                 const Dst& dst, float* __restrict__ y_out,
+                                                 int64_t rows, int64_t blk, int64_t nblk) {
+    // the plan's loads, then the first tile's (in flight through the copy's stores)
+    const int64_t first = blk * kWavesC + wave_id();
+    const int64_t ntiles = ceil_div(rows, kTile);
+    LdsCopy<64 * kWavesC, (int)sizeof(Quantizer)> qc;
+    LdsCopy<64 * kWavesC, (int)sizeof(RotLds)> rc;
+    if constexpr (kMode == 0) qc.load(&plan_quantizer(plan));
+    rc.load(&plan_compress_frags(plan));
+    __builtin_amdgcn_sched_barrier(0);
+    f16x8 xa[8], xb[8];
+    load_x_half(in, first, ntiles, rows, xa);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kMode == 0) qc.store(&qz);
+    rc.store(&rl);
+    lds_barrier();
+    load_x_half(in, first + nblk * kWavesC, ntiles, rows, xb);
+    if (kMode == 1 || qz.unit_fast)
+        compress_waves<kMode, kBits, true>(qz, rl, in, dst, y_out, rows, xa, xb, blk, nblk);
+    else
+        compress_waves_general<kMode, kBits>(qz, rl, in, dst, y_out, rows, blk, nblk);
+}
+
+// kPlanned: the quantizer and the rotation fragments come from a plan; otherwise the
 // workgroup builds them from rot and cent.
 template <int kMode, int kBits, class Dst, bool kPlanned>
 __global__ __launch_bounds__(64 * kWavesC) __attribute__((amdgpu_waves_per_eu(2))) void
@@ -490,25 +521,7 @@ tq_compress_mfma_kernel(const uint16_t* __restrict__ in, const float* __restrict
     __shared__ Quantizer qz;
     __shared__ RotLds rl;
     if constexpr (kPlanned) {
-        // the plan's loads, then the first tile's (in flight through the copy's stores)
-        const int64_t first = (int64_t)blockIdx.x * kWavesC + wave_id();
-        const int64_t ntiles = ceil_div(rows, kTile);
-        LdsCopy<64 * kWavesC, (int)sizeof(Quantizer)> qc;
-        LdsCopy<64 * kWavesC, (int)sizeof(RotLds)> rc;
-        if constexpr (kMode == 0) qc.load(&plan_quantizer(plan));
-        rc.load(&plan_compress_frags(plan));
-        __builtin_amdgcn_sched_barrier(0);
-        f16x8 xa[8], xb[8];
-        load_x_half(in, first, ntiles, rows, xa);
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (kMode == 0) qc.store(&qz);
-        rc.store(&rl);
-        lds_barrier();
-        load_x_half(in, first + (int64_t)gridDim.x * kWavesC, ntiles, rows, xb);
-        if (kMode == 1 || qz.unit_fast)
-            compress_waves<kMode, kBits, true>(qz, rl, in, dst, y_out, rows, xa, xb);
-        else
-            compress_waves_general<kMode, kBits>(qz, rl, in, dst, y_out, rows);
+        compress_planned<kMode, kBits>(qz, rl, in, plan, dst, y_out, rows, blockIdx.x, gridDim.x);
         return;
     }
     // The centroids are loaded alone first (behind the chip-wide burst of the other loads
@@ -536,9 +549,29 @@ tq_compress_mfma_kernel(const uint16_t* __restrict__ in, const float* __restrict
     lds_barrier();
     load_x_half(in, first + (int64_t)gridDim.x * kWavesC, ntiles, rows, xb);
     if (kMode == 1 || qz.unit_fast)
-        compress_waves<kMode, kBits, true>(qz, rl, in, dst, y_out, rows, xa, xb);
+        compress_waves<kMode, kBits, true>(qz, rl, in, dst, y_out, rows, xa, xb, blockIdx.x,
+                                           gridDim.x);
     else
-        compress_waves_general<kMode, kBits>(qz, rl, in, dst, y_out, rows);
+        compress_waves_general<kMode, kBits>(qz, rl, in, dst, y_out, rows, blockIdx.x,
+                                             gridDim.x);
+}
+
+// Keys and values of one layer in one launch: even workgroups compress the keys, odd ones the
+// values, each with its own plan, so the two tensors' load ramps and tails overlap on the
+// chip instead of following one another. kKBits / kVBits: the two widths.
+template <int kKBits, int kVBits, class Dst>
+__global__ __launch_bounds__(64 * kWavesC) __attribute__((amdgpu_waves_per_eu(2))) void
+tq_compress_kv_mfma_kernel(const uint16_t* __restrict__ k_in, const uint16_t* __restrict__ v_in,
+                           const TqPlanDev* __restrict__ kplan,
+                           const TqPlanDev* __restrict__ vplan, Dst kdst, Dst vdst,
+                           int64_t rows) {
+    __shared__ Quantizer qz;
+    __shared__ RotLds rl;
+    const int64_t blk = blockIdx.x >> 1, nblk = gridDim.x >> 1;
+    if (blockIdx.x & 1)
+        compress_planned<0, kVBits>(qz, rl, v_in, vplan, vdst, nullptr, rows, blk, nblk);
+    else
+        compress_planned<0, kKBits>(qz, rl, k_in, kplan, kdst, nullptr, rows, blk, nblk);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -820,6 +853,32 @@ __device__ __forceinline__ const RotLds& plan_compress_frags(const TqPlanDev* p)
     return p->comp;
 }
 
+// The planned dequantize of one tensor by workgroup blk of nblk: the tables and fragments are
+// copied from the plan into LDS while the first tile's loads are in flight.
+template <int kBits>
+__device__ __forceinline__ void dequant_planned(DequantLds& t, RotLds& rl,
+                                                const uint8_t* __restrict__ packed,
+                                                const uint16_t* __restrict__ norms,
+                                                const TqPlanDev* __restrict__ plan,
+                                                uint16_t* __restrict__ out, int64_t rows,
+                                                int64_t blk, int64_t nblk) {
+    const int64_t ntiles = ceil_div(rows, kTile);
+    const int64_t stride = nblk * kWavesD;
+    const int64_t tile = blk * kWavesD + wave_id();
+    LdsCopy<64 * kWavesD, (int)sizeof(DequantLds)> tc;
+    LdsCopy<64 * kWavesD, (int)sizeof(RotLds)> rc;
+    tc.load(&plan->dt);
+    rc.load(&plan->deq);
+    __builtin_amdgcn_sched_barrier(0);
+    CodeHalf<kBits> ca, cb;
+    load_code_half<kBits>(packed, norms, tile, ntiles, rows, ca);
+    __builtin_amdgcn_sched_barrier(0);
+    tc.store(&t);
+    rc.store(&rl);
+    lds_barrier();
+    dequant_waves<kBits>(t, rl, packed, norms, out, rows, tile, stride, ntiles, ca, cb);
+}
+
 template <int kBits, bool kPlanned>
 __global__ __launch_bounds__(64 * kWavesD) __attribute__((amdgpu_waves_per_eu(3))) void
 tq_dequant_mfma_kernel(const uint8_t* __restrict__ packed, const uint16_t* __restrict__ norms,
@@ -828,24 +887,13 @@ tq_dequant_mfma_kernel(const uint8_t* __restrict__ packed, const uint16_t* __res
                        int64_t rows) {
     __shared__ DequantLds t;
     __shared__ RotLds rl;
+    if constexpr (kPlanned) {
+        dequant_planned<kBits>(t, rl, packed, norms, plan, out, rows, blockIdx.x, gridDim.x);
+        return;
+    }
     const int64_t ntiles = ceil_div(rows, kTile);
     const int64_t stride = (int64_t)gridDim.x * kWavesD;
     int64_t tile = (int64_t)blockIdx.x * kWavesD + wave_id();
-    if constexpr (kPlanned) {
-        LdsCopy<64 * kWavesD, (int)sizeof(DequantLds)> tc;
-        LdsCopy<64 * kWavesD, (int)sizeof(RotLds)> rc;
-        tc.load(&plan->dt);
-        rc.load(&plan->deq);
-        __builtin_amdgcn_sched_barrier(0);
-        CodeHalf<kBits> ca, cb;
-        load_code_half<kBits>(packed, norms, tile, ntiles, rows, ca);
-        __builtin_amdgcn_sched_barrier(0);
-        tc.store(&t);
-        rc.store(&rl);
-        lds_barrier();
-        dequant_waves<kBits>(t, rl, packed, norms, out, rows, tile, stride, ntiles, ca, cb);
-        return;
-    }
     // Loads go out in the order their data is needed: the centroids, the rotation, then the
     // first tile, which stays in flight through the set-up (whose barriers order LDS only).
     static_assert(kMaxLevels <= 64 * kWavesD, "one centroid per thread");
@@ -866,6 +914,24 @@ tq_dequant_mfma_kernel(const uint8_t* __restrict__ packed, const uint16_t* __res
         lds_barrier();
     }
     dequant_waves<kBits>(t, rl, packed, norms, out, rows, tile, stride, ntiles, ca, cb);
+}
+
+// Keys and values of one layer in one launch: even workgroups dequantize the keys, odd ones
+// the values (as the K+V compress kernel).
+template <int kKBits, int kVBits>
+__global__ __launch_bounds__(64 * kWavesD) __attribute__((amdgpu_waves_per_eu(3))) void
+tq_dequant_kv_mfma_kernel(const uint8_t* __restrict__ k_packed, const uint16_t* __restrict__ k_norms,
+                          const uint8_t* __restrict__ v_packed, const uint16_t* __restrict__ v_norms,
+                          const TqPlanDev* __restrict__ kplan, const TqPlanDev* __restrict__ vplan,
+                          uint16_t* __restrict__ k_out, uint16_t* __restrict__ v_out,
+                          int64_t rows) {
+    __shared__ DequantLds t;
+    __shared__ RotLds rl;
+    const int64_t blk = blockIdx.x >> 1, nblk = gridDim.x >> 1;
+    if (blockIdx.x & 1)
+        dequant_planned<kVBits>(t, rl, v_packed, v_norms, vplan, v_out, rows, blk, nblk);
+    else
+        dequant_planned<kKBits>(t, rl, k_packed, k_norms, kplan, k_out, rows, blk, nblk);
 }
 
 // Build a plan (one workgroup): the quantizer exactly as the compress kernel builds it, both
@@ -1021,6 +1087,54 @@ int launch_dequant(const void* packed_in, const void* norms_in, const float* rot
                            (uint16_t*)output, rows, head_dim, (int64_t)packed_dim_per_head);
     }
     return hipGetLastError();
+}
+
+// Grid of the K+V kernels: one workgroup per CU in all (half per tensor), never more per
+// tensor than gives every wave a tile.
+int mfma_grid_kv(int64_t ntiles, int waves) {
+    const int64_t need = ceil_div(ntiles, waves);
+    const int64_t half = fhip_host::cu_count() >= 2 ? fhip_host::cu_count() / 2 : 1;
+    return 2 * (int)(need < half ? (need > 0 ? need : 1) : half);
+}
+
+// Both tensors in one launch where a K+V kernel exists for the two widths (equal widths of
+// 2, 3, 4 or 8 bits, or 4-bit keys with 2-bit values); false otherwise, nothing launched.
+template <class Dst>
+bool launch_compress_kv(const TqPlanDev* kp, const TqPlanDev* vp, int kbits, int vbits,
+                        const void* kin, const void* vin, Dst kd, Dst vd, int64_t rows,
+                        hipStream_t s) {
+    if (!fhip_host::aligned16(kin) || !fhip_host::aligned16(vin)) return false;
+    auto kern = tq_compress_kv_mfma_kernel<4, 4, Dst>;
+    if (kbits == 4 && vbits == 4) kern = tq_compress_kv_mfma_kernel<4, 4, Dst>;
+    else if (kbits == 3 && vbits == 3) kern = tq_compress_kv_mfma_kernel<3, 3, Dst>;
+    else if (kbits == 2 && vbits == 2) kern = tq_compress_kv_mfma_kernel<2, 2, Dst>;
+    else if (kbits == 8 && vbits == 8) kern = tq_compress_kv_mfma_kernel<8, 8, Dst>;
+    else if (kbits == 4 && vbits == 2) kern = tq_compress_kv_mfma_kernel<4, 2, Dst>;
+    else return false;
+    hipLaunchKernelGGL(kern, dim3(mfma_grid_kv(ceil_div(rows, kTile), kWavesC)),
+                       dim3(64 * kWavesC), 0, s, (const uint16_t*)kin, (const uint16_t*)vin, kp,
+                       vp, kd, vd, rows);
+    return true;
+}
+
+bool launch_dequant_kv(const TqPlanDev* kp, const TqPlanDev* vp, int kbits, int vbits,
+                       const void* kpk, const void* knm, const void* vpk, const void* vnm,
+                       void* kout, void* vout, int64_t rows, hipStream_t s) {
+    if (!fhip_host::aligned16(kpk) || !fhip_host::aligned16(vpk) || !fhip_host::aligned16(kout) ||
+        !fhip_host::aligned16(vout) || (((uintptr_t)knm) & 1u) || (((uintptr_t)vnm) & 1u))
+        return false;
+    auto kern = tq_dequant_kv_mfma_kernel<4, 4>;
+    if (kbits == 4 && vbits == 4) kern = tq_dequant_kv_mfma_kernel<4, 4>;
+    else if (kbits == 3 && vbits == 3) kern = tq_dequant_kv_mfma_kernel<3, 3>;
+    else if (kbits == 2 && vbits == 2) kern = tq_dequant_kv_mfma_kernel<2, 2>;
+    else if (kbits == 8 && vbits == 8) kern = tq_dequant_kv_mfma_kernel<8, 8>;
+    else if (kbits == 4 && vbits == 2) kern = tq_dequant_kv_mfma_kernel<4, 2>;
+    else return false;
+    hipLaunchKernelGGL(kern, dim3(mfma_grid_kv(ceil_div(rows, kTile), kWavesD)),
+                       dim3(64 * kWavesD), 0, s, (const uint8_t*)kpk, (const uint16_t*)knm,
+                       (const uint8_t*)vpk, (const uint16_t*)vnm, kp, vp, (uint16_t*)kout,
+                       (uint16_t*)vout, rows);
+    return true;
 }
 
 }  // namespace
@@ -1236,6 +1350,89 @@ int fhip_launch_tq_dequant_planned(const fhip_tq_plan* plan, const void* packed_
     const TqPlanDev* p = plan->dev;
     return launch_dequant(packed_in, norms_in, p->rot, p->cent, plan->n_levels, output, rows,
                           plan->head_dim, plan->bits, pd, fhip_host::as_stream(stream), p);
+}
+
+// K+V entries: one launch for a layer's keys and values (plans of head_dim 128), falling back
+// to one launch per tensor for width pairs without a K+V kernel.
+int fhip_launch_tq_compress_kv_planned(const fhip_tq_plan* kplan, const fhip_tq_plan* vplan,
+                                       const void* k_input, const void* v_input,
+                                       void* k_packed_out, void* k_norms_out,
+                                       void* v_packed_out, void* v_norms_out, int num_tokens,
+                                       int num_kv_heads, fhip_stream_t stream) {
+    if (!kplan || !vplan || num_tokens < 0 || num_kv_heads < 0) return hipErrorInvalidValue;
+    const int64_t rows = (int64_t)num_tokens * num_kv_heads;
+    if (rows == 0) return hipSuccess;
+    if (!k_input || !v_input || !k_packed_out || !k_norms_out || !v_packed_out || !v_norms_out)
+        return hipErrorInvalidValue;
+    const hipStream_t s = fhip_host::as_stream(stream);
+    const int64_t kpd = ceil_div((int64_t)kplan->head_dim * kplan->bits, 8);
+    const int64_t vpd = ceil_div((int64_t)vplan->head_dim * vplan->bits, 8);
+    FlatDst kd{(uint8_t*)k_packed_out, (uint16_t*)k_norms_out, kpd};
+    FlatDst vd{(uint8_t*)v_packed_out, (uint16_t*)v_norms_out, vpd};
+    if (kplan->head_dim == kHd && vplan->head_dim == kHd &&
+        launch_compress_kv(kplan->dev, vplan->dev, kplan->bits, vplan->bits, k_input, v_input,
+                           kd, vd, rows, s))
+        return hipGetLastError();
+    int r = fhip_launch_tq_compress_planned(kplan, k_input, k_packed_out, k_norms_out,
+                                            num_tokens, num_kv_heads, stream);
+    if (r) return r;
+    return fhip_launch_tq_compress_planned(vplan, v_input, v_packed_out, v_norms_out,
+                                           num_tokens, num_kv_heads, stream);
+}
+
+int fhip_launch_tq_compress_kv_page_ptrs_planned(
+    const fhip_tq_plan* kplan, const fhip_tq_plan* vplan, const void* k_input,
+    const void* v_input, void* const* k_packed_pages, void* const* k_norm_pages,
+    void* const* v_packed_pages, void* const* v_norm_pages, const int32_t* page_ids,
+    int num_pages, int first_pos, int num_tokens, int num_kv_heads, fhip_stream_t stream) {
+    if (!kplan || !vplan || num_tokens < 0 || num_kv_heads <= 0 || first_pos < 0 ||
+        num_pages < 0)
+        return hipErrorInvalidValue;
+    const int64_t rows = (int64_t)num_tokens * num_kv_heads;
+    if (rows == 0) return hipSuccess;
+    if (!k_input || !v_input || !k_packed_pages || !k_norm_pages || !v_packed_pages ||
+        !v_norm_pages || !page_ids)
+        return hipErrorInvalidValue;
+    const hipStream_t s = fhip_host::as_stream(stream);
+    const int64_t kpd = ceil_div((int64_t)kplan->head_dim * kplan->bits, 8);
+    const int64_t vpd = ceil_div((int64_t)vplan->head_dim * vplan->bits, 8);
+    PtrPageDst kd{(uint8_t* const*)k_packed_pages, (uint8_t* const*)k_norm_pages, page_ids,
+                  first_pos, num_kv_heads, num_pages, kpd};
+    PtrPageDst vd{(uint8_t* const*)v_packed_pages, (uint8_t* const*)v_norm_pages, page_ids,
+                  first_pos, num_kv_heads, num_pages, vpd};
+    if (kplan->head_dim == kHd && vplan->head_dim == kHd &&
+        launch_compress_kv(kplan->dev, vplan->dev, kplan->bits, vplan->bits, k_input, v_input,
+                           kd, vd, rows, s))
+        return hipGetLastError();
+    int r = fhip_launch_tq_compress_page_ptrs_planned(kplan, k_input, k_packed_pages,
+                                                      k_norm_pages, page_ids, num_pages,
+                                                      first_pos, num_tokens, num_kv_heads, stream);
+    if (r) return r;
+    return fhip_launch_tq_compress_page_ptrs_planned(vplan, v_input, v_packed_pages,
+                                                     v_norm_pages, page_ids, num_pages, first_pos,
+                                                     num_tokens, num_kv_heads, stream);
+}
+
+int fhip_launch_tq_dequant_kv_planned(const fhip_tq_plan* kplan, const fhip_tq_plan* vplan,
+                                      const void* k_packed_in, const void* k_norms_in,
+                                      const void* v_packed_in, const void* v_norms_in,
+                                      void* k_output, void* v_output, int num_tokens,
+                                      int num_kv_heads, fhip_stream_t stream) {
+    if (!kplan || !vplan || num_tokens < 0 || num_kv_heads < 0) return hipErrorInvalidValue;
+    const int64_t rows = (int64_t)num_tokens * num_kv_heads;
+    if (rows == 0) return hipSuccess;
+    if (!k_packed_in || !k_norms_in || !v_packed_in || !v_norms_in || !k_output || !v_output)
+        return hipErrorInvalidValue;
+    if (kplan->head_dim == kHd && vplan->head_dim == kHd &&
+        launch_dequant_kv(kplan->dev, vplan->dev, kplan->bits, vplan->bits, k_packed_in,
+                          k_norms_in, v_packed_in, v_norms_in, k_output, v_output, rows,
+                          fhip_host::as_stream(stream)))
+        return hipGetLastError();
+    int r = fhip_launch_tq_dequant_planned(kplan, k_packed_in, k_norms_in, k_output, num_tokens,
+                                           num_kv_heads, stream);
+    if (r) return r;
+    return fhip_launch_tq_dequant_planned(vplan, v_packed_in, v_norms_in, v_output, num_tokens,
+                                          num_kv_heads, stream);
 }
 
 }  // extern "C"

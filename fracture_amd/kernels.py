@@ -326,6 +326,42 @@ def tq_dequant_planned(plan: TqPlan, packed: torch.Tensor, norms: torch.Tensor,
                                             _stream()), "tq_dequant_planned")
 
 
+def tq_compress_kv_planned(kplan: TqPlan, vplan: TqPlan, k: torch.Tensor, v: torch.Tensor,
+                           k_packed: torch.Tensor, k_norms: torch.Tensor,
+                           v_packed: torch.Tensor, v_norms: torch.Tensor) -> None:
+    """A layer's keys and values [N, kvh, hd] fp16 compressed in one launch."""
+    _dev(k, v, k_packed, k_norms, v_packed, v_norms)
+    _need(k.dtype == torch.float16 and k.dim() == 3 and k.shape == v.shape and
+          v.dtype == torch.float16 and k.shape[2] == kplan.head_dim == vplan.head_dim,
+          "tq_compress_kv_planned: k, v [N, kv_heads, hd] fp16")
+    N, H = k.shape[0], k.shape[1]
+    _need(k_packed.dtype == torch.uint8 and k_packed.numel() >= N * H * kplan.packed_dim, "k_packed")
+    _need(v_packed.dtype == torch.uint8 and v_packed.numel() >= N * H * vplan.packed_dim, "v_packed")
+    _need(k_norms.dtype == torch.float16 and k_norms.numel() >= N * H, "k_norms")
+    _need(v_norms.dtype == torch.float16 and v_norms.numel() >= N * H, "v_norms")
+    _ok(_L().fhip_launch_tq_compress_kv_planned(kplan._h, vplan._h, _p(k), _p(v), _p(k_packed),
+                                                _p(k_norms), _p(v_packed), _p(v_norms), N, H,
+                                                _stream()), "tq_compress_kv_planned")
+
+
+def tq_dequant_kv_planned(kplan: TqPlan, vplan: TqPlan, k_packed: torch.Tensor,
+                          k_norms: torch.Tensor, v_packed: torch.Tensor, v_norms: torch.Tensor,
+                          k_out: torch.Tensor, v_out: torch.Tensor) -> None:
+    """A layer's keys and values dequantized in one launch: outputs [N, kvh, hd] fp16."""
+    _dev(k_packed, k_norms, v_packed, v_norms, k_out, v_out)
+    _need(k_out.dtype == torch.float16 and k_out.dim() == 3 and k_out.shape == v_out.shape and
+          v_out.dtype == torch.float16 and k_out.shape[2] == kplan.head_dim == vplan.head_dim,
+          "tq_dequant_kv_planned: outputs [N, kvh, hd] fp16")
+    N, H = k_out.shape[0], k_out.shape[1]
+    _need(k_packed.dtype == torch.uint8 and k_packed.numel() >= N * H * kplan.packed_dim, "k_packed")
+    _need(v_packed.dtype == torch.uint8 and v_packed.numel() >= N * H * vplan.packed_dim, "v_packed")
+    _need(k_norms.dtype == torch.float16 and k_norms.numel() >= N * H, "k_norms")
+    _need(v_norms.dtype == torch.float16 and v_norms.numel() >= N * H, "v_norms")
+    _ok(_L().fhip_launch_tq_dequant_kv_planned(kplan._h, vplan._h, _p(k_packed), _p(k_norms),
+                                               _p(v_packed), _p(v_norms), _p(k_out), _p(v_out),
+                                               N, H, _stream()), "tq_dequant_kv_planned")
+
+
 def attention_workspace(batch: int, qh: int, hd: int, max_blocks: int, device="cuda"):
     n = int(_L().fhip_attention_tq_workspace_bytes(batch, qh, hd, max_blocks))
     return torch.empty(max(n, 16), dtype=torch.uint8, device=device)

@@ -302,6 +302,28 @@ int fhip_launch_tq_dequant_planned(const fhip_tq_plan* plan, const void* packed_
                                    const void* norms_in, void* output, int num_tokens,
                                    int num_kv_heads, fhip_stream_t stream);
 
+/* One layer's keys and values in one launch (append_kv's two turboquant_compress calls,
+ * quantized_paged_kv_cache.rs:417-497, and the two decompresses of a layer): half the
+ * workgroups take the keys, half the values, each with its own plan, so the two tensors'
+ * load ramps and tails overlap. Bytes and outputs are those of the single-tensor planned
+ * launchers. Width pairs without a K+V kernel (anything but equal widths of 2, 3, 4 or 8 bits,
+ * or 4-bit keys with 2-bit values) run as two launches. */
+int fhip_launch_tq_compress_kv_planned(const fhip_tq_plan* kplan, const fhip_tq_plan* vplan,
+                                       const void* k_input, const void* v_input,
+                                       void* k_packed_out, void* k_norms_out,
+                                       void* v_packed_out, void* v_norms_out, int num_tokens,
+                                       int num_kv_heads, fhip_stream_t stream);
+int fhip_launch_tq_compress_kv_page_ptrs_planned(
+    const fhip_tq_plan* kplan, const fhip_tq_plan* vplan, const void* k_input,
+    const void* v_input, void* const* k_packed_pages, void* const* k_norm_pages,
+    void* const* v_packed_pages, void* const* v_norm_pages, const int32_t* page_ids,
+    int num_pages, int first_pos, int num_tokens, int num_kv_heads, fhip_stream_t stream);
+int fhip_launch_tq_dequant_kv_planned(const fhip_tq_plan* kplan, const fhip_tq_plan* vplan,
+                                      const void* k_packed_in, const void* k_norms_in,
+                                      const void* v_packed_in, const void* v_norms_in,
+                                      void* k_output, void* v_output, int num_tokens,
+                                      int num_kv_heads, fhip_stream_t stream);
+
 /* Batched decode attention over a TurboQuant page pool: one query token per sequence,
  * q [B, qh, hd] fp16, block_table [B, max_blocks] int32 (physical page ids), seq_lens [B]
  * int32; pages in contiguous pools (strides in bytes between pages, each at least one page:

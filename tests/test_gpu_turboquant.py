@@ -381,3 +381,90 @@ def test_planned_page_writer_equals_unplanned(dev):
         page, slot = page_ids[pos // 16], pos % 16
         assert np.array_equal(pools[1][0][page, slot], want_p[t]), f"token {t}"
         assert np.array_equal(pools[1][1][page, slot], yn.reshape(T, H)[t].view(np.uint16))
+
+
+# ---------------------------------------------------------------------------------------
+# K+V launchers: keys and values of a layer in one launch, each with its own plan.
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("kb,vb", [(4, 4), (3, 3), (2, 2), (8, 8), (4, 2), (3, 4)])
+def test_kv_planned_compress_vs_oracle(dev, kb, vb):
+    """Both tensors' bytes equal the oracle's quantize-pack of the kernel's own rotated vectors
+    (each with its own rotation and codebook) and the single-tensor planned launcher; (3, 4)
+    has no K+V kernel and runs as two launches."""
+    rng = np.random.default_rng(kb * 10 + vb)
+    N, H = 301, 8  # a ragged last tile
+    x = {"k": kv(rng, N, H, 128), "v": kv(rng, N, H, 128)}
+    rot = {"k": tq.rotation_matrix(128, 42), "v": tq.rotation_matrix(128, 542)}
+    cent = {"k": tq.codebook(128, kb)[0], "v": tq.codebook(128, vb)[0]}
+    bits = {"k": kb, "v": vb}
+    plans = {s: K.TqPlan(dev_t(rot[s], dev), dev_t(cent[s], dev), bits[s]) for s in "kv"}
+    out = {s: (torch.full((N, H * K.packed_dim(128, bits[s])), 0xAB, dtype=torch.uint8,
+                          device=dev),
+               torch.empty((N, H), dtype=torch.float16, device=dev)) for s in "kv"}
+    K.tq_compress_kv_planned(plans["k"], plans["v"], dev_t(x["k"], dev), dev_t(x["v"], dev),
+                             out["k"][0], out["k"][1], out["v"][0], out["v"][1])
+    torch.cuda.synchronize()
+    for s in "kv":
+        y, yn = rotate(x[s], rot[s], dev)
+        got = out[s][0].cpu().numpy()
+        assert np.array_equal(got.reshape(N * H, -1), oracle.tq_quantize_pack(y, cent[s], bits[s])), s
+        assert np.array_equal(out[s][1].cpu().numpy().reshape(-1).view(np.uint16), yn.view(np.uint16)), s
+        single = torch.empty_like(out[s][0]), torch.empty_like(out[s][1])
+        K.tq_compress_planned(plans[s], dev_t(x[s], dev), *single)
+        torch.cuda.synchronize()
+        assert torch.equal(single[0], out[s][0]) and torch.equal(single[1].view(torch.int16),
+                                                                 out[s][1].view(torch.int16)), s
+
+
+@pytest.mark.parametrize("kb,vb", [(4, 4), (3, 3), (4, 2), (3, 4)])
+def test_kv_planned_dequant_vs_oracle(dev, kb, vb):
+    rng = np.random.default_rng(kb * 3 + vb)
+    N, H = 200, 8
+    rot = {"k": tq.rotation_matrix(128, 7), "v": tq.rotation_matrix(128, 507)}
+    cent = {"k": tq.codebook(128, kb)[0], "v": tq.codebook(128, vb)[0]}
+    bits = {"k": kb, "v": vb}
+    pk = {s: compress(kv(rng, N, H, 128), rot[s], cent[s], bits[s], dev) for s in "kv"}
+    plans = {s: K.TqPlan(dev_t(rot[s], dev), dev_t(cent[s], dev), bits[s]) for s in "kv"}
+    tin = {s: (dev_t(pk[s][0], dev), dev_t(pk[s][1], dev)) for s in "kv"}
+    got = {s: torch.empty((N, H, 128), dtype=torch.float16, device=dev) for s in "kv"}
+    K.tq_dequant_kv_planned(plans["k"], plans["v"], *tin["k"], *tin["v"], got["k"], got["v"])
+    torch.cuda.synchronize()
+    for s in "kv":
+        want = torch.empty_like(got[s])
+        K.tq_dequant_planned(plans[s], *tin[s], want)
+        torch.cuda.synchronize()
+        assert torch.equal(got[s].view(torch.int16), want.view(torch.int16)), s
+        ref = oracle.tq_dequant(pk[s][0].reshape(N * H, -1), pk[s][1].reshape(-1), rot[s],
+                                cent[s], bits[s], 128)
+        assert_close(got[s].cpu().numpy().reshape(-1, 128).astype(np.float32),
+                     ref.astype(np.float32), 1e-3, 1e-3, f"K+V dequantize ({s}) vs oracle")
+
+
+def test_kv_planned_layer_scale(dev):
+    """The K+V launch at one layer of Llama-3.1-8B (32768 tokens x 8 kv heads, 4 bits): bytes
+    equal the per-tensor planned launches, which the oracle pins above."""
+    rng = np.random.default_rng(77)
+    N, H = 32768, 8
+    xs = [(rng.standard_normal((N, H, 128), dtype=np.float32) *
+           np.exp(rng.normal(0, 0.5, (N, 1, 1))).astype(np.float32)).astype(np.float16)
+          for _ in range(2)]
+    rots = [tq.rotation_matrix(128, 42), tq.rotation_matrix(128, 542)]
+    cent = tq.codebook(128, 4)[0]
+    plans = [K.TqPlan(dev_t(r, dev), dev_t(cent, dev), 4) for r in rots]
+    tx = [dev_t(x, dev) for x in xs]
+    fused = [(torch.empty((N, H * 64), dtype=torch.uint8, device=dev),
+              torch.empty((N, H), dtype=torch.float16, device=dev)) for _ in range(2)]
+    K.tq_compress_kv_planned(plans[0], plans[1], tx[0], tx[1], *fused[0], *fused[1])
+    for i in range(2):
+        single = torch.empty_like(fused[i][0]), torch.empty_like(fused[i][1])
+        K.tq_compress_planned(plans[i], tx[i], *single)
+        torch.cuda.synchronize()
+        assert torch.equal(single[0], fused[i][0])
+        assert torch.equal(single[1].view(torch.int16), fused[i][1].view(torch.int16))
+    outs = [torch.empty((N, H, 128), dtype=torch.float16, device=dev) for _ in range(2)]
+    K.tq_dequant_kv_planned(plans[0], plans[1], *fused[0], *fused[1], outs[0], outs[1])
+    for i in range(2):
+        want = torch.empty_like(outs[i])
+        K.tq_dequant_planned(plans[i], *fused[i], want)
+        torch.cuda.synchronize()
+        assert torch.equal(want.view(torch.int16), outs[i].view(torch.int16))
