@@ -507,6 +507,55 @@ __device__ __forceinline__ uint32_t hi_lo_pair(float v, float& hi_f) {
 __device__ __forceinline__ float ror8(float v) {  // lane n of each 16-lane row gets lane n^8
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, true));
 }
+// Row-local DPP moves (rotations within each 16-lane row: lane n takes lane (n - kRor) mod 16)
+// that write only the lanes of the 4-lane banks in kBank; other lanes keep `old`.
+template <int kRor, int kBank>
+__device__ __forceinline__ float dpp_into(float old, float src) {
+    constexpr int kCtrl = kRor == 0 ? 0xE4 : 0x120 + kRor;  // identity quad_perm, or row_ror
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(src),
+                                                      kCtrl, 0xF, kBank, false));
+}
+template <int kRor, int kBank>
+__device__ __forceinline__ uint32_t dpp_into_u(uint32_t old, uint32_t src) {
+    constexpr int kCtrl = kRor == 0 ? 0xE4 : 0x120 + kRor;
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)src, kCtrl, 0xF, kBank, false);
+}
+// acc += 2^-12 * (lane (n - kRor) mod 16's src), in the lanes of bank kBank only
+// (v_fmac_f32_dpp; `c` holds 2^-12).
+template <int kRor, int kBank>
+__device__ __forceinline__ void dpp_fmac_lo(float& acc, float src, float c) {
+    static_assert(kBank == 1 || kBank == 2 || kBank == 4 || kBank == 8, "one bank");
+#define FHIP_FMAC_DPP(CTRL, BANK) \
+    asm("v_fmac_f32_dpp %0, %1, %2 " CTRL " row_mask:0xf bank_mask:" BANK : "+v"(acc) : "v"(src), "v"(c))
+    if constexpr (kBank == 1) {
+        static_assert(kRor == 8, "tile 0");
+        FHIP_FMAC_DPP("row_ror:8", "0x1");
+    } else if constexpr (kBank == 2) {
+        static_assert(kRor == 12, "tile 1");
+        FHIP_FMAC_DPP("row_ror:12", "0x2");
+    } else if constexpr (kBank == 4) {
+        static_assert(kRor == 0, "tile 2");
+        FHIP_FMAC_DPP("quad_perm:[0,1,2,3]", "0x4");
+    } else {
+        static_assert(kRor == 4, "tile 3");
+        FHIP_FMAC_DPP("row_ror:4", "0x8");
+    }
+#undef FHIP_FMAC_DPP
+}
+// Max / sum over the 4 banks of each row (lanes n, n ^ 4, n ^ 8, n ^ 12 hold one head).
+// A DPP read of a VGPR that a VALU instruction has just written needs two wait states, which
+// the compiler does not insert for inline asm: each DPP instruction here follows an s_nop 1.
+__device__ __forceinline__ float bank_max(float v) {
+    asm("s_nop 1\n\tv_max_f32_dpp %0, %0, %0 row_ror:4 row_mask:0xf bank_mask:0xf" : "+v"(v));
+    asm("s_nop 1\n\tv_max_f32_dpp %0, %0, %0 row_ror:8 row_mask:0xf bank_mask:0xf" : "+v"(v));
+    return v;
+}
+__device__ __forceinline__ float bank_sum(float v) {
+    asm("s_nop 1\n\tv_add_f32_dpp %0, %0, %0 row_ror:4 row_mask:0xf bank_mask:0xf" : "+v"(v));
+    asm("s_nop 1\n\tv_add_f32_dpp %0, %0, %0 row_ror:8 row_mask:0xf bank_mask:0xf" : "+v"(v));
+    return v;
+}
+
 // 8 * (byte kByte of x), the byte offset of a pair-table entry, in one v_lshlrev_b32_sdwa.
 // Written as asm: the compiler turns the extract-and-shift into two instructions for most
 // byte positions.
@@ -671,7 +720,30 @@ __device__ __forceinline__ void read_v_codes(const uint32_t (&seg)[4], v2i_t (&t
         : "memory");
 }
 
-template <class Pages>
+// kG4 score compaction: tile kPt's head-h score D[h] + 2^-12 D[8 + h] (MFMA columns h and 8 + h
+// of the lane's row) into lane 4 kPt + h, elements e = 0..3; the other banks keep theirs.
+template <int kPt>
+__device__ __forceinline__ void compact_scores(float (&S)[4], const f32x4_t& d, float c12) {
+    constexpr int kBank = 1 << kPt;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        S[e] = dpp_into<(4 * kPt) & 15, kBank>(S[e], d[e]);
+        dpp_fmac_lo<(4 * kPt + 8) & 15, kBank>(S[e], d[e], c12);
+    }
+}
+// kG4 PV operand of tile kPt: column h (lanes h < 4) takes (w_hi, 0) and column 8 + h takes
+// (w_lo', w_hi) of lane 4 kPt + h; banks 1 and 3 are not written (they stay 0).
+template <int kPt>
+__device__ __forceinline__ void expand_weights(uint32_t (&b)[4], const uint32_t (&x)[4],
+                                               const uint32_t (&y)[4]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        b[e] = dpp_into_u<(16 - 4 * kPt) & 15, 0x1>(b[e], x[e]);
+        b[e] = dpp_into_u<(24 - 4 * kPt) & 15, 0x4>(b[e], y[e]);
+    }
+}
+
+template <class Pages, bool kG4>
 __global__ __launch_bounds__(64 * kWavesM) __attribute__((amdgpu_waves_per_eu(3))) void
 tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
                     const float* __restrict__ kcent, const float* __restrict__ vcent, int qh,
@@ -688,6 +760,7 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     __shared__ __attribute__((aligned(16))) uint8_t vbuf[kWavesM][2][kChunkM * 64];  // by chunk parity
     __shared__ __attribute__((aligned(16))) float2 nbuf[kWavesM][kChunkM];  // (knorm, vnorm)
     __shared__ PageAddrs pagebuf[kWavesM][kSplitPages];  // the wave's split pages
+    __shared__ int waves_done;  // waves that have left their state for the merge
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, rg = lane >> 4;  // MFMA column / row group
@@ -717,6 +790,7 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
         const uint32_t vh = hi_lo_pair(vcent[b >> 4], hf), vl = hi_lo_pair(vcent[b & 15], hf);
         pk[b] = u32x2{kh, kl};
         pv[b] = u32x2{vl, vh};
+        if (b == 0) waves_done = 0;
     }
     __syncthreads();
 
@@ -797,6 +871,17 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
         vseg[sg] = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)(
             vb + 64 * srow + 16 * (sg ^ sw));
 
+    // kG4 (at most 4 query heads per kv head): scores, probabilities and weights are held
+    // compactly, lane (n, rg) with n = 4 pt + h holding head h's 4 positions 16rg + 4e + pt of
+    // tile pt (one distinct value per lane and element, where the MFMA layout repeats each
+    // four times); the tiles' weights are moved back into the PV operand layout per tile.
+    // Norm records are stored in that order (nb index 16 rg + 4 pt + e), so a lane's four come
+    // in two 16-byte reads.
+    const int ptc = n >> 2;  // kG4: the lane's position tile
+    const int nb_idx = kG4 ? (lane & 0x30) | ((lane & 3) << 2) | ((lane >> 2) & 3) : lane;
+    const float c12 = 1.0f / 4096.0f;
+    uint32_t awz[4] = {0u, 0u, 0u, 0u};  // kG4 PV operand: banks 1 and 3 (heads 4-7) stay 0
+
     for (int t0 = t_begin, par = 0; t0 < t_end; t0 += kChunkM, par ^= 1) {
         const int tn = t0 + kChunkM;  // next chunk
         const int jn = (tn - t_begin) >> 4;  // its first split page
@@ -804,7 +889,8 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
         const bool full = pmask == 0xfu && tn <= t_end;
 
         // ---- QK: 4 tiles x 8 steps, K codes from this wave's DMA buffer
-        float sc[4][4];  // [pt][e]: position 16rg + 4e + pt, head n & 7
+        float sc[4][4];  // !kG4 [pt][e]: position 16rg + 4e + pt, head n & 7
+        float scc[4];    // kG4 [e]: position 16rg + 4e + ptc, head n & 3
         // all loads of this chunk are in (the V copies included)
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         const u32x4 kcs[4] = {kreg[0], kreg[1], kreg[2], kreg[3]};
@@ -831,15 +917,25 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
                     __builtin_bit_cast(f16x8_t, u32x4{bq[s8][0], bq[s8][1], bq[s8][2], bq[s8][3]}),
                     d, 0, 0, 0);
                 if ((t & 7) == 7) {
+                    if constexpr (kG4) {
+                        // tile pt's head-h score D[h] + 2^-12 D[8 + h] into lanes 4 pt + h
+                        switch (t >> 3) {
+                            case 0: compact_scores<0>(scc, d, c12); break;
+                            case 1: compact_scores<1>(scc, d, c12); break;
+                            case 2: compact_scores<2>(scc, d, c12); break;
+                            default: compact_scores<3>(scc, d, c12); break;
+                        }
+                    } else {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        // fma(ror8(d), cb, d * ca) with the row rotation folded into the fmac
-                        // (the multiply reads d first, after the MFMA result is ready)
-                        float v = d[e] * ca;
-                        asm("v_fmac_f32_dpp %0, %1, %2 row_ror:8 row_mask:0xf bank_mask:0xf bound_ctrl:1"
-                            : "+v"(v)
-                            : "v"(d[e]), "v"(cb));
-                        sc[t >> 3][e] = v;
+                        for (int e = 0; e < 4; ++e) {
+                            // fma(ror8(d), cb, d * ca) with the row rotation folded into the
+                            // fmac (the multiply reads d first, after the MFMA result is ready)
+                            float v = d[e] * ca;
+                            asm("v_fmac_f32_dpp %0, %1, %2 row_ror:8 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+                                : "+v"(v)
+                                : "v"(d[e]), "v"(cb));
+                            sc[t >> 3][e] = v;
+                        }
                     }
                     d = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
                 }
@@ -849,68 +945,111 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
         }
         // ---- K norms; then the K and norm registers are free: all loads of the next chunk,
         // its V codes into the other V buffer
-        nb[lane] = nreg.pack();
+        nb[nb_idx] = nreg.pack();
         uint8_t* vnext = vb + (par ^ 1) * (kChunkM * 64);
         if (tn < t_end) {
             dma_v(pages, jn, v_lane_off, vnext, lane);
             nreg = load_norms(pages, jn, pmask_n, tn, t_end, kvh, g, lane);
             load_k(pages, jn, kvh, g, lane, kreg);
         }
-        float kn[16], vn[16];  // positions 16rg + j
+        float m_new, alpha;
+        uint32_t aw[4][4];  // !kG4 [pt][e]
+        uint32_t xw[4], yw[4];  // kG4: (w_hi, 0) and (w_lo', w_hi) of the lane's 4 weights
+        if constexpr (kG4) {
+            const f32x4_t n0 = *(const f32x4_t*)&nb[16 * rg + 4 * ptc];
+            const f32x4_t n1 = *(const f32x4_t*)&nb[16 * rg + 4 * ptc + 2];
+            const float kn[4] = {n0[0], n0[2], n1[0], n1[2]};
+            const float vn[4] = {n0[1], n0[3], n1[1], n1[3]};
 #pragma unroll
-        for (int j2 = 0; j2 < 8; ++j2) {
-            const f32x4_t v = *(const f32x4_t*)&nb[16 * rg + 2 * j2];
-            kn[2 * j2] = v[0];
-            vn[2 * j2] = v[1];
-            kn[2 * j2 + 1] = v[2];
-            vn[2 * j2 + 1] = v[3];
-        }
+            for (int e = 0; e < 4; ++e) scc[e] *= kn[e];
+            if (!full) {
+                const bool row_ok = (pmask >> rg) & 1u;
 #pragma unroll
-        for (int pt = 0; pt < 4; ++pt)
+                for (int e = 0; e < 4; ++e)
+                    if (!(row_ok && t0 + 16 * rg + 4 * e + ptc < t_end)) scc[e] = -__builtin_inff();
+            }
+            float cmax = fmaxf(fmaxf(scc[0], scc[1]), fmaxf(scc[2], scc[3]));
+            cmax = bank_max(cmax);
+            cmax = fmaxf(cmax, xrow(bp16, cmax));
+            cmax = fmaxf(cmax, xrow(bp32, cmax));
+            m_new = fmaxf(m_run, cmax);
+            alpha = m_run == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+            float psum = 0.0f;
+            const float mref = m_new == -__builtin_inff() ? 0.0f : m_new;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) sc[pt][e] *= kn[4 * e + pt];
-        if (!full) {
-            const bool row_ok = (pmask >> rg) & 1u;
+            for (int e = 0; e < 4; ++e) {
+                const float pr = __builtin_amdgcn_exp2f(scc[e] - mref);
+                psum += pr;
+                const float w = pr * vn[e];
+                // w_hi = w rounded toward zero; lo' = f16(2^12 (w - w_hi)) in place of r.lo
+                uint32_t r = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(w, w));
+                xw[e] = r & 0xffffu;
+                asm("v_fma_mixlo_f16 %0, %0, %1, %2 op_sel_hi:[1,0,0]"
+                    : "+v"(r)
+                    : "v"(-4096.0f), "v"(w * 4096.0f));
+                yw[e] = r;
+            }
+            psum = bank_sum(psum);
+            psum += xrow(bp16, psum);
+            psum += xrow(bp32, psum);
+            l_run = l_run * alpha + psum;
+        } else {
+            float kn[16], vn[16];  // positions 16rg + j
+#pragma unroll
+            for (int j2 = 0; j2 < 8; ++j2) {
+                const f32x4_t v = *(const f32x4_t*)&nb[16 * rg + 2 * j2];
+                kn[2 * j2] = v[0];
+                vn[2 * j2] = v[1];
+                kn[2 * j2 + 1] = v[2];
+                vn[2 * j2 + 1] = v[3];
+            }
 #pragma unroll
             for (int pt = 0; pt < 4; ++pt)
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (!(row_ok && t0 + 16 * rg + 4 * e + pt < t_end)) sc[pt][e] = -__builtin_inff();
-        }
-        float cmax = -__builtin_inff();
+                for (int e = 0; e < 4; ++e) sc[pt][e] *= kn[4 * e + pt];
+            if (!full) {
+                const bool row_ok = (pmask >> rg) & 1u;
 #pragma unroll
-        for (int pt = 0; pt < 4; ++pt)
+                for (int pt = 0; pt < 4; ++pt)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) cmax = fmaxf(cmax, sc[pt][e]);
-        cmax = fmaxf(cmax, xrow(bp16, cmax));
-        cmax = fmaxf(cmax, xrow(bp32, cmax));
-        const float m_new = fmaxf(m_run, cmax);
-        const float alpha =
-            m_run == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-        // ---- probabilities, weights, A operands of PV
-        uint32_t aw[4][4];  // [pt][e]
-        float psum = 0.0f;
-        const float mref = m_new == -__builtin_inff() ? 0.0f : m_new;
-#pragma unroll
-        for (int pt = 0; pt < 4; ++pt) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float pr = __builtin_amdgcn_exp2f(sc[pt][e] - mref);
-                psum += pr;
-                const float w = pr * vn[4 * e + pt];
-                uint32_t r = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(w, w));
-                // in place: written in C, the compiler merges the halves with an extra v_bfi
-                asm("v_fma_mixlo_f16 %0, %0, %1, %2 op_sel_hi:[1,0,0]"
-                    : "+v"(r)
-                    : "v"(wb), "v"(w * wc));
-                aw[pt][e] = r & hmask;
+                    for (int e = 0; e < 4; ++e)
+                        if (!(row_ok && t0 + 16 * rg + 4 * e + pt < t_end)) sc[pt][e] = -__builtin_inff();
             }
+            float cmax = -__builtin_inff();
+#pragma unroll
+            for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) cmax = fmaxf(cmax, sc[pt][e]);
+            cmax = fmaxf(cmax, xrow(bp16, cmax));
+            cmax = fmaxf(cmax, xrow(bp32, cmax));
+            m_new = fmaxf(m_run, cmax);
+            alpha = m_run == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+            // ---- probabilities, weights, B operands of PV
+            float psum = 0.0f;
+            const float mref = m_new == -__builtin_inff() ? 0.0f : m_new;
+#pragma unroll
+            for (int pt = 0; pt < 4; ++pt) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float pr = __builtin_amdgcn_exp2f(sc[pt][e] - mref);
+                    psum += pr;
+                    const float w = pr * vn[4 * e + pt];
+                    uint32_t r = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(w, w));
+                    // in place: written in C, the compiler merges the halves with an extra v_bfi
+                    asm("v_fma_mixlo_f16 %0, %0, %1, %2 op_sel_hi:[1,0,0]"
+                        : "+v"(r)
+                        : "v"(wb), "v"(w * wc));
+                    aw[pt][e] = r & hmask;
+                }
+            }
+            psum += xrow(bp16, psum);
+            psum += xrow(bp32, psum);
+            l_run = l_run * alpha + psum;
         }
-        psum += xrow(bp16, psum);
-        psum += xrow(bp32, psum);
-        l_run = l_run * alpha + psum;
-        // rescale the accumulators when some head's max moved (each lane holds its own head's)
-        const bool moved_any = __ballot((n < G) && (rg == 0) && (m_new > m_run)) != 0;
+        // rescale the accumulators when some head's max moved (each lane's alpha is that of
+        // its accumulator slot's head)
+        const bool moved_any =
+            __ballot((n < G) && (!kG4 || n < 4) && (rg == 0) && (m_new > m_run)) != 0;
         if (moved_any) {
 #pragma unroll
             for (int c = 0; c < 8; ++c)
@@ -945,10 +1084,21 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
             for (int t = 0; t < 32; ++t) {
                 if (t + kAheadPv < 32) ahead[(t + kAheadPv) % (kAheadPv + 1)] = pv_b(t + kAheadPv);
                 const int pt = t >> 3, c = t & 7;
+                if constexpr (kG4) {
+                    if (c == 0) {  // tile pt's weights into the operand layout
+                        switch (pt) {
+                            case 0: expand_weights<0>(awz, xw, yw); break;
+                            case 1: expand_weights<1>(awz, xw, yw); break;
+                            case 2: expand_weights<2>(awz, xw, yw); break;
+                            default: expand_weights<3>(awz, xw, yw); break;
+                        }
+                    }
+                }
+                const u32x4 bw = kG4 ? u32x4{awz[0], awz[1], awz[2], awz[3]}
+                                     : u32x4{aw[pt][0], aw[pt][1], aw[pt][2], aw[pt][3]};
                 acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                     __builtin_bit_cast(f16x8_t, ahead[t % (kAheadPv + 1)]),
-                    __builtin_bit_cast(f16x8_t, u32x4{aw[pt][0], aw[pt][1], aw[pt][2], aw[pt][3]}),
-                    acc[c], 0, 0, 0);
+                    __builtin_bit_cast(f16x8_t, bw), acc[c], 0, 0, 0);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -962,43 +1112,67 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
 
     // ---- merge the workgroup's splits into the block's partial. Each wave leaves its state
     // in its own V buffer: acc[h][d] = slot h (hi) + 2^-12 slot 8 + h (lo'), lanes n and n ^ 8,
-    // then m (log2 units) and l per head. Each output (h, d) then sums the waves in wave order,
-    // weighted by exp2(m_w - max m) (0 for a wave with m = -inf).
+    // then m (log2 units) and l per head, and counts itself done; the last wave to finish
+    // merges (no barrier: the others leave at once and free their slots). Each output (h, d)
+    // sums the waves in wave order, weighted by exp2(m_w - max m) (0 for a wave with
+    // m = -inf), whichever wave merges.
+    // Head rows are kStRow floats apart (144: the 16 writing lanes of a 16-byte store, 4 heads
+    // x 4 row groups, land in distinct banks); a lane's 4 values of dim tile c are dims
+    // 16c + 4rg + 0..3 (element e holds dim e ^ 1), one 16-byte store.
+    constexpr int kStRow = hd + 16;
+    constexpr int kStM = kMaxG * kStRow, kStL = kStM + kMaxG;
     float* st = (float*)vbuf[wave][0];
-    static_assert(sizeof(vbuf[0]) >= (kMaxG * hd + 2 * kMaxG) * sizeof(float), "merge state");
+    static_assert(sizeof(vbuf[0]) >= (kStL + kMaxG) * sizeof(float), "merge state");
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
+        f32x4_t v;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float v = fmaf(ror8(acc[c][e]), 1.0f / 4096.0f, acc[c][e]);
-            if (n < G) st[n * hd + 16 * c + ((4 * rg + e) ^ 1)] = v;
-        }
+        for (int e = 0; e < 4; ++e) v[e ^ 1] = fmaf(ror8(acc[c][e]), 1.0f / 4096.0f, acc[c][e]);
+        if (n < G) *(f32x4_t*)&st[n * kStRow + 16 * c + 4 * rg] = v;
     }
     if (n < G && rg == 0) {
-        st[kMaxG * hd + n] = m_run;
-        st[kMaxG * hd + kMaxG + n] = l_run;
+        st[kStM + n] = m_run;
+        st[kStL + n] = l_run;
     }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < G * hd; idx += 64 * kWavesM) {
-        const int h = idx / hd, d = idx - h * hd;
+    // the state writes complete before the count (workgroup-scope release), and the merging
+    // wave reads the others' states after it (acquire)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    int arrived = 0;
+    if (lane == 0) arrived = atomicAdd(&waves_done, 1);
+    arrived = __builtin_amdgcn_readfirstlane(arrived);
+    if (arrived != kWavesM - 1) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    // one (head, 8-coordinate group) per lane and step: the head's wave weights once, then two
+    // 16-byte reads per wave state and two 16-byte stores
+    for (int it = lane; it < G * (hd / 8); it += 64) {
+        const int h = it / (hd / 8), d0 = 8 * (it % (hd / 8));
         float mw[kWavesM], M = -__builtin_inff();
 #pragma unroll
         for (int w = 0; w < kWavesM; ++w) {
-            mw[w] = ((const float*)vbuf[w][0])[kMaxG * hd + h];
+            mw[w] = ((const float*)vbuf[w][0])[kStM + h];
             M = fmaxf(M, mw[w]);
         }
-        float L = 0.0f, A = 0.0f;
+        float L = 0.0f;
+        f32x4_t A0 = {0.0f, 0.0f, 0.0f, 0.0f}, A1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int w = 0; w < kWavesM; ++w) {
             const float* sw = (const float*)vbuf[w][0];
             if (mw[w] != -__builtin_inff()) {
                 const float wt = __builtin_amdgcn_exp2f(mw[w] - M);
-                L = fmaf(wt, sw[kMaxG * hd + kMaxG + h], L);
-                A = fmaf(wt, sw[h * hd + d], A);
+                L = fmaf(wt, sw[kStL + h], L);
+                const f32x4_t a0 = *(const f32x4_t*)&sw[h * kStRow + d0];
+                const f32x4_t a1 = *(const f32x4_t*)&sw[h * kStRow + d0 + 4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    A0[k] = fmaf(wt, a0[k], A0[k]);
+                    A1[k] = fmaf(wt, a1[k], A1[k]);
+                }
             }
         }
-        part_acc[((head0 + h) * nsplit + blk) * hd + d] = A;
-        if (d == 0) {  // m back in natural units
+        float* pa = part_acc + ((head0 + h) * nsplit + blk) * hd + d0;
+        *(f32x4_t*)pa = A0;
+        *(f32x4_t*)(pa + 4) = A1;
+        if (d0 == 0) {  // m back in natural units
             part_ml[((head0 + h) * nsplit + blk) * 2 + 0] =
                 M == -__builtin_inff() ? M : M * 0.6931471805599453f;
             part_ml[((head0 + h) * nsplit + blk) * 2 + 1] = L;
@@ -1016,9 +1190,9 @@ void launch_mfma_split(const float* qrot, const Queries& qsv, const Pages& pg,
     const int64_t wgs = ceil_div((int64_t)nq * nsplit, kXcds) * kXcds * kvh;
     Queries q2 = qsv;
     q2.seq_lens_count = nq;
-    hipLaunchKernelGGL((tq_attn_mfma_kernel<Pages>), dim3((unsigned)wgs), dim3(64 * kWavesM), 0, s,
-                       qrot, q2, pg, kcent, vcent, qh, kvh, 1.0f / sqrtf(128.0f), ml, acc, nsplit,
-                       nsplit);
+    auto kern = qh / kvh <= 4 ? tq_attn_mfma_kernel<Pages, true> : tq_attn_mfma_kernel<Pages, false>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)wgs), dim3(64 * kWavesM), 0, s, qrot, q2, pg, kcent,
+                       vcent, qh, kvh, 1.0f / sqrtf(128.0f), ml, acc, nsplit, nsplit);
 }
 
 struct AttnArgs {
