@@ -14,6 +14,7 @@
 //   1. q_rot = Pi_k q                  (per query head)
 //   2. split partials                  (the HBM stream over the pages)
 //   3. merge + unrotate -> fp16 output
+#include "fhip_internal.h"
 #include "tq_quant.h"
 
 using namespace fhip;
@@ -122,9 +123,24 @@ __global__ __launch_bounds__(256) void tq_attn_prerotate_kernel(const uint16_t* 
                                                                 int nvec) {
     __shared__ float qs[kRotVecs][kMaxHd];
     const int v0 = blockIdx.x * kRotVecs;
-    for (int e = threadIdx.x; e < kRotVecs * hd; e += blockDim.x) {
-        const int v = e / hd, j = e - v * hd;
-        qs[v][j] = v0 + v < nvec ? h2f(q[(int64_t)(v0 + v) * hd + j]) : 0.0f;
+    {
+        // every load is issued before the first is waited for: vectors past nvec read
+        // vector 0 (in bounds) and are zeroed
+        constexpr int kPer = kRotVecs * kMaxHd / 256;
+        uint16_t raw[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int e = threadIdx.x + k * 256;
+            const int v = e / hd, j = e - v * hd;
+            const int64_t src = e < kRotVecs * hd && v0 + v < nvec ? (int64_t)(v0 + v) * hd + j : 0;
+            raw[k] = q[src];
+        }
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int e = threadIdx.x + k * 256;
+            const int v = e / hd, j = e - v * hd;
+            if (e < kRotVecs * hd) qs[v][j] = v0 + v < nvec ? h2f(raw[k]) : 0.0f;
+        }
     }
     __syncthreads();
     for (int r = threadIdx.x; r < 2 * hd; r += blockDim.x) {
@@ -1401,6 +1417,55 @@ int fhip_launch_attention_tq_decode_ptrs(void* output, const void* q, const int3
                 num_pages};
     return launch_attention(a, pg, fhip_host::as_stream(stream));
 }
+
+}  // extern "C"
+
+namespace fhip_internal {
+
+int attention_tq_decode_ptrs_staged(void* output, const void* q, const int32_t* block_table,
+                                    const int32_t* seq_lens, int batch, int max_blocks,
+                                    int table_stride, int num_pages, const void** k_packed_ptrs,
+                                    const void** k_norms_ptrs, const void** v_packed_ptrs,
+                                    const void** v_norms_ptrs, const float* k_rotation,
+                                    const float* v_rotation, const float* k_centroids,
+                                    const float* v_centroids, int num_q_heads, int num_kv_heads,
+                                    int head_dim, int key_bits, int value_bits, void* workspace,
+                                    hipStream_t stream) {
+    if (batch < 0 || max_blocks <= 0 || num_pages < 0 || table_stride < max_blocks ||
+        !attn_shape_ok(num_q_heads, num_kv_heads, head_dim, key_bits, value_bits))
+        return hipErrorInvalidValue;
+    if ((int64_t)batch * num_q_heads > (int64_t)1 << 30 || batch > 65535 ||
+        max_blocks * (int64_t)FHIP_PAGE_TOKENS > kMaxTokensTq)
+        return hipErrorInvalidValue;
+    if (batch == 0) return hipSuccess;
+    if (!output || !q || !block_table || !seq_lens || (num_pages > 0 && (!k_packed_ptrs ||
+        !k_norms_ptrs || !v_packed_ptrs || !v_norms_ptrs)) || !k_rotation || !v_rotation ||
+        !k_centroids || !v_centroids || !workspace)
+        return hipErrorInvalidValue;
+    AttnArgs a;
+    a.out = output;
+    a.q = q;
+    a.qs = Queries{block_table, table_stride, max_blocks, seq_lens, 0, 0, batch};
+    a.nq = batch;
+    a.krot = k_rotation;
+    a.vrot = v_rotation;
+    a.kcent = k_centroids;
+    a.vcent = v_centroids;
+    a.qh = num_q_heads;
+    a.kvh = num_kv_heads;
+    a.hd = head_dim;
+    a.kbits = key_bits;
+    a.vbits = value_bits;
+    a.ws = workspace;
+    PtrPages pg{(const uint8_t* const*)k_packed_ptrs, (const uint8_t* const*)k_norms_ptrs,
+                (const uint8_t* const*)v_packed_ptrs, (const uint8_t* const*)v_norms_ptrs,
+                num_pages};
+    return launch_attention(a, pg, stream);
+}
+
+}  // namespace fhip_internal
+
+extern "C" {
 
 // The reference interface: one sequence, num_tokens queries at positions
 // start_pos .. start_pos + num_tokens - 1, per-block pointer arrays. `ws` holds the split

@@ -23,6 +23,7 @@
 #include <vector>
 
 #include "fracture_hip.h"
+#include "fhip_internal.h"
 
 namespace {
 
@@ -154,11 +155,12 @@ struct fhip_backend {
     std::mutex launch_mu;
     static constexpr int kSlots = 16;
     StageSlot slots[kSlots];
+    // side stream for staging copies that may run ahead of `stream` (default priority)
+    hipStream_t copy_stream = nullptr;
+    hipEvent_t copy_ev[kSlots] = {};
     int next_slot = 0;
     void* workspace = nullptr;
     size_t ws_cap = 0;
-    hipEvent_t ws_ev = nullptr;
-    bool ws_pending = false;
     // registered KV page pools: device-resident arrays of the pool's per-block addresses
     struct PagePool {
         const void** dev = nullptr;          // nlists * pool_len addresses, list-major
@@ -225,7 +227,8 @@ struct fhip_backend {
 
     // Copy `bytes` of host data to a device staging slot; returns the slot index. Callers
     // hold launch_mu and call stage_done(slot) after enqueuing the consumer kernel.
-    int stage(const void* src, size_t bytes, void** dev_out, int* slot_out) {
+    // The next slot, free (its last reader has completed) and at least `bytes` large.
+    int next_free_slot(size_t bytes, int* slot_out) {
         const int si = next_slot;
         next_slot = (next_slot + 1) % kSlots;
         StageSlot& s = slots[si];
@@ -245,6 +248,16 @@ struct fhip_backend {
             HIP_TRY(hipMalloc(&s.dev, cap));
             s.cap = cap;
         }
+        *slot_out = si;
+        return FHIP_OK;
+    }
+    // Copy `bytes` of host data to a device staging slot; returns the slot index. Callers
+    // hold launch_mu and call stage_done(slot) after enqueuing the consumer kernel.
+    int stage(const void* src, size_t bytes, void** dev_out, int* slot_out) {
+        int si;
+        int r = next_free_slot(bytes, &si);
+        if (r) return r;
+        StageSlot& s = slots[si];
         if (bytes) {
             memcpy(s.host, src, bytes);
             HIP_TRY(hipMemcpyAsync(s.dev, s.host, bytes, hipMemcpyHostToDevice, stream));
@@ -253,24 +266,51 @@ struct fhip_backend {
         *slot_out = si;
         return FHIP_OK;
     }
+    // A slot of at least `bytes` whose host side the caller fills (host_out), then
+    // stage_ahead_copy(slot, bytes): the copy runs on the backend's copy stream, so it can
+    // proceed while `stream` still runs earlier calls' kernels (a copy queued on `stream`
+    // itself costs the copy plus two hand-offs between the copy engine and the compute queue
+    // in the call's own time), and `stream` waits for it. Callers hold launch_mu and call
+    // stage_done(slot) after enqueuing the last kernel that reads the slot.
+    int stage_ahead_begin(size_t bytes, void** host_out, void** dev_out, int* slot_out) {
+        int si;
+        int r = next_free_slot(bytes, &si);
+        if (r) return r;
+        if (!copy_stream) HIP_TRY(hipStreamCreateWithFlags(&copy_stream, hipStreamNonBlocking));
+        if (!copy_ev[si]) HIP_TRY(hipEventCreateWithFlags(&copy_ev[si], hipEventDisableTiming));
+        *host_out = slots[si].host;
+        *dev_out = slots[si].dev;
+        *slot_out = si;
+        return FHIP_OK;
+    }
+    int stage_ahead_copy(int si, size_t bytes) {
+        HIP_TRY(hipMemcpyAsync(slots[si].dev, slots[si].host, bytes, hipMemcpyHostToDevice,
+                               copy_stream));
+        HIP_TRY(hipEventRecord(copy_ev[si], copy_stream));
+        HIP_TRY(hipStreamWaitEvent(stream, copy_ev[si], 0));
+        return FHIP_OK;
+    }
     int stage_done(int si) {
         HIP_TRY(hipEventRecord(slots[si].ev, stream));
         slots[si].pending = true;
         return FHIP_OK;
     }
     // Backend-owned scratch (softmax partials, attention split partials). Callers hold
-    // launch_mu and call ws_done() after enqueuing the kernels that use it. Every user of the
-    // workspace runs on `stream`, so stream order already keeps one call's kernels from
-    // overwriting the previous call's partials; the host waits only before freeing a
-    // workspace that a queued kernel may still use.
+    // launch_mu. Every user of the workspace runs on `stream`, so stream order already keeps
+    // one call's kernels from overwriting the previous call's partials, and no per-call event
+    // is recorded (each one is a queue packet between two calls' kernels); growing the
+    // workspace waits for the stream before freeing the old one.
     int get_workspace(size_t bytes, void** out) {
-        if (!ws_ev) HIP_TRY(hipEventCreateWithFlags(&ws_ev, hipEventDisableTiming));
         if (bytes > ws_cap) {
-            if (ws_pending) {
-                HIP_TRY(hipEventSynchronize(ws_ev));
-                ws_pending = false;
+            // a captured graph would keep the old address, and a capturing stream cannot be
+            // waited for
+            if (capturing)
+                return fail(FHIP_ERR_BACKEND, "the workspace must grow to %zu bytes during graph "
+                            "capture: run the operation once before capturing it", bytes);
+            if (workspace) {
+                HIP_TRY(hipStreamSynchronize(stream));
+                HIP_TRY(hipFree(workspace));
             }
-            if (workspace) HIP_TRY(hipFree(workspace));
             workspace = nullptr;
             ws_cap = 0;
             size_t cap = 1 << 20;
@@ -279,11 +319,6 @@ struct fhip_backend {
             ws_cap = cap;
         }
         *out = workspace;
-        return FHIP_OK;
-    }
-    int ws_done() {
-        HIP_TRY(hipEventRecord(ws_ev, stream));
-        ws_pending = true;
         return FHIP_OK;
     }
 };
@@ -351,13 +386,16 @@ void fhip_backend_destroy(fhip_backend* b) {
         (void)hipEventDestroy(kv.second.first);
         (void)hipEventDestroy(kv.second.second);
     }
+    if (b->copy_stream) (void)hipStreamSynchronize(b->copy_stream);
     for (auto& s : b->slots) {
         if (s.host) (void)hipHostFree(s.host);
         if (s.dev) (void)hipFree(s.dev);
         if (s.ev) (void)hipEventDestroy(s.ev);
     }
+    for (hipEvent_t e : b->copy_ev)
+        if (e) (void)hipEventDestroy(e);
+    if (b->copy_stream) (void)hipStreamDestroy(b->copy_stream);
     if (b->workspace) (void)hipFree(b->workspace);
-    if (b->ws_ev) (void)hipEventDestroy(b->ws_ev);
     for (auto& e : b->plans) fhip_tq_plan_destroy(e.plan);
     for (auto& kv : b->pools) (void)hipFree((void*)kv.second.dev);
     if (b->rope_freq) (void)hipFree(b->rope_freq);
@@ -1109,9 +1147,8 @@ int fhip_softmax_rows(fhip_backend* b, const fhip_tensor* logits, float temperat
     if (r) return r;
     int e = fhip_launch_softmax_rows((const float*)pl, (float*)pp, (int)rows, (int)cols,
                                      temperature, ws, b->stream);
-    r = b->ws_done();
     if (e != hipSuccess) return hip_fail((hipError_t)e);
-    return r;
+    return FHIP_OK;
 }
 
 int fhip_argmax_rows(fhip_backend* b, const fhip_tensor* logits, uint32_t* tokens_out,
@@ -1241,7 +1278,6 @@ int fhip_attention_paged_tq(fhip_backend* b, const fhip_tensor* q, const int32_t
         (int)vpd, ws, wsb, b->stream);
     b->stage_done(s1);
     b->stage_done(s2);
-    b->ws_done();
     if (e != hipSuccess) return hip_fail((hipError_t)e);
     return FHIP_OK;
 }
@@ -1410,7 +1446,6 @@ int fhip_attention_paged_pool(fhip_backend* b, const fhip_tensor* q, const int32
                                            (int)start_pos, (int)needed_blocks, ws, wsb,
                                            b->stream);
     b->stage_done(s1);
-    b->ws_done();
     if (e != hipSuccess) return hip_fail((hipError_t)e);
     return FHIP_OK;
 }
@@ -1486,7 +1521,6 @@ int fhip_attention_paged_tq_pool(fhip_backend* b, const fhip_tensor* q,
         (int)num_kv_heads, (int)hd, (int)kv_len, (int)start_pos, key_bits, value_bits, (int)kpd,
         (int)vpd, ws, wsb, b->stream);
     b->stage_done(s1);
-    b->ws_done();
     if (e != hipSuccess) return hip_fail((hipError_t)e);
     return FHIP_OK;
 }
@@ -1662,26 +1696,37 @@ int fhip_attention_paged_tq_batched(fhip_backend* b, const fhip_tensor* q,
     if (B == 0) return FHIP_OK;
     set_device(b);
     std::lock_guard<std::mutex> g(b->launch_mu);
-    void *dbt, *dlen;
-    int s1, s2;
-    r = b->stage(block_tables, B * max_blocks * sizeof(int32_t), &dbt, &s1);
-    if (r) return r;
-    r = b->stage(seq_lens, B * sizeof(uint32_t), &dlen, &s2);
-    if (r) return r;
+    // The lengths and the block table travel in one slot, copied on the side stream ahead of
+    // the kernels; rows hold their used page ids only (the kernels read no others), at a
+    // stride rounded up to 16 bytes.
+    const size_t stride = (max_blocks + 3) & ~(size_t)3;
+    const size_t lens_bytes = (B * sizeof(int32_t) + 255) & ~(size_t)255;
+    const size_t staged = lens_bytes + B * stride * sizeof(int32_t);
     const size_t wsb = fhip_attention_tq_workspace_bytes((int)B, (int)qh, (int)hd, (int)max_blocks);
     void* ws;
     r = b->get_workspace(wsb, &ws);
     if (r) return r;
+    void *hslot, *dslot;
+    int s1;
+    r = b->stage_ahead_begin(staged, &hslot, &dslot, &s1);
+    if (r) return r;
+    int32_t* hlens = (int32_t*)hslot;
+    int32_t* htable = (int32_t*)((char*)hslot + lens_bytes);
+    for (uint64_t i = 0; i < B; ++i) {
+        hlens[i] = (int32_t)seq_lens[i];
+        const uint64_t nb = (seq_lens[i] + FHIP_PAGE_TOKENS - 1) / FHIP_PAGE_TOKENS;
+        memcpy(htable + i * stride, block_tables + i * max_blocks, nb * sizeof(int32_t));
+    }
+    r = b->stage_ahead_copy(s1, staged);
+    if (r) return r;
     const void** dp = pp.dev;
     const size_t n = pp.pool_len;
-    int e = fhip_launch_attention_tq_decode_ptrs(
-        po, pq, (const int32_t*)dbt, (const int32_t*)dlen, (int)B, (int)max_blocks, (int)n, dp,
-        dp + n, dp + 2 * n, dp + 3 * n, (const float*)pkr, (const float*)pvr, (const float*)pkc,
-        (const float*)pvc, (int)qh, (int)num_kv_heads, (int)hd, key_bits, value_bits, ws,
-        b->stream);
+    int e = fhip_internal::attention_tq_decode_ptrs_staged(
+        po, pq, (const int32_t*)((char*)dslot + lens_bytes), (const int32_t*)dslot, (int)B,
+        (int)max_blocks, (int)stride, (int)n, dp, dp + n, dp + 2 * n, dp + 3 * n,
+        (const float*)pkr, (const float*)pvr, (const float*)pkc, (const float*)pvc, (int)qh,
+        (int)num_kv_heads, (int)hd, key_bits, value_bits, ws, b->stream);
     b->stage_done(s1);
-    b->stage_done(s2);
-    b->ws_done();
     if (e != hipSuccess) return hip_fail((hipError_t)e);
     return FHIP_OK;
 }
@@ -1754,7 +1799,6 @@ int fhip_attention_paged(fhip_backend* b, const fhip_tensor* q, const int32_t* b
                                            b->stream);
     b->stage_done(s1);
     b->stage_done(s2);
-    b->ws_done();
     if (e != hipSuccess) return hip_fail((hipError_t)e);
     return FHIP_OK;
 }

@@ -146,11 +146,13 @@ def host_pool(lists, backend):
     return [np.stack([backend.download(t) for t in lst]) for lst in lists]
 
 
-def test_attention_batched_pool(backend):
+@pytest.mark.parametrize("hd,kb,vb", [(128, 4, 4), (64, 3, 3)])
+def test_attention_batched_pool(backend, hd, kb, vb):
     """One batched call over a registered pool equals the oracle and, bit for bit, one pooled
-    call per sequence (T=1 at its last position)."""
+    call per sequence (T=1 at its last position); calls that alternate two batches for more
+    than a turn of the host staging ring each repeat their batch's output bit for bit."""
     rng = np.random.default_rng(12)
-    qh, kvh, hd, kb, vb = 32, 8, 128, 4, 4
+    qh, kvh = 32, 8
     lens = [1, 17, 1030, 2100, 40, 3000]
     nbs = [(n + 15) // 16 for n in lens]
     P = sum(nbs) + 3
@@ -195,6 +197,35 @@ def test_attention_batched_pool(backend):
         bad[2][3] = P + 1
         backend.attention_paged_tq_batched(tq_, bad, lens, pool, tkr, tvr, tkc, tvc, kb, vb, kvh,
                                            out)
+    # the block table and lengths travel through the backend's ring of 16 host staging slots,
+    # read by the device in place: alternate two different batches for more than a turn of
+    # the ring, queued back to back, and each call must give its batch's first output again
+    lens2 = [3000, 1, 1030]
+    tables2 = [tables[5], tables[0], tables[2]]
+    q2 = backend.upload(q[:3])
+    first = {}
+    outs = []
+    for i in range(20):
+        o = backend.alloc([B if i % 2 == 0 else 3, qh, hd], DType.FP16)
+        if i % 2 == 0:
+            backend.attention_paged_tq_batched(tq_, tables, lens, pool, tkr, tvr, tkc, tvc, kb,
+                                               vb, kvh, o)
+        else:
+            backend.attention_paged_tq_batched(q2, tables2, lens2, pool, tkr, tvr, tkc, tvc, kb,
+                                               vb, kvh, o)
+        outs.append(o)
+    for i, o in enumerate(outs):
+        h = backend.download(o).view(np.uint16)
+        first.setdefault(i % 2, h)
+        assert np.array_equal(h, first[i % 2]), f"call {i}"
+        backend.free(o)
+    assert np.array_equal(first[0], got.view(np.uint16))
+    for j in range(3):
+        tb = np.array(tables2[j], np.int32)
+        want = oracle.tq_attention(q[j], tb, lens2[j], *hp, krot, vrot, kc, vc, kb, vb, kvh)
+        assert_close(first[1][j].view(np.float16).astype(np.float32), want.astype(np.float32),
+                     1e-3, 1e-3, f"second batch, sequence {j}")
+    backend.free(q2)
     backend.page_pool_destroy(pool)
     for t in [x for l in lists for x in l] + [tq_, out, tkr, tvr, tkc, tvc]:
         backend.free(t)
