@@ -72,6 +72,40 @@ def test_copy_rows(backend):
         backend.free(t)
 
 
+def test_small_tensor_arena(backend):
+    """Tensors up to 64 KB share large chunks in size classes and are recycled on free: live
+    tensors of every class never overlap (each keeps its own bytes through frees and
+    reallocations around it), and a freed slot is handed out again."""
+    rng = np.random.default_rng(3)
+    sizes = [0, 1, 255, 256, 257, 4095, 8192, 65536, 65537, 100000]
+    live = []
+
+    def new(n):
+        t = backend.alloc([n], DType.INT8)
+        data = rng.integers(0, 256, n).astype(np.uint8)
+        if n:
+            backend.copy_to_device(t, data)
+        live.append((t, data))
+
+    for i in range(400):
+        new(sizes[i % len(sizes)])
+    freed = set()
+    for t, _ in live[::3]:
+        freed.add(backend.get_ptr(t.id))
+        backend.free(t)
+    live = [x for i, x in enumerate(live) if i % 3]
+    reused = 0
+    for i in range(200):
+        new(sizes[i % len(sizes)])
+        reused += backend.get_ptr(live[-1][0].id) in freed
+    assert reused > 0
+    for t, data in live:
+        if len(data):
+            assert np.array_equal(backend.download(t).reshape(-1).view(np.uint8), data)
+    for t, _ in live:
+        backend.free(t)
+
+
 def test_device_info_timers_markers(backend):
     assert backend.device_name()
     assert backend.total_memory() > 0
