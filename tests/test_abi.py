@@ -144,3 +144,26 @@ def test_kernels_module_requires_device_tensors():
     a = torch.zeros(8, dtype=torch.float16)
     with pytest.raises(ValueError):
         K.add(a, a, a)
+
+
+def _c_params(decl: str) -> int:
+    inner = decl[decl.index("(") + 1:decl.rindex(")")].strip()
+    return 0 if inner in ("", "void") else inner.count(",") + 1
+
+
+def test_rust_shim_declarations_match_header():
+    """The FFI block of backends/fracture-hip (the Rust crate a Fracture maintainer drops in)
+    names only header functions, each with the header's parameter count."""
+    import re
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    ffi = (root / "backends/fracture-hip/src/ffi.rs").read_text()
+    hdr = (root / "include/fracture_hip.h").read_text()
+    decls = re.findall(r"pub fn (fhip_\w+)\(([^;]*?)\)\s*(?:->[^;]*)?;", ffi, re.S)
+    assert len(decls) > 40
+    for name, args in decls:
+        m = re.search(r"\b" + name + r"\s*\(([^;]*?)\)\s*;", hdr, re.S)
+        assert m, f"{name} is not declared in the header"
+        n_rust = 0 if not args.strip() else args.count(":")
+        assert n_rust == _c_params("(" + m.group(1) + ")"), name
