@@ -764,7 +764,7 @@ __global__ __launch_bounds__(64 * kWavesM) __attribute__((amdgpu_waves_per_eu(3)
 tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
                     const float* __restrict__ kcent, const float* __restrict__ vcent, int qh,
                     int kvh, float scale, float* __restrict__ part_ml,
-                    float* __restrict__ part_acc, int nsplit, int nblk) {
+                    float* __restrict__ part_acc, int nsplit, int nblk, int tok) {
     constexpr int hd = 128;
     // Code-byte tables: byte b -> the (c_hi | c_lo' << 16) words of its two codes, K as
     // {high nibble, low nibble} (the QK A operand's order), V as {low, high} (the PV B
@@ -794,10 +794,14 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     const int64_t per8 = (int64_t)kXcds * kvh;
     const int64_t item = (wg / per8) * kXcds + wg % kXcds;
     const int g = (int)((wg % per8) / kXcds);
-    const int qi = (int)(item / nblk);
-    if (qi >= qs.seq_lens_count) return;
+    // Item (token group, block): a group is `tok` consecutive queries of one sequence (causal
+    // prefill; 1 in decode), whose G query heads each fill MFMA columns h = G t + head.
+    const int qg = (int)(item / nblk);
+    const int tq0 = qg * tok;
+    if (tq0 >= qs.seq_lens_count) return;
+    const int tq_last = min(tq0 + tok, qs.seq_lens_count) - 1;
     const int blk = (int)(item % nblk);
-    const int clen = qs.causal_len(qi);
+    const int clen = qs.causal_len(tq_last);  // the group's longest causal length
     if (blk * kSplit >= clen) return;
     {
         const int b = threadIdx.x;
@@ -814,10 +818,17 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     const int t_begin = split * kSplitMfma;
     const int t_end = min(clen, t_begin + kSplitMfma);
     const int G = qh / kvh;
-    const int32_t* table = qs.table + (int64_t)qi * qs.table_stride;
+    const int32_t* table = qs.table + (int64_t)tq0 * qs.table_stride;
     uint8_t* vb = vbuf[wave][0];
     float2* nb = nbuf[wave];
-    const int64_t head0 = (int64_t)qi * qh + (int64_t)g * G;
+    const int ncols = tok * G;  // live head columns (at most 8)
+    // this lane's column: token tq0 + ct, head ch; its causal length (0 for a column past the
+    // queries, so that every position is masked for it)
+    const int ct = (n & 7) / G, ch = (n & 7) - ct * G;
+    const bool col_ok = (n & 7) < ncols && tq0 + ct < qs.seq_lens_count;
+    const int col_len = col_ok ? qs.causal_len(tq0 + ct) : 0;
+    // the shortest length of the group (its first query's): chunks below it need no mask
+    const int min_len = tok > 1 ? qs.causal_len(tq0) : clen;
 
     float m_run = -__builtin_inff(), l_run = 0.0f;  // log2 units; lanes n, n ^ 8: head n & 7
     // PV accumulators out^T, dim tile c: lane (n, rg) holds head slot n (n < 8: head n, hi
@@ -846,9 +857,10 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     uint32_t bq[8][4];
     {
         // heads past G read head 0 and are zeroed by the multiplier
-        const int h = n & 7;
-        const float* qsrc = qrot + ((int64_t)qi * qh + (int64_t)g * G + (h < G ? h : 0)) * hd;
-        const float qmul = h < G ? scale * 1.4426950408889634f : 0.0f;
+        // columns past the group's heads read the group's first vector and are zeroed
+        const float* qsrc =
+            qrot + ((int64_t)(col_ok ? tq0 + ct : tq0) * qh + (int64_t)g * G + (col_ok ? ch : 0)) * hd;
+        const float qmul = col_ok ? scale * 1.4426950408889634f : 0.0f;
         f32x4_t qv[8];
 #pragma unroll
         for (int s8 = 0; s8 < 8; ++s8) qv[s8] = *(const f32x4_t*)(qsrc + 32 * rg + 4 * s8);
@@ -902,7 +914,7 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
         const int tn = t0 + kChunkM;  // next chunk
         const int jn = (tn - t_begin) >> 4;  // its first split page
         const uint32_t pmask_n = tn < t_end ? (uint32_t)(vmask >> jn) & 0xfu : 0u;
-        const bool full = pmask == 0xfu && tn <= t_end;
+        const bool full = pmask == 0xfu && tn <= t_end && tn <= min_len;
 
         // ---- QK: 4 tiles x 8 steps, K codes from this wave's DMA buffer
         float sc[4][4];  // !kG4 [pt][e]: position 16rg + 4e + pt, head n & 7
@@ -1025,11 +1037,12 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
                 for (int e = 0; e < 4; ++e) sc[pt][e] *= kn[4 * e + pt];
             if (!full) {
                 const bool row_ok = (pmask >> rg) & 1u;
+                const int lim = min(t_end, col_len);
 #pragma unroll
                 for (int pt = 0; pt < 4; ++pt)
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        if (!(row_ok && t0 + 16 * rg + 4 * e + pt < t_end)) sc[pt][e] = -__builtin_inff();
+                        if (!(row_ok && t0 + 16 * rg + 4 * e + pt < lim)) sc[pt][e] = -__builtin_inff();
             }
             float cmax = -__builtin_inff();
 #pragma unroll
@@ -1065,7 +1078,7 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
         // rescale the accumulators when some head's max moved (each lane's alpha is that of
         // its accumulator slot's head)
         const bool moved_any =
-            __ballot((n < G) && (!kG4 || n < 4) && (rg == 0) && (m_new > m_run)) != 0;
+            __ballot((n < ncols) && (!kG4 || n < 4) && (rg == 0) && (m_new > m_run)) != 0;
         if (moved_any) {
 #pragma unroll
             for (int c = 0; c < 8; ++c)
@@ -1144,9 +1157,9 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
         f32x4_t v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e ^ 1] = fmaf(ror8(acc[c][e]), 1.0f / 4096.0f, acc[c][e]);
-        if (n < G) *(f32x4_t*)&st[n * kStRow + 16 * c + 4 * rg] = v;
+        if (n < ncols) *(f32x4_t*)&st[n * kStRow + 16 * c + 4 * rg] = v;
     }
-    if (n < G && rg == 0) {
+    if (n < ncols && rg == 0) {
         st[kStM + n] = m_run;
         st[kStL + n] = l_run;
     }
@@ -1160,8 +1173,12 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     // one (head, 8-coordinate group) per lane and step: the head's wave weights once, then two
     // 16-byte reads per wave state and two 16-byte stores
-    for (int it = lane; it < G * (hd / 8); it += 64) {
+    for (int it = lane; it < ncols * (hd / 8); it += 64) {
         const int h = it / (hd / 8), d0 = 8 * (it % (hd / 8));
+        const int ht = h / G;
+        if (tq0 + ht >= qs.seq_lens_count) continue;  // a column past the queries
+        // partial of vector (query tq0 + ht, q head G g + h - G ht)
+        const int64_t vec = (int64_t)(tq0 + ht) * qh + (int64_t)g * G + (h - ht * G);
         float mw[kWavesM], M = -__builtin_inff();
 #pragma unroll
         for (int w = 0; w < kWavesM; ++w) {
@@ -1185,13 +1202,13 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
                 }
             }
         }
-        float* pa = part_acc + ((head0 + h) * nsplit + blk) * hd + d0;
+        float* pa = part_acc + (vec * nsplit + blk) * hd + d0;
         *(f32x4_t*)pa = A0;
         *(f32x4_t*)(pa + 4) = A1;
         if (d0 == 0) {  // m back in natural units
-            part_ml[((head0 + h) * nsplit + blk) * 2 + 0] =
+            part_ml[(vec * nsplit + blk) * 2 + 0] =
                 M == -__builtin_inff() ? M : M * 0.6931471805599453f;
-            part_ml[((head0 + h) * nsplit + blk) * 2 + 1] = L;
+            part_ml[(vec * nsplit + blk) * 2 + 1] = L;
         }
     }
 }
@@ -1200,15 +1217,22 @@ template <class Pages>
 void launch_mfma_split(const float* qrot, const Queries& qsv, const Pages& pg,
                        const float* kcent, const float* vcent, int nq, int qh, int kvh,
                        int nsplit, float* ml, float* acc, hipStream_t s) {
-    // one workgroup per (query, kv head, kSplit-position block): the block count is the
-    // partial layout's split count; the (query, block) items are padded to a multiple of the
-    // XCD count (the kernel's index spreads items, not heads, over the XCDs)
-    const int64_t wgs = ceil_div((int64_t)nq * nsplit, kXcds) * kXcds * kvh;
+    // Causal prefill (queries at consecutive positions of one sequence: one shared block table,
+    // lengths from start_pos) groups 8 / G consecutive queries per item so that they share the
+    // MFMA columns and every code lookup; decode keeps one query per item.
+    const int G = qh / kvh;
+    const int tok = (!qsv.seq_lens && qsv.table_stride == 0 && nq > 1 && G < 8) ? 8 / G : 1;
+    const int64_t items = ceil_div((int64_t)nq, tok);
+    // one workgroup per (item, kv head, kSplit-position block): the block count is the
+    // partial layout's split count; the (item, block) pairs are padded to a multiple of the
+    // XCD count (the kernel's index spreads them, not heads, over the XCDs)
+    const int64_t wgs = ceil_div(items * nsplit, kXcds) * kXcds * kvh;
     Queries q2 = qsv;
     q2.seq_lens_count = nq;
-    auto kern = qh / kvh <= 4 ? tq_attn_mfma_kernel<Pages, true> : tq_attn_mfma_kernel<Pages, false>;
+    auto kern = G <= 4 && tok == 1 ? tq_attn_mfma_kernel<Pages, true>
+                                   : tq_attn_mfma_kernel<Pages, false>;
     hipLaunchKernelGGL(kern, dim3((unsigned)wgs), dim3(64 * kWavesM), 0, s, qrot, q2, pg, kcent,
-                       vcent, qh, kvh, 1.0f / sqrtf(128.0f), ml, acc, nsplit, nsplit);
+                       vcent, qh, kvh, 1.0f / sqrtf(128.0f), ml, acc, nsplit, nsplit, tok);
 }
 
 struct AttnArgs {

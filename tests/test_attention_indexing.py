@@ -12,8 +12,14 @@ over lanes with numpy:
   load_k             entry(j0 + n / 4) + ((4 (n % 4) + pt) kvh + g) 64 + 16 rg, 16 bytes
   dma_v              entry(j0 + i) + ((lane / 4) kvh + g) 64 + 16 ((lane % 4) ^ ((lane / 8) % 4)), 16 bytes
   load_norms         norm entry(j0 + lane / 16) + 2 ((lane % 16) kvh + g), 2 bytes
-  Q (rotated)        (qi qh + g G + h) hd + 32 rg + 4 s, 16 bytes
-  partials           ((head0 + h) nsplit + block) (2 | hd) + ..., written by the workgroup's merge
+  Q (rotated)        (q qh + g G + head) hd + 32 rg + 4 s, 16 bytes, for column h = G t + head
+                     of query q = tq0 + t
+  partials           ((q qh + g G + head) nsplit + block) (2 | hd) + ..., written by the
+                     workgroup's merge
+
+In causal prefill (one block table shared by all queries, lengths from start_pos) a workgroup
+item is a group of `tok` = 8 / G consecutive queries whose heads share the MFMA columns; in
+decode tok = 1 and every query has its own table row.
 
 and asserts that each access stays inside its pool AND inside the page it means to read
 (an access past the page's rows reads a neighbouring page: in bounds, but wrong data).
@@ -58,10 +64,14 @@ class Bounds:
         self.count[buf] += off.size
 
 
-def model_mfma_kernel(lens, table, num_pages, qh, kvh, page_bytes, pool_bytes):
-    """Every access of tq_attn_mfma_kernel<PoolPages> for one launch (hd 128, K4/V4)."""
+def model_mfma_kernel(lens, table, num_pages, qh, kvh, page_bytes, pool_bytes, tok=1):
+    """Every access of tq_attn_mfma_kernel<PoolPages> for one launch (hd 128, K4/V4). With
+    tok > 1, `table` has one row that every query reads (causal prefill)."""
     hd, pd = 128, 64
-    B, max_blocks = table.shape
+    B = len(lens)
+    rows, max_blocks = table.shape
+    stride = 0 if tok > 1 else max_blocks
+    assert tok == 1 or rows == 1
     G = qh // kvh
     nsplit, _, ml_bytes, acc_bytes = ws_layout(B, qh, hd, max_blocks * PAGE)
     bnd = Bounds({"table": table.size * 4, "kp": pool_bytes["kp"], "kn": pool_bytes["kn"],
@@ -69,8 +79,9 @@ def model_mfma_kernel(lens, table, num_pages, qh, kvh, page_bytes, pool_bytes):
                   "part_ml": ml_bytes, "part_acc": acc_bytes})
     lane = np.arange(64)
     n, rg = lane & 15, lane >> 4
-    for qi in range(B):
-        clen = causal_len(lens[qi], max_blocks)
+    for tq0 in range(0, B, tok):
+        tq_last = min(tq0 + tok, B) - 1
+        clen = causal_len(lens[tq_last], max_blocks)
         for blk in range(nsplit):
             if blk * SPLIT >= clen:
                 continue  # the workgroup leaves before building its tables
@@ -83,9 +94,9 @@ def model_mfma_kernel(lens, table, num_pages, qh, kvh, page_bytes, pool_bytes):
                     has = t_begin + PAGE * lane < t_end
                     tidx = t_begin // PAGE + lane[has]
                     assert tidx.max() < max_blocks
-                    bnd.check("table", (qi * max_blocks + tidx) * 4, 4)
+                    bnd.check("table", (tq0 * stride + tidx) * 4, 4)
                     ids = np.full(64, -1, np.int64)
-                    ids[has] = table[qi, tidx]
+                    ids[has] = table.reshape(-1)[tq0 * stride + tidx]
                     ok = has & (ids >= 0) & (ids < num_pages)
                     if not ok.any():
                         continue
@@ -112,17 +123,21 @@ def model_mfma_kernel(lens, table, num_pages, qh, kvh, page_bytes, pool_bytes):
                         for nm in ("kn", "vn"):
                             assert (2 * row + 2).max() <= min(PAGE * kvh * 2, page_bytes[nm])
                             bnd.check(nm, e * page_bytes[nm] + 2 * row, 2)
-                    # Q: heads past G read head 0
+                    # Q: column h = G ct + ch; columns past the group read its first vector
                     h = n & 7
-                    hsrc = np.where(h < G, h, 0)
+                    ct, ch = h // G, h % G
+                    col_ok = (h < tok * G) & (tq0 + ct < B)
+                    qsrc = np.where(col_ok, tq0 + ct, tq0) * qh + g * G + np.where(col_ok, ch, 0)
                     for s8 in range(8):
-                        bnd.check("qrot", ((qi * qh + g * G + hsrc) * hd + 32 * rg + 4 * s8) * 4, 16)
-                # the workgroup's merge: one partial per head of the group
-                hg0 = qi * qh + g * G
-                hs = np.arange(G)
-                bnd.check("part_ml", (((hg0 + hs) * nsplit + blk) * 2) * 4, 8)
-                bnd.check("part_acc", (((hg0 + hs[:, None]) * nsplit + blk) * hd
-                                       + np.arange(hd)[None, :]) * 4, 4)
+                        bnd.check("qrot", (qsrc * hd + 32 * rg + 4 * s8) * 4, 16)
+                # the workgroup's merge: one partial per live column (query, head) of the group
+                for h in range(tok * G):
+                    ht = h // G
+                    if tq0 + ht >= B:
+                        continue
+                    vec = (tq0 + ht) * qh + g * G + (h - ht * G)
+                    bnd.check("part_ml", ((vec * nsplit + blk) * 2) * 4, 8)
+                    bnd.check("part_acc", ((vec * nsplit + blk) * hd + np.arange(hd)) * 4, 4)
     return bnd, nsplit
 
 
@@ -200,6 +215,26 @@ def test_mfma_decode_accesses_in_bounds(which):
     assert bnd.count["kp"] > 0 and bnd.count["vp"] > 0
     _, _, ml, acc = ws_layout(len(lens), qh, 128, table.shape[1] * PAGE)
     model_combine(lens, table.shape[1], qh, 128, nsplit, ml, acc)
+
+
+@pytest.mark.parametrize("qh,kvh,T,kv_len", [(32, 8, 37, 3000), (16, 8, 9, 1100), (8, 8, 20, 2100),
+                                             (32, 8, 64, 64)])
+def test_mfma_prefill_groups_in_bounds(qh, kvh, T, kv_len):
+    """Causal prefill: groups of 8 / G consecutive queries over one shared block table (the
+    reference interface's num_tokens > 1), ragged last group included."""
+    G = qh // kvh
+    tok = 8 // G if G < 8 else 1
+    start_pos = kv_len - T
+    lens = np.array([min(start_pos + t + 1, kv_len) for t in range(T)], np.int32)
+    nb = (kv_len + 15) // 16
+    rng = np.random.default_rng(T)
+    P = nb + 5
+    table = rng.permutation(P)[:nb].astype(np.int32)[None, :]
+    page, pool = pools(P, kvh)
+    bnd, nsplit = model_mfma_kernel(lens, table, P, qh, kvh, page, pool, tok=tok)
+    assert bnd.count["kp"] > 0 and bnd.count["part_acc"] > 0
+    _, _, ml, acc = ws_layout(T, qh, 128, nb * PAGE)
+    model_combine(lens, nb, qh, 128, nsplit, ml, acc)
 
 
 def test_page_stride_smaller_than_page_is_caught():
