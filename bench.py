@@ -632,15 +632,78 @@ def run_tq(args, torch, K, dev):
             "kernels": out}
 
 
+def prefill_attention_inputs(torch, K, dev, T, kv_len):
+    """Causal prefill of T queries at positions kv_len - T .. kv_len - 1 of one sequence
+    through the reference-signature launcher (per-page address arrays into one pool, K4/V4,
+    32/8 heads): returns (fn, algorithmic bytes, positions scored per kv head)."""
+    import ctypes as C
+
+    import numpy as np
+
+    from fracture_amd import turboquant as tq
+
+    QH, KVH, HD = ATT_SHAPE["QH"], ATT_SHAPE["KVH"], ATT_SHAPE["HD"]
+    nb = (kv_len + 15) // 16
+    P = nb + 3
+    g = torch.Generator(device=dev)
+    g.manual_seed(T + kv_len)
+    kp = torch.randint(0, 256, (P, 16, KVH * 64), generator=g, device=dev, dtype=torch.uint8)
+    vp = torch.randint(0, 256, (P, 16, KVH * 64), generator=g, device=dev, dtype=torch.uint8)
+    kn = (torch.rand((P, 16, KVH), generator=g, device=dev) * 10 + 6).to(torch.float16)
+    vn = (torch.rand((P, 16, KVH), generator=g, device=dev) * 10 + 6).to(torch.float16)
+
+    def ptrs(t, stride):
+        return torch.tensor([t.data_ptr() + p * stride for p in range(P)], dtype=torch.int64,
+                            device=dev)
+
+    pk, pkn, pv, pvn = (ptrs(kp, 16 * KVH * 64), ptrs(kn, 16 * KVH * 2), ptrs(vp, 16 * KVH * 64),
+                        ptrs(vn, 16 * KVH * 2))
+    table = torch.from_numpy(np.random.default_rng(2).permutation(P)[:nb].astype(np.int32)).to(dev)
+    q = torch.randn((T, QH, HD), generator=g, device=dev).to(torch.float16)
+    out = torch.empty_like(q)
+    krot = torch.from_numpy(tq.rotation_matrix(HD, 42)).to(dev)
+    vrot = torch.from_numpy(tq.rotation_matrix(HD, 542)).to(dev)
+    cent = torch.from_numpy(tq.codebook(HD, 4)[0]).to(dev)
+    lib = K._L()
+    wsb = lib.fhip_attention_tq_workspace_bytes(T, QH, HD, nb)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    keep = (kp, vp, kn, vn, pk, pkn, pv, pvn, table, q, out, krot, vrot, cent, ws)
+
+    def fn():
+        _ = keep
+        r = lib.fhip_launch_attention_paged_tq_ws(
+            out.data_ptr(), q.data_ptr(), table.data_ptr(), pk.data_ptr(), pkn.data_ptr(),
+            pv.data_ptr(), pvn.data_ptr(), krot.data_ptr(), vrot.data_ptr(), cent.data_ptr(),
+            cent.data_ptr(), T, QH, KVH, HD, kv_len, kv_len - T, 4, 4, 64, 64, ws.data_ptr(),
+            C.c_size_t(wsb), K._stream())
+        assert r == 0, r
+
+    scored = sum(min(kv_len - T + t + 1, kv_len) for t in range(T))
+    nbytes = kv_len * KVH * (64 + 64 + 4) + 2 * T * QH * HD * 2 + nb * 4
+    return fn, nbytes, scored
+
+
 def run_attention(args, torch, K, dev):
     fn, nb, tok, mean = attention_inputs(torch, K, dev)
     us = Timer(torch).time_us(fn, 10, warmup=2)
-    return {"workload": "TurboQuant K4/V4 paged decode attention, B=64, 32/8 heads, hd 128",
-            "kernels": {"attention_tq_decode": {
-                "us": round(us, 1), "GB/s": round(gbs(nb, us), 1),
-                "frac_of_peak": round(gbs(nb, us) / PEAK_HBM_GBS, 4), "bytes": nb,
-                "context_tokens": tok, "mean_ctx": mean,
-                "traffic": traffic_of("attention_tq_decode")}}}
+    kernels = {"attention_tq_decode": {
+        "us": round(us, 1), "GB/s": round(gbs(nb, us), 1),
+        "frac_of_peak": round(gbs(nb, us) / PEAK_HBM_GBS, 4), "bytes": nb,
+        "context_tokens": tok, "mean_ctx": mean,
+        "traffic": traffic_of("attention_tq_decode")}}
+    for T, kv_len in ((2048, 2048), (512, 8192)):
+        pfn, pnb, scored = prefill_attention_inputs(torch, K, dev, T, kv_len)
+        pus = Timer(torch).time_us(pfn, 5, warmup=2)
+        kernels[f"attention_tq_prefill_T{T}_ctx{kv_len}"] = {
+            "us": round(pus, 1), "GB/s": round(gbs(pnb, pus), 1),
+            "frac_of_peak": round(gbs(pnb, pus) / PEAK_HBM_GBS, 5), "bytes": pnb,
+            "positions_scored_per_kv_head": scored,
+            "Gpos/s": round(scored * ATT_SHAPE["KVH"] / pus / 1e3, 2),
+            "note": "causal prefill through fhip_launch_attention_paged_tq_ws; bytes are the "
+                    "distinct K/V pages, queries and outputs (each page is re-read by every "
+                    "group of 8 / G queries)"}
+    return {"workload": "TurboQuant K4/V4 paged decode attention, B=64, 32/8 heads, hd 128; "
+                        "causal prefill of one sequence", "kernels": kernels}
 
 
 def paged_inputs(torch, K, dev):

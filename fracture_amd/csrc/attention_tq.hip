@@ -117,6 +117,7 @@ __device__ __forceinline__ void row_group(const uint32_t* w, int g, int bits_rt,
 // A workgroup rotates kRotVecs vectors so Pi_k is read once per workgroup: work unit
 // (row i, half) computes row i of vectors 4 half .. 4 half + 3.
 constexpr int kRotVecs = 8;
+constexpr int kMfmaRotVecs = 4096;  // from this many query vectors on, batched MFMA rotations
 __global__ __launch_bounds__(256) void tq_attn_prerotate_kernel(const uint16_t* __restrict__ q,
                                                                 const float* __restrict__ rot,
                                                                 float* __restrict__ qrot, int hd,
@@ -373,25 +374,27 @@ __global__ __launch_bounds__(256) void tq_attn_split_kernel(
 constexpr int kCombHeads = 8;
 constexpr int kRotLdsMaxHd = 128;
 constexpr int kMaxTokensTq = kSplit * kSplit;  // 1024 splits: 32 KB of combine weights
-size_t combine_lds_bytes(int hd, int nsplit) {
-    return ((hd <= kRotLdsMaxHd ? (size_t)hd * hd : 0) + (size_t)kCombHeads * nsplit) *
+size_t combine_lds_bytes(int hd, int nsplit, bool merge_only = false) {
+    return ((hd <= kRotLdsMaxHd && !merge_only ? (size_t)hd * hd : 0) + (size_t)kCombHeads * nsplit) *
            sizeof(float);
 }
-template <bool kRotLds>
+// kMergeOnly: phase 2 writes each merged vector (fp32, already divided by its sum) to
+// merged[vector] and the kernel ends; the unrotation then runs as a batched MFMA product.
+template <bool kRotLds, bool kMergeOnly = false>
 __global__ __launch_bounds__(256) void tq_attn_combine_kernel(
     Queries qs, const float* __restrict__ part_ml, const float* __restrict__ part_acc,
     const float* __restrict__ vrot, uint16_t* __restrict__ out, int qh, int hd, int nsplit,
-    int64_t nvec) {
+    int64_t nvec, float* __restrict__ merged = nullptr) {
     __shared__ float o[kCombHeads][kMaxHd];
     __shared__ float linv[kCombHeads];
     __shared__ int nsv[kCombHeads];
     extern __shared__ uint32_t dyn[];
     float* rl = (float*)dyn;                                  // [hd][hd] (kRotLds)
-    float* wts = (float*)dyn + (kRotLds ? hd * hd : 0);      // [kCombHeads][nsplit]
+    float* wts = (float*)dyn + (kRotLds && !kMergeOnly ? hd * hd : 0);  // [kCombHeads][nsplit]
     const float* rot = kRotLds ? (const float*)rl : vrot;
     const int tid = threadIdx.x;
     const int64_t h0 = (int64_t)blockIdx.x * kCombHeads;
-    if (kRotLds) {   // the rotation into LDS: hd * hd / 4 16-byte chunks, all loads first
+    if (kRotLds && !kMergeOnly) {   // the rotation into LDS: hd * hd / 4 16-byte chunks, all loads first
         const int n16 = hd * hd / 4;
         for (int c0 = tid; c0 < n16; c0 += 16 * 256) {
             u32x4 v[16];
@@ -459,9 +462,17 @@ __global__ __launch_bounds__(256) void tq_attn_combine_kernel(
                     if (sp + u < ns[k]) sum[k] = fmaf(v[k][u], wts[hh[k] * nsplit + sp + u], sum[k]);
         }
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
-            if (idx0 + k * 256 < kCombHeads * hd) o[hh[k]][idx0 + k * 256 - hh[k] * hd] = sum[k] * linv[hh[k]];
+        for (int k = 0; k < 4; ++k) {
+            if (idx0 + k * 256 >= kCombHeads * hd) continue;
+            const float v = sum[k] * linv[hh[k]];
+            if constexpr (kMergeOnly) {
+                if (h0 + hh[k] < nvec) merged[(h0 + hh[k]) * hd + idx0 + k * 256 - hh[k] * hd] = v;
+            } else {
+                o[hh[k]][idx0 + k * 256 - hh[k] * hd] = v;
+            }
+        }
     }
+    if constexpr (kMergeOnly) return;
     __syncthreads();
     for (int idx = tid; idx < 2 * hd; idx += 256) {
         const int hg = idx / hd, i = idx - hg * hd;
@@ -1279,9 +1290,19 @@ int launch_attention(const AttnArgs& a, const Pages& pg, hipStream_t s) {
     float* ml = (float*)((char*)a.ws + off_ml);
     float* acc = (float*)((char*)a.ws + off_acc);
     const int nvec = a.nq * a.qh;
-    const unsigned rot_groups = (unsigned)ceil_div(nvec, kRotVecs);
-    hipLaunchKernelGGL(tq_attn_prerotate_kernel, dim3(rot_groups), dim3(256), 0, s,
-                       (const uint16_t*)a.q, a.krot, qrot, a.hd, nvec);
+    // Many vectors (prefill): both rotations as batched MFMA products (the VALU kernels'
+    // per-workgroup copies of Pi would cross L2 once per 8 vectors); the merged outputs reuse
+    // the q_rot buffer, which the split kernel has finished with.
+    const bool batched_rot = nvec >= kMfmaRotVecs && a.hd == 128 &&
+                             fhip_host::aligned16(a.q) && fhip_host::aligned16(a.out);
+    if (batched_rot) {
+        const int e = fhip_internal::tq_rotate_rows(a.q, a.krot, qrot, nvec, s);
+        if (e != hipSuccess) return e;
+    } else {
+        const unsigned rot_groups = (unsigned)ceil_div(nvec, kRotVecs);
+        hipLaunchKernelGGL(tq_attn_prerotate_kernel, dim3(rot_groups), dim3(256), 0, s,
+                           (const uint16_t*)a.q, a.krot, qrot, a.hd, nvec);
+    }
     if (a.kbits == 4 && a.vbits == 4 && a.hd == 128 && a.qh / a.kvh <= 8)
         launch_mfma_split(qrot, a.qs, pg, a.kcent, a.vcent, a.nq, a.qh, a.kvh, nsplit, ml, acc, s);
     else if (a.kbits == 4 && a.vbits == 4)
@@ -1290,10 +1311,19 @@ int launch_attention(const AttnArgs& a, const Pages& pg, hipStream_t s) {
         launch_split<4, 2>(a, pg, nsplit, ml, acc, s);
     else
         launch_split<0, 0>(a, pg, nsplit, ml, acc, s);
+    if (batched_rot) {
+        hipLaunchKernelGGL((tq_attn_combine_kernel<true, true>),
+                           dim3((unsigned)ceil_div(nvec, kCombHeads)), dim3(256),
+                           combine_lds_bytes(a.hd, nsplit, true), s, a.qs, ml, acc, a.vrot,
+                           (uint16_t*)a.out, a.qh, a.hd, nsplit, (int64_t)nvec, qrot);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return fhip_internal::tq_rotate_back_rows(qrot, a.vrot, a.out, nvec, s);
+    }
     auto comb = a.hd <= kRotLdsMaxHd ? tq_attn_combine_kernel<true> : tq_attn_combine_kernel<false>;
     hipLaunchKernelGGL(comb, dim3((unsigned)ceil_div(nvec, kCombHeads)), dim3(256),
                        combine_lds_bytes(a.hd, nsplit), s, a.qs, ml, acc, a.vrot,
-                       (uint16_t*)a.out, a.qh, a.hd, nsplit, (int64_t)nvec);
+                       (uint16_t*)a.out, a.qh, a.hd, nsplit, (int64_t)nvec, nullptr);
     return hipGetLastError();
 }
 

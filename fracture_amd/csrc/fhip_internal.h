@@ -20,4 +20,14 @@ int attention_tq_decode_ptrs_staged(void* output, const void* q, const int32_t* 
                                     int head_dim, int key_bits, int value_bits, void* workspace,
                                     hipStream_t stream);
 
+// Rows of 128: out[r] = Pi x[r] in fp32 from fp16 x (the compress kernel's MFMA rotation,
+// fp16 operands split hi / lo for fp32 accuracy, without normalisation).
+int tq_rotate_rows(const void* input, const float* rotation, float* out, int64_t rows,
+                   hipStream_t stream);
+
+// Rows of 128: out[r] = fp16(Pi^T y[r]) from fp32 y (the dequantize kernel's MFMA products,
+// y split into fp16 hi / lo operands).
+int tq_rotate_back_rows(const float* input, const float* rotation, void* out, int64_t rows,
+                        hipStream_t stream);
+
 }  // namespace fhip_internal

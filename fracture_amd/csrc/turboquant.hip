@@ -26,6 +26,7 @@
 // kernel's arithmetic.
 #include <type_traits>
 
+#include "fhip_internal.h"
 #include "tq_quant.h"
 
 using namespace fhip;
@@ -265,7 +266,8 @@ __device__ __forceinline__ void load_x_half(const uint16_t* __restrict__ in, int
 
 // ---------------------------------------------------------------------------------------
 // MFMA compress / rotate of one tile by one wave (head_dim 128).
-//   kMode 0: quantize + pack to Dst (kBits 2, 3, 4, 8);  kMode 1: fp32 y (and norms).
+//   kMode 0: quantize + pack to Dst (kBits 2, 3, 4, 8);  kMode 1: fp32 y (and norms);
+//   kMode 2: the raw fp32 product Pi x (no normalisation, no norms).
 // Lane (r, h) ends block c holding coordinates 32c + 8g + 4h + e (g, e = 0..3) of vector r
 // (accumulator element 4g + e); it quantizes them into half-groups (4 codes, 4*kBits bits,
 // MSB first). After the 4 blocks lane h owns groups [8h, 8h+8) of row r: 8*kBits contiguous
@@ -294,7 +296,7 @@ struct TileQuant {
     // quantizer issue the bucket-table read.
     __device__ __forceinline__ void a(const f32x16& acc, int c, int v) {
         y[v] = acc[v] * inv_s;
-        if constexpr (kMode == 1) {
+        if constexpr (kMode >= 1) {
             if ((v & 3) == 3 && yrow >= 0)
                 *(f32x4*)&y_out[yrow + 32 * c + 8 * (v >> 2) + 4 * (threadIdx.x >> 5 & 1)] =
                     f32x4{y[v - 3], y[v - 2], y[v - 1], y[v]};
@@ -332,14 +334,15 @@ __device__ __forceinline__ void compress_tile(const Quantizer& qz, const RotLds&
     const float nrm = sqrtf(ssq + partner_f(ssq));
     const float inv = 1.0f / (nrm + 1e-8f);
     const bool row_ok = r < nvalid;
-    if (h == 0 && row_ok) {
+    if (kMode != 2 && h == 0 && row_ok) {
         uint16_t* np = dst.nptr(m0 + r);
         if (np) *np = (uint16_t)f2h(nrm);
     }
     uint32_t half[16];  // kMode 0: half-group of group 4c + g held by this lane
     // Both fragment parts carry the factor 2^12 (hi stored as 2^12 Pi_hi), so hi and lo
     // products accumulate into one fp32 sum, 2^12 y_raw, scaled out with the norm.
-    TileQuant<kMode, kBits, kUnitFast> tq{qz, qz.scale, qz.offset, qz.jmax, inv * kLoInv,
+    TileQuant<kMode, kBits, kUnitFast> tq{qz, qz.scale, qz.offset, qz.jmax,
+                                          kMode == 2 ? kLoInv : inv * kLoInv,
                                           {}, {}, {}, half, y_out,
                                           row_ok ? (m0 + r) * kHd : -1};
     constexpr int kAhead = 2;
@@ -505,7 +508,7 @@ __device__ __forceinline__ void compress_planned(Quantizer& qz, RotLds& rl,
     rc.store(&rl);
     lds_barrier();
     load_x_half(in, first + nblk * kWavesC, ntiles, rows, xb);
-    if (kMode == 1 || qz.unit_fast)
+    if (kMode >= 1 || qz.unit_fast)
         compress_waves<kMode, kBits, true>(qz, rl, in, dst, y_out, rows, xa, xb, blk, nblk);
     else
         compress_waves_general<kMode, kBits>(qz, rl, in, dst, y_out, rows, blk, nblk);
@@ -548,7 +551,7 @@ tq_compress_mfma_kernel(const uint16_t* __restrict__ in, const float* __restrict
     rs.store(rl);
     lds_barrier();
     load_x_half(in, first + (int64_t)gridDim.x * kWavesC, ntiles, rows, xb);
-    if (kMode == 1 || qz.unit_fast)
+    if (kMode >= 1 || qz.unit_fast)
         compress_waves<kMode, kBits, true>(qz, rl, in, dst, y_out, rows, xa, xb, blockIdx.x,
                                            gridDim.x);
     else
@@ -761,15 +764,12 @@ __device__ __forceinline__ void decode_group(const DequantLds& t, const CodeHalf
 // Lane (r, h) ends block c holding coordinates 32c + 8g + 4h + e of row r; neighbouring
 // chunks are exchanged with the partner lane so every lane stores 16 contiguous bytes.
 // ---------------------------------------------------------------------------------------
-template <int kBits>
-__device__ __forceinline__ void dequant_tile(const DequantLds& t, const RotLds& L,
-                                             const CodeHalf<kBits>& cw,
-                                             uint16_t* __restrict__ out, int64_t m0, int nvalid) {
+// x = Pi^T y of the lane's row from the (hi, lo') B fragments of y, stored as fp16(x * nrm).
+__device__ __forceinline__ void rotate_back_store(const RotLds& L, const f16x8 (&bh)[8],
+                                                  const f16x8 (&bl)[8], float nrm,
+                                                  uint16_t* __restrict__ out, int64_t m0,
+                                                  int nvalid) {
     const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
-    f16x8 bh[8], bl[8];
-#pragma unroll
-    for (int s = 0; s < 8; ++s) decode_group<kBits>(t, cw, s, bh[s], bl[s]);
-    const float nrm = h2f(cw.norm);
     uint16_t* orow = out + m0 * kHd + (r * kHd + 8 * h);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -802,6 +802,82 @@ __device__ __forceinline__ void dequant_tile(const DequantLds& t, const RotLds& 
                 *(u32x4*)&orow[32 * c + 16 * m] =
                     u32x4{ch[2 * m][0], ch[2 * m][1], ch[2 * m + 1][0], ch[2 * m + 1][1]};
         }
+    }
+}
+template <int kBits>
+__device__ __forceinline__ void dequant_tile(const DequantLds& t, const RotLds& L,
+                                             const CodeHalf<kBits>& cw,
+                                             uint16_t* __restrict__ out, int64_t m0, int nvalid) {
+    f16x8 bh[8], bl[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) decode_group<kBits>(t, cw, s, bh[s], bl[s]);
+    rotate_back_store(L, bh, bl, h2f(cw.norm), out, m0, nvalid);
+}
+
+// ---------------------------------------------------------------------------------------
+// x = Pi^T y for fp32 rows y [rows, 128] -> fp16 (the attention combine's unrotation of the
+// merged outputs, attention_paged_tq.cu:245-257, for batches of many vectors): each lane's
+// 64 values of its row split into fp16 (hi, lo') operands as the dequantize tables split the
+// centroids (y = hi + 2^-12 lo'), then the dequantize kernel's three products per step.
+// ---------------------------------------------------------------------------------------
+struct RowHalf {
+    f32x4 v[16];  // coordinates 64 h + 4 i .. + 3 of the lane's row
+};
+__device__ __forceinline__ void load_row_half(const float* __restrict__ y, int64_t tile,
+                                              int64_t ntiles, int64_t rows, RowHalf& rh) {
+    const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
+    const int64_t m0 = tile * kTile;
+    // rows past the end read row 0 (their results are not stored)
+    const int64_t row = tile < ntiles && r < rows - m0 ? m0 + r : 0;
+    const float* src = y + row * kHd + 64 * h;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) rh.v[i] = *(const f32x4*)(src + 4 * i);
+}
+__device__ __forceinline__ void rotate_back_tile(const RotLds& L, const RowHalf& rh,
+                                                 uint16_t* __restrict__ out, int64_t m0,
+                                                 int nvalid) {
+    f16x8 bh[8], bl[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            uint32_t hb[2], lb[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const float x = rh.v[2 * s + p / 2][2 * (p % 2) + e];
+                const _Float16 hi = (_Float16)x;
+                hb[e] = __builtin_bit_cast(uint16_t, hi);
+                lb[e] = __builtin_bit_cast(uint16_t, (_Float16)((x - (float)hi) * kLoScale));
+            }
+            hw[p] = hb[0] | (hb[1] << 16);
+            lw[p] = lb[0] | (lb[1] << 16);
+        }
+        bh[s] = __builtin_bit_cast(f16x8, u32x4{hw[0], hw[1], hw[2], hw[3]});
+        bl[s] = __builtin_bit_cast(f16x8, u32x4{lw[0], lw[1], lw[2], lw[3]});
+    }
+    rotate_back_store(L, bh, bl, 1.0f, out, m0, nvalid);
+}
+constexpr int kWavesR = 4;  // waves per workgroup of the back-rotation (two workgroups per CU)
+__global__ __launch_bounds__(64 * kWavesR) __attribute__((amdgpu_waves_per_eu(2))) void
+tq_rotate_back_kernel(const float* __restrict__ y, const float* __restrict__ rot,
+                      uint16_t* __restrict__ out, int64_t rows) {
+    __shared__ RotLds rl;
+    const int64_t ntiles = ceil_div(rows, kTile);
+    const int64_t stride = (int64_t)gridDim.x * kWavesR;
+    int64_t tile = (int64_t)blockIdx.x * kWavesR + wave_id();
+    RotStage<true, 64 * kWavesR, false> rs;
+    rs.load(rot);
+    RowHalf ra;
+    load_row_half(y, tile, ntiles, rows, ra);
+    rs.store(rl);
+    lds_barrier();
+    while (tile < ntiles) {
+        RowHalf rb;
+        load_row_half(y, tile + stride, ntiles, rows, rb);
+        rotate_back_tile(rl, ra, out, tile * kTile, (int)min<int64_t>(kTile, rows - tile * kTile));
+        ra = rb;
+        tile += stride;
     }
 }
 
@@ -1026,7 +1102,7 @@ int launch_compress(const void* input, const float* rot, const float* cent, int 
                     Dst dst, float* y_out, int64_t rows, int hd, hipStream_t s,
                     const TqPlanDev* plan = nullptr) {
     if (rows == 0) return hipSuccess;
-    const bool mfma_bits = kMode == 1 || bits == 2 || bits == 3 || bits == 4 || bits == 8;
+    const bool mfma_bits = kMode >= 1 || bits == 2 || bits == 3 || bits == 4 || bits == 8;
     if (hd == kHd && mfma_bits && fhip_host::aligned16(input) &&
         (kMode == 0 || fhip_host::aligned16(y_out))) {
         auto pick = [&](auto planned) {
@@ -1046,6 +1122,8 @@ int launch_compress(const void* input, const float* rot, const float* cent, int 
         hipLaunchKernelGGL(kern, dim3(mfma_grid(ceil_div(rows, kTile), kWavesC)),
                            dim3(64 * kWavesC), 0, s, (const uint16_t*)input, rot, cent, L, plan,
                            dst, y_out, rows);
+    } else if constexpr (kMode == 2) {
+        return hipErrorInvalidValue;  // the raw product exists for head_dim 128 only
     } else {
         const int grid = tq_grid(rows, 2048);
         const size_t lds = 2 * (size_t)hd * sizeof(float);
@@ -1156,6 +1234,36 @@ int fhip_launch_turboquant_compress(const void* input, const float* rotation,
     return launch_compress<0>(input, rotation, centroids, n_levels, bits, dst, nullptr, rows,
                               head_dim, fhip_host::as_stream(stream));
 }
+
+}  // extern "C"
+
+namespace fhip_internal {
+
+int tq_rotate_rows(const void* input, const float* rotation, float* out, int64_t rows,
+                   hipStream_t stream) {
+    if (rows < 0 || !input || !rotation || !out || !fhip_host::aligned16(input) ||
+        !fhip_host::aligned16(out))
+        return hipErrorInvalidValue;
+    FlatDst dst{nullptr, nullptr, 0};
+    return launch_compress<2>(input, rotation, nullptr, 0, 8, dst, out, rows, kHd, stream);
+}
+
+int tq_rotate_back_rows(const float* input, const float* rotation, void* out, int64_t rows,
+                        hipStream_t stream) {
+    if (rows < 0 || !input || !rotation || !out || !fhip_host::aligned16(input) ||
+        !fhip_host::aligned16(out))
+        return hipErrorInvalidValue;
+    if (rows == 0) return hipSuccess;
+    const int64_t need = ceil_div(ceil_div(rows, kTile), kWavesR);
+    const int64_t cap = 2 * (int64_t)fhip_host::cu_count();
+    hipLaunchKernelGGL(tq_rotate_back_kernel, dim3((unsigned)(need < cap ? need : cap)),
+                       dim3(64 * kWavesR), 0, stream, input, rotation, (uint16_t*)out, rows);
+    return hipGetLastError();
+}
+
+}  // namespace fhip_internal
+
+extern "C" {
 
 int fhip_launch_tq_rotate(const void* input, const float* rotation, float* y_out,
                           void* norms_out, int rows, int head_dim, fhip_stream_t stream) {
