@@ -739,15 +739,52 @@ def paged_inputs(torch, K, dev):
     return fn, nb, tok, float(lens.mean())
 
 
+def paged_prefill_inputs(torch, K, dev, T, kv_len):
+    """FP16 causal prefill of T queries at positions kv_len - T .. kv_len - 1 of one sequence
+    through the reference-signature launcher (per-page address arrays, 32/8 heads, hd 128):
+    returns (fn, algorithmic bytes, positions scored per kv head)."""
+    import numpy as np
+
+    QH, KVH, HD = ATT_SHAPE["QH"], ATT_SHAPE["KVH"], ATT_SHAPE["HD"]
+    nb = (kv_len + 15) // 16
+    P = nb + 3
+    g = torch.Generator(device=dev)
+    g.manual_seed(T + kv_len)
+    kp = torch.randn((P, 16, KVH, HD), generator=g, device=dev, dtype=torch.float16)
+    vp = torch.randn((P, 16, KVH, HD), generator=g, device=dev, dtype=torch.float16)
+    kptr = torch.tensor([kp[i].data_ptr() for i in range(P)], dtype=torch.int64, device=dev)
+    vptr = torch.tensor([vp[i].data_ptr() for i in range(P)], dtype=torch.int64, device=dev)
+    table = torch.from_numpy(np.random.default_rng(2).permutation(P)[:nb].astype(np.int32)).to(dev)
+    q = torch.randn((T, QH, HD), generator=g, device=dev).to(torch.float16)
+    out = torch.empty_like(q)
+    ws = K.attention_paged_workspace(T, QH, HD, nb, dev)
+    fn = lambda: K.paged_attention(out, q, table, kptr, vptr, KVH, kv_len, kv_len - T, ws)
+    scored = sum(min(kv_len - T + t + 1, kv_len) for t in range(T))
+    nbytes = kv_len * KVH * HD * 2 * 2 + 2 * T * QH * HD * 2 + nb * 4
+    return fn, nbytes, scored
+
+
 def run_paged(args, torch, K, dev):
     fn, nb, tok, mean = paged_inputs(torch, K, dev)
     us = Timer(torch).time_us(fn, 10, warmup=2)
-    return {"workload": "FP16 paged decode attention, B=64, 32/8 heads, hd 128",
-            "kernels": {"attention_paged_decode": {
-                "us": round(us, 1), "GB/s": round(gbs(nb, us), 1),
-                "frac_of_peak": round(gbs(nb, us) / PEAK_HBM_GBS, 4), "bytes": nb,
-                "context_tokens": tok, "mean_ctx": mean,
-                "traffic": traffic_of("attention_paged_decode")}}}
+    kernels = {"attention_paged_decode": {
+        "us": round(us, 1), "GB/s": round(gbs(nb, us), 1),
+        "frac_of_peak": round(gbs(nb, us) / PEAK_HBM_GBS, 4), "bytes": nb,
+        "context_tokens": tok, "mean_ctx": mean,
+        "traffic": traffic_of("attention_paged_decode")}}
+    for T, kv_len in ((2048, 2048), (512, 8192)):
+        pfn, pnb, scored = paged_prefill_inputs(torch, K, dev, T, kv_len)
+        pus = Timer(torch).time_us(pfn, 5, warmup=2)
+        kernels[f"attention_paged_prefill_T{T}_ctx{kv_len}"] = {
+            "us": round(pus, 1), "GB/s": round(gbs(pnb, pus), 1),
+            "frac_of_peak": round(gbs(pnb, pus) / PEAK_HBM_GBS, 5), "bytes": pnb,
+            "positions_scored_per_kv_head": scored,
+            "Gpos/s": round(scored * ATT_SHAPE["KVH"] / pus / 1e3, 2),
+            "note": "causal prefill through fhip_launch_paged_attention_ws; bytes are the "
+                    "distinct K/V pages, queries and outputs (each page is re-read by every "
+                    "group of 8 / G queries)"}
+    return {"workload": "FP16 paged decode attention, B=64, 32/8 heads, hd 128; causal "
+                        "prefill of one sequence", "kernels": kernels}
 
 
 # ---------------------------------------------------------------------------------------

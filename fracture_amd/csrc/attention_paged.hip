@@ -9,8 +9,10 @@
 // online softmax each, merged by a second kernel: up to 1,048,576 positions per sequence.
 //
 // Work split: one wave per (query, kv head, block of up to 8 of its q heads, split). Each K
-// row crosses HBM once per (query, kv head) for up to 8 q heads. Per 32-position chunk
-// (16 when head_dim is 256):
+// row crosses HBM once per (query, kv head) for up to 8 q heads. In causal prefill with fewer
+// than 8 q heads per kv head, a wave takes 8 / G consecutive queries instead, its columns
+// being (query, head) pairs each masked to its own causal length, so that a K or V row is
+// read once for all of them. Per 32-position chunk (16 when head_dim is 256):
 //   QK on v_mfma_f32_16x16x32_f16: A = K rows (row = position, 8 consecutive dims per lane,
 //      exactly their memory layout), B = Q^T (column = q head): fp16 x fp16 products are
 //      exact in fp32, the sums are fp32;
@@ -106,7 +108,7 @@ template <int HD, int NH, class Pages>
 __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2))) void
 paged_attn_split_kernel(const uint16_t* __restrict__ q, PQueries qs, Pages pg, int qh, int kvh,
                         int nhb, float scale_log2, float* __restrict__ part_ml,
-                        float* __restrict__ part_acc, int nsplit) {
+                        float* __restrict__ part_acc, int nsplit, int tok) {
     constexpr int kChunk = HD <= 128 ? 32 : 16;  // positions per chunk
     constexpr int kTiles = kChunk / 16;          // 16-position MFMA tiles (= pages) per chunk
     constexpr int kSteps = HD / 32;              // MFMA steps per tile
@@ -125,20 +127,25 @@ paged_attn_split_kernel(const uint16_t* __restrict__ q, PQueries qs, Pages pg, i
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t item = (int64_t)blockIdx.x * kPWaves + wave;
     const int64_t per_q = (int64_t)kvh * nhb * nsplit;
-    const int qi = (int)(item / per_q);
-    if (qi >= qs.count) return;
+    // queries tq0 .. tq0 + ntok - 1 (tok > 1 only in causal prefill over one shared table
+    // with nhb == 1, where causal lengths grow with the query index)
+    const int tq0 = (int)(item / per_q) * tok;
+    if (tq0 >= qs.count) return;
+    const int ntok = min(tok, qs.count - tq0);
     // kv head fastest: waves of one workgroup read neighbouring rows of the same pages
     const int g = (int)(item % kvh);
     const int hb = (int)((item / kvh) % nhb);
     const int split = (int)((item / ((int64_t)kvh * nhb)) % nsplit);
-    const int clen = qs.causal_len(qi);
+    const int clen = qs.causal_len(tq0 + ntok - 1);
     const int t_begin = split * kPSplit;
     if (t_begin >= clen) return;
     const int t_end = min(clen, t_begin + kPSplit);
     const int G = qh / kvh;
     const int h0 = g * G + hb * kHeadsMax;
-    const int nh = min(kHeadsMax, G - hb * kHeadsMax);  // <= NH
-    const int32_t* table = qs.table + (int64_t)qi * qs.table_stride;
+    // MFMA columns (<= NH): with tok == 1 heads h0 .. h0 + ncols - 1 of query tq0, else
+    // column c is head h0 + c % G of query tq0 + c / G
+    const int ncols = tok > 1 ? ntok * G : min(kHeadsMax, G - hb * kHeadsMax);
+    const int32_t* table = qs.table + (int64_t)tq0 * qs.table_stride;
 
     // the split's pages, one per lane, read once
     static_assert(kPSplit == 64 * FHIP_PAGE_TOKENS, "one cached page per lane");
@@ -146,16 +153,21 @@ paged_attn_split_kernel(const uint16_t* __restrict__ q, PQueries qs, Pages pg, i
         t_begin + FHIP_PAGE_TOKENS * lane < t_end ? table[t_begin / FHIP_PAGE_TOKENS + lane] : -1;
     const typename Pages::Lane pl = pg.lane_load(split_page);
 
-    // Q^T as the QK B operand: lane (column n, k group kg) holds q[h0 + n][32 s + 8 kg + 0..7]
-    // at step s; columns n >= nh are zero.
+    // Q^T as the QK B operand: lane (column n, k group kg) holds dims 32 s + 8 kg + 0..7 of
+    // column n's query row at step s; columns n >= ncols are zero and fully masked.
     const int n = lane & 15, kg = lane >> 4;
+    const bool col_ok = n < ncols;
+    const int ct = col_ok ? n / G : 0;  // 0 whenever tok == 1 (n < ncols <= G)
+    const int hn = col_ok ? n - ct * G : 0;
+    const int col_len = !col_ok ? 0 : tok > 1 ? qs.causal_len(tq0 + ct) : clen;
+    const int lim = min(t_end, col_len);  // column n scores positions below lim
     u32x4 bq[kSteps];
     {
-        const uint16_t* qrow = q + ((int64_t)qi * qh + h0 + (n < nh ? n : 0)) * HD + 8 * kg;
+        const uint16_t* qrow = q + ((int64_t)(tq0 + ct) * qh + h0 + hn) * HD + 8 * kg;
 #pragma unroll
         for (int s = 0; s < kSteps; ++s) {
             const u32x4 v = ld16(qrow + 32 * s);
-            bq[s] = n < nh ? v : u32x4{0u, 0u, 0u, 0u};
+            bq[s] = col_ok ? v : u32x4{0u, 0u, 0u, 0u};
         }
     }
     // lane offsets inside a page: K row (lane & 15) segment kg; V row of position subset ps,
@@ -218,7 +230,7 @@ paged_attn_split_kernel(const uint16_t* __restrict__ q, PQueries qs, Pages pg, i
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int pos = t0 + 16 * tt + 4 * kg + e;
-                sc[tt][e] = pok[tt] && pos < t_end ? d[e] * scale_log2 : -__builtin_inff();
+                sc[tt][e] = pok[tt] && pos < lim ? d[e] * scale_log2 : -__builtin_inff();
             }
         }
         // ---- online softmax per head (lanes n, n + 16, n + 32, n + 48 share head n)
@@ -293,18 +305,25 @@ paged_attn_split_kernel(const uint16_t* __restrict__ q, PQueries qs, Pages pg, i
         for (int h = 0; h < NH; ++h)
 #pragma unroll
             for (int i = 0; i < 8; ++i) acc[h][i] += __shfl_xor(acc[h][i], o);
-    const int64_t v0 = (int64_t)qi * qh + h0;
-    if (lane < nh) {
-        part_ml[((v0 + lane) * nsplit + split) * 2 + 0] = m_run * 0.6931471805599453f;
-        part_ml[((v0 + lane) * nsplit + split) * 2 + 1] = l_run;
+    // column c's vector: (query tq0 + c / G, head h0 + c % G)
+    if (lane < ncols) {  // lane == n here
+        const int64_t v = (int64_t)(tq0 + ct) * qh + h0 + hn;
+        part_ml[(v * nsplit + split) * 2 + 0] = m_run * 0.6931471805599453f;
+        part_ml[(v * nsplit + split) * 2 + 1] = l_run;
     }
     if (ps == 0) {
+        int hc = 0, hh = 0;  // column h is head h0 + hh of query tq0 + hc
 #pragma unroll
         for (int h = 0; h < NH; ++h) {
-            if (h < nh) {
-                float* dst = part_acc + ((v0 + h) * nsplit + split) * HD + 8 * dg;
+            if (h < ncols) {
+                const int64_t v = (int64_t)(tq0 + hc) * qh + h0 + hh;
+                float* dst = part_acc + (v * nsplit + split) * HD + 8 * dg;
                 *(f4_t*)dst = f4_t{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
                 *(f4_t*)(dst + 4) = f4_t{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
+            }
+            if (++hh == G) {
+                hh = 0;
+                ++hc;
             }
         }
     }
@@ -380,20 +399,22 @@ bool paged_shape_ok(int qh, int kvh, int hd) {
 
 template <int HD, int NH, class Pages>
 void launch_split_t(const uint16_t* q, const PQueries& qs, const Pages& pg, int qh, int kvh,
-                    int nhb, float* ml, float* acc, int nsplit, int64_t groups, hipStream_t s) {
+                    int nhb, float* ml, float* acc, int nsplit, int tok, int64_t groups,
+                    hipStream_t s) {
     const float scale_log2 = 1.4426950408889634f / sqrtf((float)HD);
     hipLaunchKernelGGL((paged_attn_split_kernel<HD, NH, Pages>), dim3((unsigned)groups),
                        dim3(64 * kPWaves), 0, s, q, qs, pg, qh, kvh, nhb, scale_log2, ml, acc,
-                       nsplit);
+                       nsplit, tok);
 }
 
 template <int HD, class Pages>
 void launch_split_hd(const uint16_t* q, const PQueries& qs, const Pages& pg, int qh, int kvh,
-                     int nhb, float* ml, float* acc, int nsplit, int64_t groups, hipStream_t s) {
-    if (qh / kvh <= 4)
-        launch_split_t<HD, 4>(q, qs, pg, qh, kvh, nhb, ml, acc, nsplit, groups, s);
+                     int nhb, float* ml, float* acc, int nsplit, int tok, int64_t groups,
+                     hipStream_t s) {
+    if (qh / kvh * tok <= 4)
+        launch_split_t<HD, 4>(q, qs, pg, qh, kvh, nhb, ml, acc, nsplit, tok, groups, s);
     else
-        launch_split_t<HD, 8>(q, qs, pg, qh, kvh, nhb, ml, acc, nsplit, groups, s);
+        launch_split_t<HD, 8>(q, qs, pg, qh, kvh, nhb, ml, acc, nsplit, tok, groups, s);
 }
 
 template <class Pages>
@@ -405,18 +426,31 @@ int launch_paged(void* out, const void* q, const PQueries& qs, int nq, const Pag
     paged_ws_layout(nq, qh, hd, qs.max_blocks * FHIP_PAGE_TOKENS, &off_acc, &nsplit);
     float* ml = (float*)ws;
     float* acc = (float*)((char*)ws + off_acc);
-    const int nhb = (qh / kvh + kHeadsMax - 1) / kHeadsMax;
-    const int64_t items = (int64_t)nq * kvh * nhb * nsplit;
+    const int G = qh / kvh;
+    const int nhb = (G + kHeadsMax - 1) / kHeadsMax;
+    // causal prefill over one shared table: 8 / G consecutive queries per wave
+    const int tok = (!qs.seq_lens && qs.table_stride == 0 && nq > 1 && G < kHeadsMax)
+                        ? kHeadsMax / G
+                        : 1;
+    const int64_t items = ceil_div((int64_t)nq, tok) * kvh * nhb * nsplit;
     const int64_t groups = ceil_div(items, kPWaves);
     if (groups > 0x7fffffff || (int64_t)nq * qh > 0x7fffffff) return hipErrorInvalidValue;
     PQueries q2 = qs;
     q2.count = nq;
     const uint16_t* qp = (const uint16_t*)q;
     switch (hd) {
-        case 32: launch_split_hd<32>(qp, q2, pg, qh, kvh, nhb, ml, acc, nsplit, groups, s); break;
-        case 64: launch_split_hd<64>(qp, q2, pg, qh, kvh, nhb, ml, acc, nsplit, groups, s); break;
-        case 128: launch_split_hd<128>(qp, q2, pg, qh, kvh, nhb, ml, acc, nsplit, groups, s); break;
-        default: launch_split_hd<256>(qp, q2, pg, qh, kvh, nhb, ml, acc, nsplit, groups, s); break;
+        case 32:
+            launch_split_hd<32>(qp, q2, pg, qh, kvh, nhb, ml, acc, nsplit, tok, groups, s);
+            break;
+        case 64:
+            launch_split_hd<64>(qp, q2, pg, qh, kvh, nhb, ml, acc, nsplit, tok, groups, s);
+            break;
+        case 128:
+            launch_split_hd<128>(qp, q2, pg, qh, kvh, nhb, ml, acc, nsplit, tok, groups, s);
+            break;
+        default:
+            launch_split_hd<256>(qp, q2, pg, qh, kvh, nhb, ml, acc, nsplit, tok, groups, s);
+            break;
     }
     hipLaunchKernelGGL(paged_attn_combine_kernel, dim3((unsigned)((int64_t)nq * qh)),
                        dim3(kCombThreads), (size_t)nsplit * sizeof(float), s, q2, ml, acc,

@@ -432,16 +432,25 @@ def attention_paged_decode(out: torch.Tensor, q: torch.Tensor, block_table: torc
 
 def paged_attention(out: torch.Tensor, q: torch.Tensor, block_table: torch.Tensor,
                     k_block_ptrs: torch.Tensor, v_block_ptrs: torch.Tensor, num_kv_heads: int,
-                    kv_len: int, start_pos: int) -> None:
+                    kv_len: int, start_pos: int, workspace: torch.Tensor | None = None) -> None:
     """The reference interface (attention_paged.cu:172-185): T causal queries of one sequence;
-    block_table [nblocks] int32; k/v_block_ptrs int64 device arrays of block addresses."""
+    block_table [nblocks] int32; k/v_block_ptrs int64 device arrays of block addresses. With
+    `workspace` (attention_paged_workspace(T, qh, hd, nblocks)) nothing is allocated."""
     _dev(out, q, block_table, k_block_ptrs, v_block_ptrs)
     _need(q.dtype == torch.float16 and q.dim() == 3 and out.shape == q.shape, "q/out")
     _need(block_table.dtype == torch.int32 and block_table.dim() == 1, "block_table")
     T, qh, hd = q.shape
-    _ok(_L().fhip_launch_paged_attention(
+    if workspace is None:
+        _ok(_L().fhip_launch_paged_attention(
+            _p(out), _p(q), _p(block_table), _p(k_block_ptrs), _p(v_block_ptrs), T, qh,
+            num_kv_heads, hd, kv_len, start_pos, block_table.numel(), _stream()),
+            "paged_attention")
+        return
+    _dev(workspace)
+    _ok(_L().fhip_launch_paged_attention_ws(
         _p(out), _p(q), _p(block_table), _p(k_block_ptrs), _p(v_block_ptrs), T, qh,
-        num_kv_heads, hd, kv_len, start_pos, block_table.numel(), _stream()), "paged_attention")
+        num_kv_heads, hd, kv_len, start_pos, block_table.numel(), _p(workspace),
+        C.c_size_t(workspace.numel()), _stream()), "paged_attention")
 
 
 def matmul(c: torch.Tensor, a: torch.Tensor, b: torch.Tensor) -> None:

@@ -115,13 +115,17 @@ def test_decode_empty_sequence_and_masked_pages(dev):
     assert_close(got[2].astype(np.float32), want2.astype(np.float32), 1e-3, 1e-3, "seq 2")
 
 
-@pytest.mark.parametrize("kv_len,T,start_pos", [(90, 6, 84), (40, 5, 38), (1030, 3, 1027),
-                                                (16, 1, 15)])
-def test_reference_interface_prefill_causal(dev, kv_len, T, start_pos):
+@pytest.mark.parametrize("kv_len,T,start_pos,qh,kvh,hd", [
+    (90, 6, 84, 8, 2, 64), (40, 5, 38, 8, 2, 64), (1030, 3, 1027, 8, 2, 64),
+    (16, 1, 15, 8, 2, 64),
+    # 8 / G queries per wave: ragged last groups, groups whose lengths straddle a page or
+    # the 1024-position split edge, whole prefills from position 0
+    (1050, 19, 1020, 4, 4, 128), (300, 13, 0, 8, 4, 32), (1100, 11, 1019, 6, 2, 256),
+    (70, 70, 0, 8, 2, 128), (2100, 9, 2040, 16, 16, 64), (50, 7, 43, 16, 2, 64)])
+def test_reference_interface_prefill_causal(dev, kv_len, T, start_pos, qh, kvh, hd):
     """fhip_launch_paged_attention: T queries at start_pos.. over per-block pointer arrays;
     query i attends to min(start_pos + i + 1, kv_len) positions."""
     rng = np.random.default_rng(kv_len + T)
-    qh, kvh, hd = 8, 2, 64
     kp, vp, table = build_pool(rng, [kv_len], kvh, hd, extra_pages=2)
     P = kp.shape[0]
     tk, tv = dev_t(kp, dev), dev_t(vp, dev)
@@ -130,9 +134,16 @@ def test_reference_interface_prefill_causal(dev, kv_len, T, start_pos):
     q = (rng.standard_normal((T, qh, hd)) * 2).astype(np.float16)
     tq_ = dev_t(q, dev)
     out = torch.empty_like(tq_)
-    K.paged_attention(out, tq_, dev_t(table[0], dev), kptr, vptr, kvh, kv_len, start_pos)
+    tb = dev_t(table[0], dev)
+    K.paged_attention(out, tq_, tb, kptr, vptr, kvh, kv_len, start_pos)
     torch.cuda.synchronize()
     got = out.cpu().numpy()
+    # the caller-workspace form launches the same kernels
+    ws = K.attention_paged_workspace(T, qh, hd, table.shape[1], dev)
+    out2 = torch.empty_like(tq_)
+    K.paged_attention(out2, tq_, tb, kptr, vptr, kvh, kv_len, start_pos, ws)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out2.cpu().numpy().view(np.uint16), got.view(np.uint16))
     for t in range(T):
         clen = min(start_pos + t + 1, kv_len)
         want = oracle.paged_attention(q[t], table[0], clen, kp, vp, kvh)
