@@ -159,3 +159,77 @@ def test_fixture_greedy_tokens(dev, golden, case):
     torch.cuda.synchronize()
     assert int(idx.cpu().numpy()[-1]) == int(golden[f"{case}/greedy_token"][0])
     assert np.array_equal(idx.cpu().numpy(), oracle.argmax_rows(l)[0].astype(np.int32))
+
+
+
+def _check_softmax(p, l, what):
+    ref = oracle.softmax_rows(l)
+    np.testing.assert_allclose(p, ref / ref.sum(1, dtype=np.float64, keepdims=True),
+                               rtol=1e-5, atol=1e-12, err_msg=what)
+
+
+def test_shared_workspace_across_shapes(dev):
+    """Calls of every op and shape in a row on one workspace sized for the largest."""
+    ws = K.rows_workspace(64, 128256, dev)
+    shapes = [(64, 128256), (3, 1000), (5, 4097), (64, 128256), (1, 1), (2, 7), (64, 32000),
+              (7, 8193), (64, 128256)]
+    for i, (rows, cols) in enumerate(shapes):
+        l, _ = spiky_logits(rows, cols, 100 + i)
+        tl = torch.from_numpy(l).to(dev)
+        want, _ = oracle.argmax_rows(l)
+        p = torch.empty_like(tl)
+        idx = torch.empty(rows, dtype=torch.int32, device=dev)
+        fl = torch.empty(rows, dtype=torch.int32, device=dev)
+        K.softmax_rows(tl, p, 1.0, ws)
+        torch.cuda.synchronize()
+        _check_softmax(p.cpu().numpy(), l, f"softmax {rows}x{cols}")
+        K.argmax_rows(tl, idx, fl, ws)
+        torch.cuda.synchronize()
+        assert np.array_equal(idx.cpu().numpy(), want.astype(np.int32)), f"argmax {rows}x{cols}"
+        p.zero_()
+        idx.zero_()
+        K.softmax_argmax_rows(tl, p, idx, fl, 1.0, ws)
+        torch.cuda.synchronize()
+        _check_softmax(p.cpu().numpy(), l, f"fused {rows}x{cols}")
+        assert np.array_equal(idx.cpu().numpy(), want.astype(np.int32)), f"fused {rows}x{cols}"
+
+
+def test_softmax_many_rows(dev):
+    """1536 rows of 32,000 columns: more chunk workgroups than the device holds at once."""
+    rows, cols = 1536, 32000
+    l, _ = spiky_logits(rows, cols, 9)
+    p, idx, fl = run_softmax(l, dev)
+    _check_softmax(p, l, "many rows")
+    assert np.array_equal(idx, oracle.argmax_rows(l)[0].astype(np.int32))
+
+
+def test_softmax_argmax_graph_replays(dev):
+    """Captured once, replayed with new logits between replays (eager work and host
+    synchronisation in between): every replay equals an eager call on the same logits."""
+    rows, cols = 64, 128256
+    tl = torch.empty((rows, cols), dtype=torch.float32, device=dev)
+    p = torch.empty_like(tl)
+    idx = torch.empty(rows, dtype=torch.int32, device=dev)
+    fl = torch.empty_like(idx)
+    ws = K.rows_workspace(rows, cols, dev)
+    tl.copy_(torch.from_numpy(spiky_logits(rows, cols, 0)[0]))
+    K.softmax_argmax_rows(tl, p, idx, fl, 1.0, ws)  # warm-up outside capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            K.softmax_argmax_rows(tl, p, idx, fl, 1.0, ws)
+    torch.cuda.synchronize()
+    ws_e = K.rows_workspace(rows, cols, dev)
+    pe, idxe, fle = torch.empty_like(p), torch.empty_like(idx), torch.empty_like(fl)
+    for rep in range(4):
+        l, _ = spiky_logits(rows, cols, 50 + rep)
+        tl.copy_(torch.from_numpy(l))
+        g.replay()
+        torch.cuda.synchronize()
+        K.softmax_argmax_rows(tl, pe, idxe, fle, 1.0, ws_e)
+        torch.cuda.synchronize()
+        assert np.array_equal(p.cpu().numpy().view(np.uint32), pe.cpu().numpy().view(np.uint32)), rep
+        assert np.array_equal(idx.cpu().numpy(), idxe.cpu().numpy()), rep
+        assert np.array_equal(idx.cpu().numpy(), oracle.argmax_rows(l)[0].astype(np.int32)), rep
