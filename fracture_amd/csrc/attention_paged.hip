@@ -329,6 +329,222 @@ paged_attn_split_kernel(const uint16_t* __restrict__ q, PQueries qs, Pages pg, i
     }
 }
 
+// Causal prefill groups with PV on the MFMA as well (head_dim 32 / 64 / 128, G < 8 q heads per
+// kv head, 8 / G queries per wave as above). Per 32-position chunk:
+//   QK as in paged_attn_split_kernel, except that MFMA columns 8..15 repeat columns 0..7, so a
+//     lane n >= 8 holds the same scores and probabilities as lane n - 8;
+//   PV on v_mfma_f32_16x16x32_f16: out[col][d] += P[col][slot] V[slot][d]. Slot 8q + i of
+//     lane group q is position 4q + i (i < 4) or 16 + 4q + i - 4: exactly the positions whose
+//     probabilities that lane group holds after QK, so A needs no data movement. Row m < 8 of
+//     A is fp16(p) of column m, row 8 + m is fp16((p - fp16(p)) 2^12), and the output is
+//     D[m] + 2^-12 D[8 + m]: fp32 weights to ~2^-22, V exact.
+//   B = V transposed: the chunk's V rows are staged in LDS row-major (rows padded so that the
+//     four rows one transposed read gathers sit on different banks), and
+//     ds_read_b64_tr_b16 gives lane (d, q) dim d of the 4 positions addressed by source
+//     lanes a + 4k of its 16-lane group (destination lane 4a + b takes element b of each).
+template <int HD, class Pages>
+__global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2))) void
+paged_attn_prefill_mfma_kernel(const uint16_t* __restrict__ q, PQueries qs, Pages pg, int qh,
+                               int kvh, float scale_log2, float* __restrict__ part_ml,
+                               float* __restrict__ part_acc, int nsplit, int tok) {
+    constexpr int kChunk = 32;
+    constexpr int kTiles = 2;
+    constexpr int kSteps = HD / 32;
+    constexpr int kBlk = HD / 16;  // PV output dim blocks
+    constexpr int kDg = HD / 8;    // lanes per V row load, 8 dims each
+    constexpr int kPpl = 64 / kDg;
+    constexpr int kVLoads = kChunk / kPpl;
+    constexpr int kRow = HD * 2 + 32;  // bytes per staged V row
+    static_assert(HD >= 32 && HD <= 128, "head_dim 32, 64 or 128");
+    __shared__ __attribute__((aligned(16))) uint8_t vbuf[kPWaves][kChunk * kRow];
+    __shared__ __attribute__((aligned(16))) float abuf[kPWaves][64];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t item = (int64_t)blockIdx.x * kPWaves + wave;
+    const int64_t per_q = (int64_t)kvh * nsplit;
+    const int tq0 = (int)(item / per_q) * tok;
+    if (tq0 >= qs.count) return;
+    const int ntok = min(tok, qs.count - tq0);
+    const int g = (int)(item % kvh);
+    const int split = (int)((item / kvh) % nsplit);
+    const int clen = qs.causal_len(tq0 + ntok - 1);
+    const int t_begin = split * kPSplit;
+    if (t_begin >= clen) return;
+    const int t_end = min(clen, t_begin + kPSplit);
+    const int G = qh / kvh;
+    const int h0 = g * G;
+    const int ncols = ntok * G;  // <= 8
+    const int32_t* table = qs.table + (int64_t)tq0 * qs.table_stride;
+
+    static_assert(kPSplit == 64 * FHIP_PAGE_TOKENS, "one cached page per lane");
+    const int split_page =
+        t_begin + FHIP_PAGE_TOKENS * lane < t_end ? table[t_begin / FHIP_PAGE_TOKENS + lane] : -1;
+    const typename Pages::Lane pl = pg.lane_load(split_page);
+
+    // columns: c = n mod 8 is head h0 + c % G of query tq0 + c / G
+    const int n = lane & 15, kg = lane >> 4;
+    const int c = n & 7;
+    const bool col_ok = c < ncols;
+    const int ct = col_ok ? c / G : 0;
+    const int hn = col_ok ? c - ct * G : 0;
+    const int lim = col_ok ? min(t_end, qs.causal_len(tq0 + ct)) : 0;
+    u32x4 bq[kSteps];
+    {
+        const uint16_t* qrow = q + ((int64_t)(tq0 + ct) * qh + h0 + hn) * HD + 8 * kg;
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) {
+            const u32x4 v = ld16(qrow + 32 * s);
+            bq[s] = col_ok ? v : u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+    const int64_t k_off = ((int64_t)(lane & 15) * kvh + g) * (HD * 2) + 16 * kg;
+    const int dg = lane % kDg, ps = lane / kDg;
+    const uint8_t* dummy = (const uint8_t*)q;
+    uint8_t* vb = vbuf[wave];
+    // transposed-read source of this lane: row 4q + k (+16 for slots 4..7), dims 4a .. 4a + 3
+    // of each 16-dim block (q = lane / 16, k = (lane / 4) % 4, a = lane % 4)
+    const uint32_t tr_off =
+        (uint32_t)((4 * (lane >> 4) + ((lane >> 2) & 3)) * kRow + 8 * (lane & 3));
+
+    float m_run = -__builtin_inff(), l_run = 0.0f;
+    f4_t acc[kBlk];
+#pragma unroll
+    for (int b = 0; b < kBlk; ++b) acc[b] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int t0 = t_begin; t0 < t_end; t0 += kChunk) {
+        const int j0 = (t0 - t_begin) / FHIP_PAGE_TOKENS;
+        bool pok[kTiles];
+        const uint8_t* kb[kTiles];
+        const uint8_t* vsrc[kTiles];
+#pragma unroll
+        for (int tt = 0; tt < kTiles; ++tt) {
+            const int id = __builtin_amdgcn_readlane(split_page, j0 + tt);
+            pok[tt] = pg.valid(id);
+            kb[tt] = pok[tt] ? pg.k_at(pl, j0 + tt, id) : dummy;
+            vsrc[tt] = pok[tt] ? pg.v_at(pl, j0 + tt, id) : dummy;
+        }
+        u32x4 kr[kTiles][kSteps];
+#pragma unroll
+        for (int tt = 0; tt < kTiles; ++tt) {
+            const bool ok = pok[tt] && t0 + 16 * tt + (lane & 15) < t_end;
+            const uint8_t* src = ok ? kb[tt] + k_off : dummy;
+#pragma unroll
+            for (int s = 0; s < kSteps; ++s) kr[tt][s] = ld16(src + 64 * s);
+        }
+        u32x4 vr[kVLoads];
+        bool vok[kVLoads];
+#pragma unroll
+        for (int j = 0; j < kVLoads; ++j) {
+            const int pp = j * kPpl + ps;
+            const int tt = (j * kPpl) / 16;
+            vok[j] = pok[tt] && t0 + pp < t_end;
+            const uint8_t* src =
+                vok[j] ? vsrc[tt] + (((int64_t)(pp % 16) * kvh + g) * HD + 8 * dg) * 2 : dummy;
+            vr[j] = ld16(src);
+        }
+
+        // ---- QK: lane (n, kg) gets positions 16 tt + 4 kg + e of column n
+        float sc[kTiles][4];
+#pragma unroll
+        for (int tt = 0; tt < kTiles; ++tt) {
+            f4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < kSteps; ++s)
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, kr[tt][s]),
+                                                           __builtin_bit_cast(h8_t, bq[s]), d,
+                                                           0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int pos = t0 + 16 * tt + 4 * kg + e;
+                sc[tt][e] = pok[tt] && pos < lim ? d[e] * scale_log2 : -__builtin_inff();
+            }
+        }
+        // ---- V rows to LDS (zeros where there is no position: 0 * NaN would poison PV)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int j = 0; j < kVLoads; ++j)
+            *(u32x4*)(vb + (j * kPpl + ps) * kRow + 16 * dg) =
+                vok[j] ? vr[j] : u32x4{0u, 0u, 0u, 0u};
+        // ---- online softmax per column (lanes n, n + 16, n + 32, n + 48)
+        float cmax = -__builtin_inff();
+#pragma unroll
+        for (int tt = 0; tt < kTiles; ++tt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) cmax = fmaxf(cmax, sc[tt][e]);
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+        const float m_new = fmaxf(m_run, cmax);
+        const float mref = m_new == -__builtin_inff() ? 0.0f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - mref);
+        float psum = 0.0f;
+        _Float16 a[8];
+#pragma unroll
+        for (int tt = 0; tt < kTiles; ++tt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float p = __builtin_amdgcn_exp2f(sc[tt][e] - mref);
+                psum += p;
+                const _Float16 hi = (_Float16)p;
+                a[4 * tt + e] = n < 8 ? hi : (_Float16)((p - (float)hi) * 4096.0f);
+            }
+        psum += __shfl_xor(psum, 16);
+        psum += __shfl_xor(psum, 32);
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+        abuf[wave][lane] = alpha;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // ---- PV: rescale rows 4 kg + e (columns 4 (kg % 2) + e), then accumulate
+        const f4_t al = *(const f4_t*)&abuf[wave][4 * (kg & 1)];
+        const h8_t av = {a[0], a[1], a[2], a[3], a[4], a[5], a[6], a[7]};
+#pragma unroll
+        for (int b = 0; b < kBlk; ++b) {
+            typedef short v4s_t __attribute__((ext_vector_type(4)));
+            typedef __attribute__((address_space(3))) v4s_t lds_v4s_t;
+            const uint8_t* base = vb + tr_off + 32 * b;
+            const v4s_t lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_v4s_t*)(__attribute__((address_space(3))) uint8_t*)base);
+            const v4s_t hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_v4s_t*)(__attribute__((address_space(3))) uint8_t*)(base + 16 * kRow));
+            const h8_t bv = __builtin_bit_cast(
+                h8_t, (short __attribute__((ext_vector_type(8)))){lo4[0], lo4[1], lo4[2], lo4[3],
+                                                                  hi4[0], hi4[1], hi4[2], hi4[3]});
+            acc[b] *= al;
+            acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[b], 0, 0, 0);
+        }
+    }
+
+    // ---- partials: lanes kg < 2 hold rows 4 kg + e (columns 4 kg + e, fp16(p) part), lanes
+    // kg + 2 the matching 2^12 (p - fp16(p)) rows
+    if (lane < ncols) {  // lane == c here
+        const int64_t v = (int64_t)(tq0 + ct) * qh + h0 + hn;
+        part_ml[(v * nsplit + split) * 2 + 0] = m_run * 0.6931471805599453f;
+        part_ml[(v * nsplit + split) * 2 + 1] = l_run;
+    }
+    float o[kBlk][4];
+#pragma unroll
+    for (int b = 0; b < kBlk; ++b)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            o[b][e] = acc[b][e] + __shfl_xor(acc[b][e], 32) * (1.0f / 4096.0f);
+    if (kg < 2) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int col = 4 * kg + e;
+            if (col < ncols) {
+                const int cq = col / G;
+                const int64_t v = (int64_t)(tq0 + cq) * qh + h0 + (col - cq * G);
+                float* dst = part_acc + (v * nsplit + split) * HD + n;
+#pragma unroll
+                for (int b = 0; b < kBlk; ++b) dst[16 * b] = o[b][e];
+            }
+        }
+    }
+}
+
 // Merge of the splits of one (query, q head) vector per workgroup:
 // out = (sum_s w_s acc_s) / (sum_s w_s l_s), w_s = exp(m_s - max m); zeros when the query
 // attends to no position. The split weights are computed once, in parallel, into LDS; each
@@ -411,6 +627,15 @@ template <int HD, class Pages>
 void launch_split_hd(const uint16_t* q, const PQueries& qs, const Pages& pg, int qh, int kvh,
                      int nhb, float* ml, float* acc, int nsplit, int tok, int64_t groups,
                      hipStream_t s) {
+    if constexpr (HD <= 128) {
+        if (tok > 1) {
+            const float scale_log2 = 1.4426950408889634f / sqrtf((float)HD);
+            hipLaunchKernelGGL((paged_attn_prefill_mfma_kernel<HD, Pages>), dim3((unsigned)groups),
+                               dim3(64 * kPWaves), 0, s, q, qs, pg, qh, kvh, scale_log2, ml, acc,
+                               nsplit, tok);
+            return;
+        }
+    }
     if (qh / kvh * tok <= 4)
         launch_split_t<HD, 4>(q, qs, pg, qh, kvh, nhb, ml, acc, nsplit, tok, groups, s);
     else
