@@ -329,15 +329,17 @@ paged_attn_split_kernel(const uint16_t* __restrict__ q, PQueries qs, Pages pg, i
     }
 }
 
-// Causal prefill groups with PV on the MFMA as well (head_dim 32 / 64 / 128, G < 8 q heads per
-// kv head, 8 / G queries per wave as above). Per 32-position chunk:
-//   QK as in paged_attn_split_kernel, except that MFMA columns 8..15 repeat columns 0..7, so a
-//     lane n >= 8 holds the same scores and probabilities as lane n - 8;
-//   PV on v_mfma_f32_16x16x32_f16: out[col][d] += P[col][slot] V[slot][d]. Slot 8q + i of
-//     lane group q is position 4q + i (i < 4) or 16 + 4q + i - 4: exactly the positions whose
-//     probabilities that lane group holds after QK, so A needs no data movement. Row m < 8 of
-//     A is fp16(p) of column m, row 8 + m is fp16((p - fp16(p)) 2^12), and the output is
-//     D[m] + 2^-12 D[8 + m]: fp32 weights to ~2^-22, V exact.
+// Causal prefill groups with PV on the MFMA as well (head_dim 32 / 64 / 128, G <= 8 q heads per
+// kv head): a wave takes 16 / G consecutive queries, MFMA column c being head c % G of query
+// c / G. Per 32-position chunk:
+//   QK as in paged_attn_split_kernel, over 16 columns;
+//   PV on v_mfma_f32_16x16x32_f16, two products per 16-dim block: out[col][d] +=
+//     P[col][slot] V[slot][d] for columns 0..7, then 8..15. Slot 8q + i of lane group q is
+//     position 4q + i (i < 4) or 16 + 4q + i - 4: exactly the positions whose probabilities
+//     that lane group holds after QK. In the product for columns 8h .. 8h + 7, A row m < 8 is
+//     fp16(p) of column 8h + m and row 8 + m is fp16((p - fp16(p)) 2^12) of the same column
+//     (one DPP row rotation by 8 brings each lane its partner column's p), and the output
+//     is D[m] + 2^-12 D[8 + m]: fp32 weights to ~2^-22, V exact.
 //   B = V transposed: the chunk's V rows are staged in LDS row-major (rows padded so that the
 //     four rows one transposed read gathers sit on different banks), and
 //     ds_read_b64_tr_b16 gives lane (d, q) dim d of the 4 positions addressed by source
@@ -374,7 +376,7 @@ paged_attn_prefill_mfma_kernel(const uint16_t* __restrict__ q, PQueries qs, Page
     const int t_end = min(clen, t_begin + kPSplit);
     const int G = qh / kvh;
     const int h0 = g * G;
-    const int ncols = ntok * G;  // <= 8
+    const int ncols = ntok * G;  // <= 16
     const int32_t* table = qs.table + (int64_t)tq0 * qs.table_stride;
 
     static_assert(kPSplit == 64 * FHIP_PAGE_TOKENS, "one cached page per lane");
@@ -382,12 +384,11 @@ paged_attn_prefill_mfma_kernel(const uint16_t* __restrict__ q, PQueries qs, Page
         t_begin + FHIP_PAGE_TOKENS * lane < t_end ? table[t_begin / FHIP_PAGE_TOKENS + lane] : -1;
     const typename Pages::Lane pl = pg.lane_load(split_page);
 
-    // columns: c = n mod 8 is head h0 + c % G of query tq0 + c / G
+    // column n is head h0 + n % G of query tq0 + n / G
     const int n = lane & 15, kg = lane >> 4;
-    const int c = n & 7;
-    const bool col_ok = c < ncols;
-    const int ct = col_ok ? c / G : 0;
-    const int hn = col_ok ? c - ct * G : 0;
+    const bool col_ok = n < ncols;
+    const int ct = col_ok ? n / G : 0;
+    const int hn = col_ok ? n - ct * G : 0;
     const int lim = col_ok ? min(t_end, qs.causal_len(tq0 + ct)) : 0;
     u32x4 bq[kSteps];
     {
@@ -408,9 +409,11 @@ paged_attn_prefill_mfma_kernel(const uint16_t* __restrict__ q, PQueries qs, Page
         (uint32_t)((4 * (lane >> 4) + ((lane >> 2) & 3)) * kRow + 8 * (lane & 3));
 
     float m_run = -__builtin_inff(), l_run = 0.0f;
-    f4_t acc[kBlk];
+    f4_t acc[2][kBlk];  // columns 0..7, 8..15
 #pragma unroll
-    for (int b = 0; b < kBlk; ++b) acc[b] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int b = 0; b < kBlk; ++b) acc[h][b] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
     for (int t0 = t_begin; t0 < t_end; t0 += kChunk) {
         const int j0 = (t0 - t_begin) / FHIP_PAGE_TOKENS;
@@ -479,15 +482,21 @@ paged_attn_prefill_mfma_kernel(const uint16_t* __restrict__ q, PQueries qs, Page
         const float mref = m_new == -__builtin_inff() ? 0.0f : m_new;
         const float alpha = __builtin_amdgcn_exp2f(m_run - mref);
         float psum = 0.0f;
-        _Float16 a[8];
+        _Float16 a[2][8];  // A of the products for columns 0..7 and 8..15
 #pragma unroll
         for (int tt = 0; tt < kTiles; ++tt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float p = __builtin_amdgcn_exp2f(sc[tt][e] - mref);
                 psum += p;
-                const _Float16 hi = (_Float16)p;
-                a[4 * tt + e] = n < 8 ? hi : (_Float16)((p - (float)hi) * 4096.0f);
+                // p of column n ^ 8 (lane n of each 16-lane row takes lane n ^ 8)
+                const float po = __int_as_float(
+                    __builtin_amdgcn_mov_dpp(__float_as_int(p), 0x128, 0xF, 0xF, true));
+                const _Float16 ph = (_Float16)p, oh = (_Float16)po;
+                const _Float16 pl_ = (_Float16)((p - (float)ph) * 4096.0f);
+                const _Float16 ol = (_Float16)((po - (float)oh) * 4096.0f);
+                a[0][4 * tt + e] = n < 8 ? ph : ol;  // rows: hi of column n / lo of column n - 8
+                a[1][4 * tt + e] = n < 8 ? oh : pl_;  // hi of column n + 8 / lo of column n
             }
         psum += __shfl_xor(psum, 16);
         psum += __shfl_xor(psum, 32);
@@ -497,9 +506,11 @@ paged_attn_prefill_mfma_kernel(const uint16_t* __restrict__ q, PQueries qs, Page
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // ---- PV: rescale rows 4 kg + e (columns 4 (kg % 2) + e), then accumulate
-        const f4_t al = *(const f4_t*)&abuf[wave][4 * (kg & 1)];
-        const h8_t av = {a[0], a[1], a[2], a[3], a[4], a[5], a[6], a[7]};
+        // ---- PV: rescale rows 4 kg + e (columns 8h + 4 (kg % 2) + e), then accumulate
+        const f4_t al0 = *(const f4_t*)&abuf[wave][4 * (kg & 1)];
+        const f4_t al1 = *(const f4_t*)&abuf[wave][8 + 4 * (kg & 1)];
+        const h8_t av0 = {a[0][0], a[0][1], a[0][2], a[0][3], a[0][4], a[0][5], a[0][6], a[0][7]};
+        const h8_t av1 = {a[1][0], a[1][1], a[1][2], a[1][3], a[1][4], a[1][5], a[1][6], a[1][7]};
 #pragma unroll
         for (int b = 0; b < kBlk; ++b) {
             typedef short v4s_t __attribute__((ext_vector_type(4)));
@@ -512,34 +523,39 @@ paged_attn_prefill_mfma_kernel(const uint16_t* __restrict__ q, PQueries qs, Page
             const h8_t bv = __builtin_bit_cast(
                 h8_t, (short __attribute__((ext_vector_type(8)))){lo4[0], lo4[1], lo4[2], lo4[3],
                                                                   hi4[0], hi4[1], hi4[2], hi4[3]});
-            acc[b] *= al;
-            acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[b], 0, 0, 0);
+            acc[0][b] *= al0;
+            acc[0][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av0, bv, acc[0][b], 0, 0, 0);
+            acc[1][b] *= al1;
+            acc[1][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av1, bv, acc[1][b], 0, 0, 0);
         }
     }
 
-    // ---- partials: lanes kg < 2 hold rows 4 kg + e (columns 4 kg + e, fp16(p) part), lanes
-    // kg + 2 the matching 2^12 (p - fp16(p)) rows
-    if (lane < ncols) {  // lane == c here
+    // ---- partials: in product h, lanes kg < 2 hold rows 4 kg + e (column 8h + 4 kg + e,
+    // fp16(p) part), lanes kg + 2 the matching 2^12 (p - fp16(p)) rows
+    if (lane < ncols) {  // lane == n here
         const int64_t v = (int64_t)(tq0 + ct) * qh + h0 + hn;
         part_ml[(v * nsplit + split) * 2 + 0] = m_run * 0.6931471805599453f;
         part_ml[(v * nsplit + split) * 2 + 1] = l_run;
     }
-    float o[kBlk][4];
 #pragma unroll
-    for (int b = 0; b < kBlk; ++b)
+    for (int h = 0; h < 2; ++h) {
+        float o[kBlk][4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            o[b][e] = acc[b][e] + __shfl_xor(acc[b][e], 32) * (1.0f / 4096.0f);
-    if (kg < 2) {
+        for (int b = 0; b < kBlk; ++b)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int col = 4 * kg + e;
-            if (col < ncols) {
-                const int cq = col / G;
-                const int64_t v = (int64_t)(tq0 + cq) * qh + h0 + (col - cq * G);
-                float* dst = part_acc + (v * nsplit + split) * HD + n;
+            for (int e = 0; e < 4; ++e)
+                o[b][e] = acc[h][b][e] + __shfl_xor(acc[h][b][e], 32) * (1.0f / 4096.0f);
+        if (kg < 2) {
 #pragma unroll
-                for (int b = 0; b < kBlk; ++b) dst[16 * b] = o[b][e];
+            for (int e = 0; e < 4; ++e) {
+                const int col = 8 * h + 4 * kg + e;
+                if (col < ncols) {
+                    const int cq = col / G;
+                    const int64_t v = (int64_t)(tq0 + cq) * qh + h0 + (col - cq * G);
+                    float* dst = part_acc + (v * nsplit + split) * HD + n;
+#pragma unroll
+                    for (int b = 0; b < kBlk; ++b) dst[16 * b] = o[b][e];
+                }
             }
         }
     }
@@ -653,10 +669,13 @@ int launch_paged(void* out, const void* q, const PQueries& qs, int nq, const Pag
     float* acc = (float*)((char*)ws + off_acc);
     const int G = qh / kvh;
     const int nhb = (G + kHeadsMax - 1) / kHeadsMax;
-    // causal prefill over one shared table: 8 / G consecutive queries per wave
-    const int tok = (!qs.seq_lens && qs.table_stride == 0 && nq > 1 && G < kHeadsMax)
-                        ? kHeadsMax / G
-                        : 1;
+    // causal prefill over one shared table: 16 / G consecutive queries per wave on the MFMA
+    // prefill kernel (head_dim <= 128, G <= 8), else 8 / G (G < 8)
+    const bool prefill = !qs.seq_lens && qs.table_stride == 0 && nq > 1;
+    const int tok = !prefill                          ? 1
+                    : (hd <= 128 && G <= kHeadsMax)   ? 2 * kHeadsMax / G
+                    : G < kHeadsMax                   ? kHeadsMax / G
+                                                      : 1;
     const int64_t items = ceil_div((int64_t)nq, tok) * kvh * nhb * nsplit;
     const int64_t groups = ceil_div(items, kPWaves);
     if (groups > 0x7fffffff || (int64_t)nq * qh > 0x7fffffff) return hipErrorInvalidValue;

@@ -121,7 +121,9 @@ def test_decode_empty_sequence_and_masked_pages(dev):
     # 8 / G queries per wave: ragged last groups, groups whose lengths straddle a page or
     # the 1024-position split edge, whole prefills from position 0
     (1050, 19, 1020, 4, 4, 128), (300, 13, 0, 8, 4, 32), (1100, 11, 1019, 6, 2, 256),
-    (70, 70, 0, 8, 2, 128), (2100, 9, 2040, 16, 16, 64), (50, 7, 43, 16, 2, 64)])
+    (70, 70, 0, 8, 2, 128), (2100, 9, 2040, 16, 16, 64), (50, 7, 43, 16, 2, 64),
+    # 16 / G queries per wave on the MFMA prefill kernel: G = 8 (2 queries), G = 1 (16)
+    (2100, 33, 2067, 32, 4, 128), (600, 37, 563, 4, 4, 64), (1030, 21, 1010, 24, 3, 32)])
 def test_reference_interface_prefill_causal(dev, kv_len, T, start_pos, qh, kvh, hd):
     """fhip_launch_paged_attention: T queries at start_pos.. over per-block pointer arrays;
     query i attends to min(start_pos + i + 1, kv_len) positions."""

@@ -1,14 +1,15 @@
-"""CPU model of the work split of the FP16 paged-attention kernel (paged_attn_split_kernel in
-fracture_amd/csrc/attention_paged.hip): which query rows each wave reads and which split
-partials it writes, checked against the combine kernel's reads.
+"""CPU model of the work split of the FP16 paged-attention kernels (paged_attn_split_kernel
+and paged_attn_prefill_mfma_kernel in fracture_amd/csrc/attention_paged.hip): which query rows
+each wave reads and which split partials it writes, checked against the combine kernel's reads.
 
 A wave item is (query group, kv head g, head block hb, split). In causal prefill over one
-shared block table with G = qh / kvh < 8, a group is tok = 8 / G consecutive queries and MFMA
-column c is head g G + c % G of query tq0 + c / G; otherwise tok = 1 and column c is head
-g G + 8 hb + c. Each column scores positions below min(split end, its own causal length).
-The combine reads partial (vector, split) for every split below the vector's causal length;
-the model asserts that each of those is written by exactly one wave, with the causal length
-of that vector, and nothing else is written. No GPU is used.
+shared block table, a group is tok consecutive queries: 16 / G of them on the MFMA prefill
+kernel (head_dim <= 128, G = qh / kvh <= 8), else 8 / G (G < 8); MFMA column c is head
+g G + c % G of query tq0 + c / G. Otherwise tok = 1 and column c is head g G + 8 hb + c. Each
+column scores positions below min(split end, its own causal length). The combine reads partial
+(vector, split) for every split below the vector's causal length; the model asserts that each
+of those is written by exactly one wave, with the causal length of that vector, and that
+nothing else is read. No GPU is used.
 """
 import numpy as np
 import pytest
@@ -24,14 +25,17 @@ def causal_len(qi, kv_len, start_pos, max_blocks, seq_lens=None):
 
 
 def model_split_kernel(nq, qh, kvh, kv_len, start_pos, shared_table=True, seq_lens=None,
-                       wrap=None):
+                       wrap=None, hd=128):
     G = qh // kvh
     wrap = G if wrap is None else wrap  # head count at which the acc loop's counter wraps
     nhb = (G + HEADS_MAX - 1) // HEADS_MAX
     max_blocks = (max(kv_len, int(max(seq_lens)) if seq_lens is not None else 0) + 15) // 16
     nsplit = max(1, (max_blocks * PAGE + SPLIT - 1) // SPLIT)
-    tok = HEADS_MAX // G if (seq_lens is None and shared_table and nq > 1 and G < HEADS_MAX) else 1
-    NH = 4 if G * tok <= 4 else 8
+    prefill = seq_lens is None and shared_table and nq > 1
+    mfma = prefill and hd <= 128 and G <= HEADS_MAX
+    tok = (2 * HEADS_MAX // G if mfma else
+           HEADS_MAX // G if prefill and G < HEADS_MAX else 1)
+    NH = 16 if mfma else 4 if G * tok <= 4 else 8
     items = -(-nq // tok) * kvh * nhb * nsplit
     per_q = kvh * nhb * nsplit
     written = {}
@@ -66,14 +70,20 @@ def model_split_kernel(nq, qh, kvh, kv_len, start_pos, shared_table=True, seq_le
                 if tok > 1 else clen
             lim = min(t_end, col_len)
             q_rows.add(row)
-            # the partial write of lane n (== column n) and of the acc loop's column n
-            hc, hh = 0, 0
-            for h in range(NH):
-                if h == n:
-                    assert (tq0 + hc) * qh + h0 + hh == row
-                hh += 1
-                if hh == wrap:
-                    hh, hc = 0, hc + 1
+            if mfma:
+                # the MFMA kernel's partial write of product h, row 4 kg + e: column 8h + 4kg + e
+                for col in range(ncols):
+                    if col == n:
+                        assert (tq0 + col // G) * qh + h0 + col % G == row
+            else:
+                # the partial write of lane n (== column n) and of the acc loop's column n
+                hc, hh = 0, 0
+                for h in range(NH):
+                    if h == n:
+                        assert (tq0 + hc) * qh + h0 + hh == row
+                    hh += 1
+                    if hh == wrap:
+                        hh, hc = 0, hc + 1
             key = (row, split)
             assert key not in written, f"partial {key} written twice"
             written[key] = (lim, t_begin)
@@ -94,12 +104,13 @@ def model_split_kernel(nq, qh, kvh, kv_len, start_pos, shared_table=True, seq_le
     return tok
 
 
-@pytest.mark.parametrize("nq,qh,kvh,kv_len,start_pos,tok", [
-    (19, 4, 4, 1050, 1020, 8), (13, 8, 4, 300, 0, 4), (11, 6, 2, 1100, 1019, 2),
-    (70, 8, 2, 70, 0, 2), (9, 16, 16, 2100, 2040, 8), (7, 16, 2, 50, 43, 1),
-    (37, 32, 8, 3000, 2963, 2), (5, 24, 2, 1030, 1025, 1), (1, 8, 8, 40, 39, 1)])
-def test_prefill_groups_cover_every_partial(nq, qh, kvh, kv_len, start_pos, tok):
-    assert model_split_kernel(nq, qh, kvh, kv_len, start_pos) == tok
+@pytest.mark.parametrize("nq,qh,kvh,kv_len,start_pos,hd,tok", [
+    (19, 4, 4, 1050, 1020, 128, 16), (13, 8, 4, 300, 0, 32, 8), (11, 6, 2, 1100, 1019, 256, 2),
+    (11, 6, 2, 1100, 1019, 64, 5), (70, 8, 2, 70, 0, 128, 4), (9, 16, 16, 2100, 2040, 64, 16),
+    (7, 16, 2, 50, 43, 64, 2), (37, 32, 8, 3000, 2963, 128, 4), (5, 24, 2, 1030, 1025, 128, 1),
+    (1, 8, 8, 40, 39, 128, 1), (33, 32, 4, 2100, 2067, 128, 2), (21, 8, 8, 600, 579, 256, 8)])
+def test_prefill_groups_cover_every_partial(nq, qh, kvh, kv_len, start_pos, hd, tok):
+    assert model_split_kernel(nq, qh, kvh, kv_len, start_pos, hd=hd) == tok
 
 
 def test_decode_rows_keep_one_query_per_wave():
@@ -110,4 +121,4 @@ def test_decode_rows_keep_one_query_per_wave():
 def test_column_mapping_error_is_caught():
     """The model fails when the acc loop's column counter wraps at the wrong head count."""
     with pytest.raises(AssertionError):
-        model_split_kernel(13, 8, 4, 300, 0, wrap=3)
+        model_split_kernel(13, 8, 4, 300, 0, wrap=3, hd=256)
