@@ -614,6 +614,40 @@ __global__ __launch_bounds__(kCombThreads) void paged_attn_combine_kernel(
     }
 }
 
+// The same merge with one wave per vector, four vectors per workgroup, for launches with at
+// most 8 splits per vector (contexts up to 8192 positions; causal prefill): lane s holds split
+// s's (m, l) and the weights reach the dim loop by lane broadcasts, so no LDS and no barrier.
+// A workgroup per vector spent most of its time being scheduled at prefill sizes.
+constexpr int kCombWaveMaxSplits = 8;
+__global__ __launch_bounds__(256) void paged_attn_combine_wave_kernel(
+    PQueries qs, const float* __restrict__ ml, const float* __restrict__ acc,
+    uint16_t* __restrict__ out, int qh, int hd, int nsplit, int64_t nvec) {
+    const int lane = threadIdx.x & 63;
+    const int64_t vec = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (vec >= nvec) return;
+    const int clen = qs.causal_len((int)(vec / qh));
+    const int ns = (clen + kPSplit - 1) / kPSplit;  // <= nsplit <= kCombWaveMaxSplits
+    const float* m = ml + vec * nsplit * 2;
+    const float ms = lane < ns ? m[2 * lane] : -__builtin_inff();
+    const float ls = lane < ns ? m[2 * lane + 1] : 0.0f;
+    const float M = wave_max(ms);
+    const float w = lane < ns && M != -__builtin_inff() ? expf(ms - M) : 0.0f;
+    const float L = wave_sum(w * ls);
+    float ws[kCombWaveMaxSplits];
+#pragma unroll
+    for (int j = 0; j < kCombWaveMaxSplits; ++j) ws[j] = __shfl(w, j);
+    const float* a = acc + vec * nsplit * hd;
+    for (int d = lane; d < hd; d += 64) {
+        float av[kCombWaveMaxSplits];
+#pragma unroll
+        for (int j = 0; j < kCombWaveMaxSplits; ++j) av[j] = j < ns ? a[(int64_t)j * hd + d] : 0.0f;
+        float o = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kCombWaveMaxSplits; ++j) o = fmaf(ws[j], av[j], o);
+        out[vec * hd + d] = (uint16_t)f2h(L > 0.0f ? o / L : 0.0f);
+    }
+}
+
 size_t paged_ws_layout(int nq, int qh, int hd, int max_tokens, size_t* off_acc, int* nsplit) {
     const int ns = max_tokens > 0 ? (max_tokens + kPSplit - 1) / kPSplit : 1;
     const size_t ml = (size_t)nq * qh * ns * 2 * sizeof(float);
@@ -696,9 +730,14 @@ int launch_paged(void* out, const void* q, const PQueries& qs, int nq, const Pag
             launch_split_hd<256>(qp, q2, pg, qh, kvh, nhb, ml, acc, nsplit, tok, groups, s);
             break;
     }
-    hipLaunchKernelGGL(paged_attn_combine_kernel, dim3((unsigned)((int64_t)nq * qh)),
-                       dim3(kCombThreads), (size_t)nsplit * sizeof(float), s, q2, ml, acc,
-                       (uint16_t*)out, qh, hd, nsplit);
+    const int64_t nvec = (int64_t)nq * qh;
+    if (nsplit <= kCombWaveMaxSplits)
+        hipLaunchKernelGGL(paged_attn_combine_wave_kernel, dim3((unsigned)ceil_div(nvec, 4)),
+                           dim3(256), 0, s, q2, ml, acc, (uint16_t*)out, qh, hd, nsplit, nvec);
+    else
+        hipLaunchKernelGGL(paged_attn_combine_kernel, dim3((unsigned)nvec), dim3(kCombThreads),
+                           (size_t)nsplit * sizeof(float), s, q2, ml, acc, (uint16_t*)out, qh,
+                           hd, nsplit);
     return hipGetLastError();
 }
 
