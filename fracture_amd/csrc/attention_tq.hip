@@ -378,6 +378,42 @@ size_t combine_lds_bytes(int hd, int nsplit, bool merge_only = false) {
     return ((hd <= kRotLdsMaxHd && !merge_only ? (size_t)hd * hd : 0) + (size_t)kCombHeads * nsplit) *
            sizeof(float);
 }
+// The merge alone with one wave per vector, four vectors per workgroup, when a vector has at
+// most 8 splits (contexts up to 8192 positions; causal prefill): lane s holds split s's
+// (m, l), the weights reach the dim loop by lane broadcasts, and each merged vector (fp32,
+// divided by its sum) goes to merged[vector]. The combine kernel's 16-split load batches
+// would be mostly clamped repeats at these sizes.
+constexpr int kMergeWaveMaxSplits = 8;
+__global__ __launch_bounds__(256) void tq_attn_merge_wave_kernel(
+    Queries qs, const float* __restrict__ part_ml, const float* __restrict__ part_acc, int qh,
+    int hd, int nsplit, int64_t nvec, float* __restrict__ merged) {
+    const int lane = threadIdx.x & 63;
+    const int64_t vec = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (vec >= nvec) return;
+    const int clen = qs.causal_len((int)(vec / qh));
+    const int ns = (clen + kSplit - 1) / kSplit;  // <= nsplit <= kMergeWaveMaxSplits
+    const float* ml = part_ml + vec * nsplit * 2;
+    const float ms = lane < ns ? ml[2 * lane] : -__builtin_inff();
+    const float ls = lane < ns ? ml[2 * lane + 1] : 0.0f;
+    const float M = wave_max(ms);
+    const float w = lane < ns && ms != -__builtin_inff() ? expf(ms - M) : 0.0f;
+    const float L = wave_sum(w * ls);
+    const float linv = L > 0.0f ? 1.0f / L : 0.0f;
+    float ws[kMergeWaveMaxSplits];
+#pragma unroll
+    for (int j = 0; j < kMergeWaveMaxSplits; ++j) ws[j] = __shfl(w, j);
+    const float* a = part_acc + vec * nsplit * hd;
+    for (int d = lane; d < hd; d += 64) {
+        float av[kMergeWaveMaxSplits];
+#pragma unroll
+        for (int j = 0; j < kMergeWaveMaxSplits; ++j) av[j] = j < ns ? a[(int64_t)j * hd + d] : 0.0f;
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kMergeWaveMaxSplits; ++j) sum = fmaf(av[j], ws[j], sum);
+        merged[vec * hd + d] = sum * linv;
+    }
+}
+
 // kMergeOnly: phase 2 writes each merged vector (fp32, already divided by its sum) to
 // merged[vector] and the kernel ends; the unrotation then runs as a batched MFMA product.
 template <bool kRotLds, bool kMergeOnly = false>
@@ -1312,10 +1348,15 @@ int launch_attention(const AttnArgs& a, const Pages& pg, hipStream_t s) {
     else
         launch_split<0, 0>(a, pg, nsplit, ml, acc, s);
     if (batched_rot) {
-        hipLaunchKernelGGL((tq_attn_combine_kernel<true, true>),
-                           dim3((unsigned)ceil_div(nvec, kCombHeads)), dim3(256),
-                           combine_lds_bytes(a.hd, nsplit, true), s, a.qs, ml, acc, a.vrot,
-                           (uint16_t*)a.out, a.qh, a.hd, nsplit, (int64_t)nvec, qrot);
+        if (nsplit <= kMergeWaveMaxSplits)
+            hipLaunchKernelGGL(tq_attn_merge_wave_kernel, dim3((unsigned)ceil_div(nvec, 4)),
+                               dim3(256), 0, s, a.qs, ml, acc, a.qh, a.hd, nsplit, (int64_t)nvec,
+                               qrot);
+        else
+            hipLaunchKernelGGL((tq_attn_combine_kernel<true, true>),
+                               dim3((unsigned)ceil_div(nvec, kCombHeads)), dim3(256),
+                               combine_lds_bytes(a.hd, nsplit, true), s, a.qs, ml, acc, a.vrot,
+                               (uint16_t*)a.out, a.qh, a.hd, nsplit, (int64_t)nvec, qrot);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         return fhip_internal::tq_rotate_back_rows(qrot, a.vrot, a.out, nvec, s);
