@@ -340,6 +340,9 @@ paged_attn_split_kernel(const uint16_t* __restrict__ q, PQueries qs, Pages pg, i
 //     fp16(p) of column 8h + m and row 8 + m is fp16((p - fp16(p)) 2^12) of the same column
 //     (one DPP row rotation by 8 brings each lane its partner column's p), and the output
 //     is D[m] + 2^-12 D[8 + m]: fp32 weights to ~2^-22, V exact.
+//   The two waves of a workgroup take consecutive query groups over the same kv head and
+//     split and share each chunk: each loads half of its K and V rows into LDS, and both read
+//     all of them (the chunk's K and V cross L2 once per 2 x 16 / G queries);
 //   B = V transposed: the chunk's V rows are staged in LDS row-major (rows padded so that the
 //     four rows one transposed read gathers sit on different banks), and
 //     ds_read_b64_tr_b16 gives lane (d, q) dim d of the 4 positions addressed by source
@@ -356,28 +359,35 @@ paged_attn_prefill_mfma_kernel(const uint16_t* __restrict__ q, PQueries qs, Page
     constexpr int kDg = HD / 8;    // lanes per V row load, 8 dims each
     constexpr int kPpl = 64 / kDg;
     constexpr int kVLoads = kChunk / kPpl;
-    constexpr int kRow = HD * 2 + 32;  // bytes per staged V row
+    constexpr int kRow = HD * 2 + 32;   // bytes per staged V row
+    constexpr int kRowK = HD * 2 + 16;  // per staged K row: 16 rows' reads of one segment
+                                        // cover all banks
     static_assert(HD >= 32 && HD <= 128, "head_dim 32, 64 or 128");
-    __shared__ __attribute__((aligned(16))) uint8_t vbuf[kPWaves][kChunk * kRow];
+    static_assert(kPWaves == 2 && kTiles == 2, "one tile of each chunk loaded per wave");
+    __shared__ __attribute__((aligned(16))) uint8_t kbuf[kChunk * kRowK];
+    __shared__ __attribute__((aligned(16))) uint8_t vbuf[kChunk * kRow];
     __shared__ __attribute__((aligned(16))) float abuf[kPWaves][64];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t item = (int64_t)blockIdx.x * kPWaves + wave;
-    const int64_t per_q = (int64_t)kvh * nsplit;
-    const int tq0 = (int)(item / per_q) * tok;
-    if (tq0 >= qs.count) return;
-    const int ntok = min(tok, qs.count - tq0);
-    const int g = (int)(item % kvh);
-    const int split = (int)((item / kvh) % nsplit);
-    const int clen = qs.causal_len(tq0 + ntok - 1);
+    // workgroup (pair of query groups, kv head, split); wave w takes group 2 pair + w. Every
+    // exit before the chunk loop is uniform over the workgroup (the loop has barriers).
+    const int64_t wg = blockIdx.x;
+    const int64_t per_p = (int64_t)kvh * nsplit;
+    const int tp0 = (int)(wg / per_p) * 2 * tok;  // the pair's first query
+    if (tp0 >= qs.count) return;
+    const int tq0 = tp0 + wave * tok;
+    const int ntok = max(0, min(tok, qs.count - tq0));  // 0: a wave past the last query
+    const int g = (int)(wg % kvh);
+    const int split = (int)((wg / kvh) % nsplit);
+    const int clen = qs.causal_len(min(tp0 + 2 * tok, qs.count) - 1);  // the pair's longest
     const int t_begin = split * kPSplit;
     if (t_begin >= clen) return;
     const int t_end = min(clen, t_begin + kPSplit);
     const int G = qh / kvh;
     const int h0 = g * G;
     const int ncols = ntok * G;  // <= 16
-    const int32_t* table = qs.table + (int64_t)tq0 * qs.table_stride;
+    const int32_t* table = qs.table + (int64_t)tp0 * qs.table_stride;
 
     static_assert(kPSplit == 64 * FHIP_PAGE_TOKENS, "one cached page per lane");
     const int split_page =
@@ -392,7 +402,7 @@ paged_attn_prefill_mfma_kernel(const uint16_t* __restrict__ q, PQueries qs, Page
     const int lim = col_ok ? min(t_end, qs.causal_len(tq0 + ct)) : 0;
     u32x4 bq[kSteps];
     {
-        const uint16_t* qrow = q + ((int64_t)(tq0 + ct) * qh + h0 + hn) * HD + 8 * kg;
+        const uint16_t* qrow = q + ((int64_t)(col_ok ? tq0 + ct : tp0) * qh + h0 + hn) * HD + 8 * kg;
 #pragma unroll
         for (int s = 0; s < kSteps; ++s) {
             const u32x4 v = ld16(qrow + 32 * s);
@@ -402,7 +412,7 @@ paged_attn_prefill_mfma_kernel(const uint16_t* __restrict__ q, PQueries qs, Page
     const int64_t k_off = ((int64_t)(lane & 15) * kvh + g) * (HD * 2) + 16 * kg;
     const int dg = lane % kDg, ps = lane / kDg;
     const uint8_t* dummy = (const uint8_t*)q;
-    uint8_t* vb = vbuf[wave];
+    uint8_t* vb = vbuf;
     // transposed-read source of this lane: row 4q + k (+16 for slots 4..7), dims 4a .. 4a + 3
     // of each 16-dim block (q = lane / 16, k = (lane / 4) % 4, a = lane % 4)
     const uint32_t tr_off =
@@ -418,34 +428,44 @@ paged_attn_prefill_mfma_kernel(const uint16_t* __restrict__ q, PQueries qs, Page
     for (int t0 = t_begin; t0 < t_end; t0 += kChunk) {
         const int j0 = (t0 - t_begin) / FHIP_PAGE_TOKENS;
         bool pok[kTiles];
-        const uint8_t* kb[kTiles];
-        const uint8_t* vsrc[kTiles];
 #pragma unroll
-        for (int tt = 0; tt < kTiles; ++tt) {
-            const int id = __builtin_amdgcn_readlane(split_page, j0 + tt);
-            pok[tt] = pg.valid(id);
-            kb[tt] = pok[tt] ? pg.k_at(pl, j0 + tt, id) : dummy;
-            vsrc[tt] = pok[tt] ? pg.v_at(pl, j0 + tt, id) : dummy;
+        for (int tt = 0; tt < kTiles; ++tt)
+            pok[tt] = pg.valid(__builtin_amdgcn_readlane(split_page, j0 + tt));
+        // ---- this wave's tile of the chunk (positions 16 wave ..): K and V rows into
+        // registers; positions past the end or in invalid pages read `dummy` (finite)
+        const int idw = __builtin_amdgcn_readlane(split_page, j0 + wave);
+        const bool pw = pg.valid(idw);
+        const uint8_t* kbw = pw ? pg.k_at(pl, j0 + wave, idw) : dummy;
+        const uint8_t* vbw = pw ? pg.v_at(pl, j0 + wave, idw) : dummy;
+        u32x4 kr[kSteps];
+        {
+            const bool ok = pw && t0 + 16 * wave + (lane & 15) < t_end;
+            const uint8_t* src = ok ? kbw + k_off : dummy;
+#pragma unroll
+            for (int st = 0; st < kSteps; ++st) kr[st] = ld16(src + 64 * st);
         }
-        u32x4 kr[kTiles][kSteps];
+        constexpr int kVHalf = kVLoads / 2;
+        u32x4 vr[kVHalf];
+        bool vok[kVHalf];
 #pragma unroll
-        for (int tt = 0; tt < kTiles; ++tt) {
-            const bool ok = pok[tt] && t0 + 16 * tt + (lane & 15) < t_end;
-            const uint8_t* src = ok ? kb[tt] + k_off : dummy;
-#pragma unroll
-            for (int s = 0; s < kSteps; ++s) kr[tt][s] = ld16(src + 64 * s);
-        }
-        u32x4 vr[kVLoads];
-        bool vok[kVLoads];
-#pragma unroll
-        for (int j = 0; j < kVLoads; ++j) {
-            const int pp = j * kPpl + ps;
-            const int tt = (j * kPpl) / 16;
-            vok[j] = pok[tt] && t0 + pp < t_end;
+        for (int j = 0; j < kVHalf; ++j) {
+            const int pp = 16 * wave + j * kPpl + ps;  // position in the chunk
+            vok[j] = pw && t0 + pp < t_end;
             const uint8_t* src =
-                vok[j] ? vsrc[tt] + (((int64_t)(pp % 16) * kvh + g) * HD + 8 * dg) * 2 : dummy;
+                vok[j] ? vbw + (((int64_t)(pp % 16) * kvh + g) * HD + 8 * dg) * 2 : dummy;
             vr[j] = ld16(src);
         }
+        // ---- stage both halves: the other wave has finished reading the previous chunk
+        __syncthreads();
+#pragma unroll
+        for (int st = 0; st < kSteps; ++st)
+            *(u32x4*)(kbuf + (16 * wave + (lane & 15)) * kRowK + 64 * st + 16 * kg) = kr[st];
+        // V zeros where there is no position: 0 * NaN would poison PV
+#pragma unroll
+        for (int j = 0; j < kVHalf; ++j)
+            *(u32x4*)(vb + (16 * wave + j * kPpl + ps) * kRow + 16 * dg) =
+                vok[j] ? vr[j] : u32x4{0u, 0u, 0u, 0u};
+        __syncthreads();
 
         // ---- QK: lane (n, kg) gets positions 16 tt + 4 kg + e of column n
         float sc[kTiles][4];
@@ -453,23 +473,19 @@ paged_attn_prefill_mfma_kernel(const uint16_t* __restrict__ q, PQueries qs, Page
         for (int tt = 0; tt < kTiles; ++tt) {
             f4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int s = 0; s < kSteps; ++s)
-                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, kr[tt][s]),
-                                                           __builtin_bit_cast(h8_t, bq[s]), d,
+            for (int st = 0; st < kSteps; ++st) {
+                const u32x4 kv =
+                    *(const u32x4*)(kbuf + (16 * tt + (lane & 15)) * kRowK + 64 * st + 16 * kg);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, kv),
+                                                           __builtin_bit_cast(h8_t, bq[st]), d,
                                                            0, 0, 0);
+            }
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int pos = t0 + 16 * tt + 4 * kg + e;
                 sc[tt][e] = pok[tt] && pos < lim ? d[e] * scale_log2 : -__builtin_inff();
             }
         }
-        // ---- V rows to LDS (zeros where there is no position: 0 * NaN would poison PV)
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int j = 0; j < kVLoads; ++j)
-            *(u32x4*)(vb + (j * kPpl + ps) * kRow + 16 * dg) =
-                vok[j] ? vr[j] : u32x4{0u, 0u, 0u, 0u};
         // ---- online softmax per column (lanes n, n + 16, n + 32, n + 48)
         float cmax = -__builtin_inff();
 #pragma unroll
@@ -679,8 +695,11 @@ void launch_split_hd(const uint16_t* q, const PQueries& qs, const Pages& pg, int
                      hipStream_t s) {
     if constexpr (HD <= 128) {
         if (tok > 1) {
+            // one workgroup per (pair of query groups, kv head, split)
+            const int64_t pairs = ceil_div(ceil_div((int64_t)qs.count, tok), 2);
+            const int64_t wgs = pairs * kvh * nsplit;
             const float scale_log2 = 1.4426950408889634f / sqrtf((float)HD);
-            hipLaunchKernelGGL((paged_attn_prefill_mfma_kernel<HD, Pages>), dim3((unsigned)groups),
+            hipLaunchKernelGGL((paged_attn_prefill_mfma_kernel<HD, Pages>), dim3((unsigned)wgs),
                                dim3(64 * kPWaves), 0, s, q, qs, pg, qh, kvh, scale_log2, ml, acc,
                                nsplit, tok);
             return;

@@ -36,23 +36,42 @@ def model_split_kernel(nq, qh, kvh, kv_len, start_pos, shared_table=True, seq_le
     tok = (2 * HEADS_MAX // G if mfma else
            HEADS_MAX // G if prefill and G < HEADS_MAX else 1)
     NH = 16 if mfma else 4 if G * tok <= 4 else 8
-    items = -(-nq // tok) * kvh * nhb * nsplit
     per_q = kvh * nhb * nsplit
+    waves = []  # (tp0, tq0, ntok, g, hb, split, t_begin, t_end) of each wave that runs the loop
+    if mfma:
+        # workgroup (pair of groups, kv head, split); wave w takes group 2 pair + w, and
+        # both run the chunks of the pair's longest causal length (uniform exits only)
+        for wg in range(-(-(-(-nq // tok)) // 2) * kvh * nsplit):
+            tp0 = (wg // per_q) * 2 * tok
+            if tp0 >= nq:
+                continue
+            g, split = wg % kvh, (wg // kvh) % nsplit
+            clen = causal_len(min(tp0 + 2 * tok, nq) - 1, kv_len, start_pos, max_blocks, seq_lens)
+            t_begin = split * SPLIT
+            if t_begin >= clen:
+                continue
+            for w in range(2):
+                tq0 = tp0 + w * tok
+                waves.append((tp0, tq0, max(0, min(tok, nq - tq0)), g, 0, split, t_begin,
+                              min(clen, t_begin + SPLIT)))
+    else:
+        for item in range(-(-nq // tok) * per_q):
+            tq0 = (item // per_q) * tok
+            if tq0 >= nq:
+                continue
+            ntok = min(tok, nq - tq0)
+            g = item % kvh
+            hb = (item // kvh) % nhb
+            split = (item // (kvh * nhb)) % nsplit
+            clen = causal_len(tq0 + ntok - 1, kv_len, start_pos, max_blocks, seq_lens)
+            t_begin = split * SPLIT
+            if t_begin >= clen:
+                continue
+            waves.append((tq0, tq0, ntok, g, hb, split, t_begin, min(clen, t_begin + SPLIT)))
     written = {}
     q_rows = set()
-    for item in range(items):
-        tq0 = (item // per_q) * tok
-        if tq0 >= nq:
-            continue
-        ntok = min(tok, nq - tq0)
-        g = item % kvh
-        hb = (item // kvh) % nhb
-        split = (item // (kvh * nhb)) % nsplit
-        clen = causal_len(tq0 + ntok - 1, kv_len, start_pos, max_blocks, seq_lens)
-        t_begin = split * SPLIT
-        if t_begin >= clen:
-            continue
-        t_end = min(clen, t_begin + SPLIT)
+    for tp0, tq0, ntok, g, hb, split, t_begin, t_end in waves:
+        clen = t_end  # only its bound on the column lengths matters below
         h0 = g * G + hb * HEADS_MAX
         ncols = ntok * G if tok > 1 else min(HEADS_MAX, G - hb * HEADS_MAX)
         assert ncols <= NH
@@ -61,13 +80,14 @@ def model_split_kernel(nq, qh, kvh, kv_len, start_pos, shared_table=True, seq_le
             col_ok = n < ncols
             ct = n // G if col_ok else 0
             hn = n - ct * G if col_ok else 0
-            row = (tq0 + ct) * qh + h0 + hn
+            # a column past the queries reads the workgroup's first query row (unused)
+            row = ((tq0 + ct) if col_ok else tp0) * qh + h0 + hn
             assert 0 <= row < nq * qh
             if not col_ok:
                 continue
             assert tok > 1 or ct == 0
             col_len = causal_len(tq0 + ct, kv_len, start_pos, max_blocks, seq_lens) \
-                if tok > 1 else clen
+                if tok > 1 else t_end
             lim = min(t_end, col_len)
             q_rows.add(row)
             if mfma:
