@@ -340,15 +340,16 @@ paged_attn_split_kernel(const uint16_t* __restrict__ q, PQueries qs, Pages pg, i
 //     fp16(p) of column 8h + m and row 8 + m is fp16((p - fp16(p)) 2^12) of the same column
 //     (one DPP row rotation by 8 brings each lane its partner column's p), and the output
 //     is D[m] + 2^-12 D[8 + m]: fp32 weights to ~2^-22, V exact.
-//   The two waves of a workgroup take consecutive query groups over the same kv head and
-//     split and share each chunk: each loads half of its K and V rows into LDS, and both read
-//     all of them (the chunk's K and V cross L2 once per 2 x 16 / G queries);
+//   The kPfWaves waves of a workgroup take consecutive query groups over the same kv head and
+//     split and share each chunk: the workgroup loads its K and V rows into LDS once and every
+//     wave reads all of them (the chunk's K and V cross L2 once per kPfWaves x 16 / G queries);
 //   B = V transposed: the chunk's V rows are staged in LDS row-major (rows padded so that the
 //     four rows one transposed read gathers sit on different banks), and
 //     ds_read_b64_tr_b16 gives lane (d, q) dim d of the 4 positions addressed by source
 //     lanes a + 4k of its 16-lane group (destination lane 4a + b takes element b of each).
+constexpr int kPfWaves = 4;  // prefill: waves (query groups) per workgroup sharing each chunk
 template <int HD, class Pages>
-__global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2))) void
+__global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2))) void
 paged_attn_prefill_mfma_kernel(const uint16_t* __restrict__ q, PQueries qs, Pages pg, int qh,
                                int kvh, float scale_log2, float* __restrict__ part_ml,
                                float* __restrict__ part_acc, int nsplit, int tok) {
@@ -356,31 +357,30 @@ paged_attn_prefill_mfma_kernel(const uint16_t* __restrict__ q, PQueries qs, Page
     constexpr int kTiles = 2;
     constexpr int kSteps = HD / 32;
     constexpr int kBlk = HD / 16;  // PV output dim blocks
-    constexpr int kDg = HD / 8;    // lanes per V row load, 8 dims each
-    constexpr int kPpl = 64 / kDg;
-    constexpr int kVLoads = kChunk / kPpl;
     constexpr int kRow = HD * 2 + 32;   // bytes per staged V row
     constexpr int kRowK = HD * 2 + 16;  // per staged K row: 16 rows' reads of one segment
                                         // cover all banks
     static_assert(HD >= 32 && HD <= 128, "head_dim 32, 64 or 128");
-    static_assert(kPWaves == 2 && kTiles == 2, "one tile of each chunk loaded per wave");
+    constexpr int kPieces = kChunk * HD / 8;  // 16-byte pieces of a chunk's K (and of its V)
+    constexpr int kPer = (kPieces + 64 * kPfWaves - 1) / (64 * kPfWaves);
     __shared__ __attribute__((aligned(16))) uint8_t kbuf[kChunk * kRowK];
     __shared__ __attribute__((aligned(16))) uint8_t vbuf[kChunk * kRow];
-    __shared__ __attribute__((aligned(16))) float abuf[kPWaves][64];
+    __shared__ __attribute__((aligned(16))) float abuf[kPfWaves][64];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    // workgroup (pair of query groups, kv head, split); wave w takes group 2 pair + w. Every
+    // workgroup (kPfWaves query groups, kv head, split); wave w takes the set's group w. Every
     // exit before the chunk loop is uniform over the workgroup (the loop has barriers).
     const int64_t wg = blockIdx.x;
     const int64_t per_p = (int64_t)kvh * nsplit;
-    const int tp0 = (int)(wg / per_p) * 2 * tok;  // the pair's first query
+    const int tp0 = (int)(wg / per_p) * kPfWaves * tok;  // the set's first query
     if (tp0 >= qs.count) return;
     const int tq0 = tp0 + wave * tok;
     const int ntok = max(0, min(tok, qs.count - tq0));  // 0: a wave past the last query
     const int g = (int)(wg % kvh);
     const int split = (int)((wg / kvh) % nsplit);
-    const int clen = qs.causal_len(min(tp0 + 2 * tok, qs.count) - 1);  // the pair's longest
+    // the set's longest causal length
+    const int clen = qs.causal_len(min(tp0 + kPfWaves * tok, qs.count) - 1);
     const int t_begin = split * kPSplit;
     if (t_begin >= clen) return;
     const int t_end = min(clen, t_begin + kPSplit);
@@ -409,8 +409,6 @@ paged_attn_prefill_mfma_kernel(const uint16_t* __restrict__ q, PQueries qs, Page
             bq[s] = col_ok ? v : u32x4{0u, 0u, 0u, 0u};
         }
     }
-    const int64_t k_off = ((int64_t)(lane & 15) * kvh + g) * (HD * 2) + 16 * kg;
-    const int dg = lane % kDg, ps = lane / kDg;
     const uint8_t* dummy = (const uint8_t*)q;
     uint8_t* vb = vbuf;
     // transposed-read source of this lane: row 4q + k (+16 for slots 4..7), dims 4a .. 4a + 3
@@ -431,40 +429,39 @@ paged_attn_prefill_mfma_kernel(const uint16_t* __restrict__ q, PQueries qs, Page
 #pragma unroll
         for (int tt = 0; tt < kTiles; ++tt)
             pok[tt] = pg.valid(__builtin_amdgcn_readlane(split_page, j0 + tt));
-        // ---- this wave's tile of the chunk (positions 16 wave ..): K and V rows into
-        // registers; positions past the end or in invalid pages read `dummy` (finite)
-        const int idw = __builtin_amdgcn_readlane(split_page, j0 + wave);
-        const bool pw = pg.valid(idw);
-        const uint8_t* kbw = pw ? pg.k_at(pl, j0 + wave, idw) : dummy;
-        const uint8_t* vbw = pw ? pg.v_at(pl, j0 + wave, idw) : dummy;
-        u32x4 kr[kSteps];
-        {
-            const bool ok = pw && t0 + 16 * wave + (lane & 15) < t_end;
-            const uint8_t* src = ok ? kbw + k_off : dummy;
+        // ---- the chunk's K and V rows, 16-byte pieces spread over the workgroup: piece i is
+        // row i / (HD / 8), segment i % (HD / 8). Rows past the end or in invalid pages read
+        // `dummy` (finite); their V is staged as zeros (0 * NaN would poison PV).
+        const uint8_t* kpg[kTiles];
+        const uint8_t* vpg[kTiles];
 #pragma unroll
-            for (int st = 0; st < kSteps; ++st) kr[st] = ld16(src + 64 * st);
+        for (int tt = 0; tt < kTiles; ++tt) {
+            const int id = __builtin_amdgcn_readlane(split_page, j0 + tt);
+            kpg[tt] = pok[tt] ? pg.k_at(pl, j0 + tt, id) : dummy;
+            vpg[tt] = pok[tt] ? pg.v_at(pl, j0 + tt, id) : dummy;
         }
-        constexpr int kVHalf = kVLoads / 2;
-        u32x4 vr[kVHalf];
-        bool vok[kVHalf];
+        u32x4 kr[kPer], vr[kPer];
+        bool rok[kPer];
 #pragma unroll
-        for (int j = 0; j < kVHalf; ++j) {
-            const int pp = 16 * wave + j * kPpl + ps;  // position in the chunk
-            vok[j] = pw && t0 + pp < t_end;
-            const uint8_t* src =
-                vok[j] ? vbw + (((int64_t)(pp % 16) * kvh + g) * HD + 8 * dg) * 2 : dummy;
-            vr[j] = ld16(src);
+        for (int u = 0; u < kPer; ++u) {
+            const int i = min((int)threadIdx.x + 64 * kPfWaves * u, kPieces - 1);
+            const int r = i / (HD / 8), sg = i % (HD / 8);
+            rok[u] = pok[r / 16] && t0 + r < t_end;
+            const int64_t off = ((int64_t)(r % 16) * kvh + g) * (HD * 2) + 16 * sg;
+            kr[u] = ld16(rok[u] ? kpg[r / 16] + off : dummy);
+            vr[u] = ld16(rok[u] ? vpg[r / 16] + off : dummy);
         }
-        // ---- stage both halves: the other wave has finished reading the previous chunk
+        // ---- stage: every wave has finished reading the previous chunk
         __syncthreads();
 #pragma unroll
-        for (int st = 0; st < kSteps; ++st)
-            *(u32x4*)(kbuf + (16 * wave + (lane & 15)) * kRowK + 64 * st + 16 * kg) = kr[st];
-        // V zeros where there is no position: 0 * NaN would poison PV
-#pragma unroll
-        for (int j = 0; j < kVHalf; ++j)
-            *(u32x4*)(vb + (16 * wave + j * kPpl + ps) * kRow + 16 * dg) =
-                vok[j] ? vr[j] : u32x4{0u, 0u, 0u, 0u};
+        for (int u = 0; u < kPer; ++u) {
+            const int i = (int)threadIdx.x + 64 * kPfWaves * u;
+            if (i < kPieces) {
+                const int r = i / (HD / 8), sg = i % (HD / 8);
+                *(u32x4*)(kbuf + r * kRowK + 16 * sg) = kr[u];
+                *(u32x4*)(vb + r * kRow + 16 * sg) = rok[u] ? vr[u] : u32x4{0u, 0u, 0u, 0u};
+            }
+        }
         __syncthreads();
 
         // ---- QK: lane (n, kg) gets positions 16 tt + 4 kg + e of column n
@@ -695,12 +692,12 @@ void launch_split_hd(const uint16_t* q, const PQueries& qs, const Pages& pg, int
                      hipStream_t s) {
     if constexpr (HD <= 128) {
         if (tok > 1) {
-            // one workgroup per (pair of query groups, kv head, split)
-            const int64_t pairs = ceil_div(ceil_div((int64_t)qs.count, tok), 2);
-            const int64_t wgs = pairs * kvh * nsplit;
+            // one workgroup per (kPfWaves query groups, kv head, split)
+            const int64_t sets = ceil_div(ceil_div((int64_t)qs.count, tok), kPfWaves);
+            const int64_t wgs = sets * kvh * nsplit;
             const float scale_log2 = 1.4426950408889634f / sqrtf((float)HD);
             hipLaunchKernelGGL((paged_attn_prefill_mfma_kernel<HD, Pages>), dim3((unsigned)wgs),
-                               dim3(64 * kPWaves), 0, s, q, qs, pg, qh, kvh, scale_log2, ml, acc,
+                               dim3(64 * kPfWaves), 0, s, q, qs, pg, qh, kvh, scale_log2, ml, acc,
                                nsplit, tok);
             return;
         }

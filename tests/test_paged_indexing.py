@@ -17,6 +17,7 @@ import pytest
 PAGE = 16
 SPLIT = 1024
 HEADS_MAX = 8
+PF_WAVES = 4  # query groups per workgroup of the MFMA prefill kernel
 
 
 def causal_len(qi, kv_len, start_pos, max_blocks, seq_lens=None):
@@ -39,18 +40,19 @@ def model_split_kernel(nq, qh, kvh, kv_len, start_pos, shared_table=True, seq_le
     per_q = kvh * nhb * nsplit
     waves = []  # (tp0, tq0, ntok, g, hb, split, t_begin, t_end) of each wave that runs the loop
     if mfma:
-        # workgroup (pair of groups, kv head, split); wave w takes group 2 pair + w, and
-        # both run the chunks of the pair's longest causal length (uniform exits only)
-        for wg in range(-(-(-(-nq // tok)) // 2) * kvh * nsplit):
-            tp0 = (wg // per_q) * 2 * tok
+        # workgroup (PF_WAVES groups, kv head, split); wave w takes the set's group w, and
+        # all run the chunks of the set's longest causal length (uniform exits only)
+        for wg in range(-(-(-(-nq // tok)) // PF_WAVES) * kvh * nsplit):
+            tp0 = (wg // per_q) * PF_WAVES * tok
             if tp0 >= nq:
                 continue
             g, split = wg % kvh, (wg // kvh) % nsplit
-            clen = causal_len(min(tp0 + 2 * tok, nq) - 1, kv_len, start_pos, max_blocks, seq_lens)
+            clen = causal_len(min(tp0 + PF_WAVES * tok, nq) - 1, kv_len, start_pos, max_blocks,
+                              seq_lens)
             t_begin = split * SPLIT
             if t_begin >= clen:
                 continue
-            for w in range(2):
+            for w in range(PF_WAVES):
                 tq0 = tp0 + w * tok
                 waves.append((tp0, tq0, max(0, min(tok, nq - tq0)), g, 0, split, t_begin,
                               min(clen, t_begin + SPLIT)))
