@@ -160,3 +160,36 @@ def test_reference_interface_rejects_unsupported_head_dim(dev):
     ptr = torch.zeros(1, dtype=torch.int64, device=dev)
     with pytest.raises(RuntimeError):
         K.paged_attention(out, q, bt, ptr, ptr, 4, 1, 0)
+
+
+@pytest.mark.parametrize("qh,kvh,hd", [(32, 8, 128), (8, 8, 64), (12, 2, 256)])
+def test_reference_interface_prefill_masked_page_and_no_blocks(dev, qh, kvh, hd):
+    """Causal prefill with a negative page id in the block table: its 16 positions are masked
+    for every query whose causal length covers them, which equals attending without that page
+    (queries whose length ends inside it see the positions before it). With no blocks at all,
+    every query returns zeros."""
+    rng = np.random.default_rng(qh + hd)
+    kv_len, T, start_pos = 1090, 40, 1050
+    kp, vp, table = build_pool(rng, [kv_len], kvh, hd, extra_pages=2)
+    P = kp.shape[0]
+    tk, tv = dev_t(kp, dev), dev_t(vp, dev)
+    kptr = torch.tensor([tk[i].data_ptr() for i in range(P)], dtype=torch.int64, device=dev)
+    vptr = torch.tensor([vp_.data_ptr() for vp_ in tv], dtype=torch.int64, device=dev)
+    tab = table[0].copy()
+    tab[3] = -1  # positions 48..63
+    q = (rng.standard_normal((T, qh, hd)) * 2).astype(np.float16)
+    tq_ = dev_t(q, dev)
+    out = torch.empty_like(tq_)
+    K.paged_attention(out, tq_, dev_t(tab, dev), kptr, vptr, kvh, kv_len, start_pos)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    keep = np.delete(tab, 3)
+    for t in range(T):
+        clen = min(start_pos + t + 1, kv_len)
+        want = oracle.paged_attention(q[t], keep, clen - 16, kp, vp, kvh)
+        assert_close(got[t].astype(np.float32), want.astype(np.float32), 1e-3, 1e-3,
+                     f"token {t}")
+    empty = torch.full_like(tq_, 7.0)
+    K.paged_attention(empty, tq_, dev_t(tab[:0], dev), kptr, vptr, kvh, 0, 0)
+    torch.cuda.synchronize()
+    assert not empty.cpu().numpy().any()
