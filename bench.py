@@ -21,8 +21,9 @@ and for every configuration (bounded samples, scaled to the full workload).
 Other workloads (parity-tested configurations, printed as their own JSON lines):
   --workload prefill      add+RMSNorm [8192,4096], SwiGLU [8192,14336], softmax/argmax [64,128256]
   --workload tq           TurboQuant compress + dequantize of K and V [32768, 8, 128], 4 and 3 bit
-  --workload attention    decode attention over a K4/V4 page pool, B=64, 32/8 heads, ctx U[1024,32768]
-  --workload paged        the same decode attention over an FP16 page pool (attention_paged.cu)
+  --workload attention    decode attention over a K4/V4 page pool, B=64, 32/8 heads, ctx U[1024,32768],
+                          and causal prefill of one sequence (2048 over 2048, 512 over 8192 positions)
+  --workload paged        the same decode attention and prefill over FP16 pages (attention_paged.cu)
 
 HBM traffic (the roofline's "traffic" field, from profiles/traffic.json):
   rocprofv3 --pmc FETCH_SIZE -d <F> -o pmc -- python3 bench.py --workload pmc
