@@ -2,6 +2,7 @@
 //! counterpart): each method converts its tensors to `FhipTensor` descriptors and makes one
 //! handle-runtime call; shape rules, error messages and staging live in the library.
 
+use crate::ext::BackendExt;
 use crate::ffi::*;
 use fracture_core::{Backend, DType, DeviceTensor, DeviceTimer, FractureError, Result, TensorId};
 use std::ffi::{c_int, c_void, CStr, CString};
@@ -67,7 +68,7 @@ fn descs(ts: &[&DeviceTensor]) -> Result<Vec<FhipTensor>> {
 
 impl HipBackend {
     /// CudaBackend::new (lib.rs:76-114): the backend of device `device_id`.
-    pub fn new(device_id: usize) -> Result<Self> {
+    pub fn new(device_id: i32) -> Result<Self> {
         let mut h = std::ptr::null_mut();
         check(unsafe { fhip_backend_create(device_id as c_int, &mut h) })?;
         let p = unsafe { fhip_device_name(h) };
@@ -86,13 +87,15 @@ impl HipBackend {
         Ok(p)
     }
 
-    /// CudaBackend::stream (lib.rs:127-129): the hipStream_t every launch goes to.
-    pub fn stream(&self) -> *mut c_void {
+    /// CudaBackend::stream (lib.rs:127-129): the stream every launch goes to, for direct
+    /// calls of the raw launchers in `ffi`.
+    pub fn stream(&self) -> hipStream_t {
         unsafe { fhip_stream(self.h) }
     }
 
-    /// CudaBackend::precompute_rope_freqs (lib.rs:133-155).
-    pub fn precompute_rope_freqs(&self, head_dim: usize, theta: f64) -> Result<()> {
+    /// CudaBackend::precompute_rope_freqs (lib.rs:133-155): the frequency table `rope` reads
+    /// (`&mut self` as in the reference; the table lives in the runtime).
+    pub fn precompute_rope_freqs(&mut self, head_dim: usize, theta: f64) -> Result<()> {
         check(unsafe { fhip_precompute_rope_freqs(self.h, head_dim, theta) })
     }
 
@@ -136,42 +139,35 @@ impl HipBackend {
     }
 
     /// The engine's per-sequence attention_paged_tq calls of a decode step (batched.rs:145-194)
-    /// as one call: block_tables is [B, max_blocks] row-major.
+    /// as one call over a registered pool: block_tables is [B, max_blocks] row-major and
+    /// seq_lens has B entries, B being q's first dimension (checked here and in the library,
+    /// which reads the two host arrays only that far).
     #[allow(clippy::too_many_arguments)]
-    pub fn attention_paged_tq_batched(&self, q: &DeviceTensor, block_tables: &[i32],
-                                      max_blocks: usize, seq_lens: &[u32], pool: u64,
-                                      k_rotation: &DeviceTensor, v_rotation: &DeviceTensor,
-                                      k_centroids: &DeviceTensor, v_centroids: &DeviceTensor,
-                                      key_bits: u8, value_bits: u8, num_kv_heads: usize,
-                                      out: &DeviceTensor) -> Result<()> {
-        if block_tables.len() < seq_lens.len() * max_blocks {
-            return Err(FractureError::InvalidShape("block_tables shorter than B * max_blocks".into()));
+    pub fn attention_paged_tq_batched_pool(&self, q: &DeviceTensor, block_tables: &[i32],
+                                           max_blocks: usize, seq_lens: &[u32], pool: u64,
+                                           k_rotation: &DeviceTensor, v_rotation: &DeviceTensor,
+                                           k_centroids: &DeviceTensor,
+                                           v_centroids: &DeviceTensor, key_bits: u8,
+                                           value_bits: u8, num_kv_heads: usize,
+                                           out: &DeviceTensor) -> Result<()> {
+        let b = q.shape.first().copied().unwrap_or(0);
+        if seq_lens.len() != b || block_tables.len() != b * max_blocks {
+            return Err(FractureError::InvalidShape(format!(
+                "attention_paged_tq_batched: {} lengths and {} block-table entries ({} per \
+                 sequence) for {} queries",
+                seq_lens.len(),
+                block_tables.len(),
+                max_blocks,
+                b
+            )));
         }
         check(unsafe {
-            fhip_attention_paged_tq_batched(self.h, &desc(q)?, block_tables.as_ptr(), max_blocks,
-                                            seq_lens.as_ptr(), pool, &desc(k_rotation)?,
-                                            &desc(v_rotation)?, &desc(k_centroids)?,
-                                            &desc(v_centroids)?, key_bits, value_bits,
-                                            num_kv_heads, &desc(out)?)
+            fhip_attention_paged_tq_batched(self.h, &desc(q)?, block_tables.as_ptr(),
+                                            seq_lens.len(), max_blocks, seq_lens.as_ptr(), pool,
+                                            &desc(k_rotation)?, &desc(v_rotation)?,
+                                            &desc(k_centroids)?, &desc(v_centroids)?, key_bits,
+                                            value_bits, num_kv_heads, &desc(out)?)
         })
-    }
-
-    /// residual += delta; normed = rmsnorm(residual) in one pass (engine.rs:692-697 issues
-    /// add then rmsnorm).
-    pub fn add_rmsnorm(&self, residual: &DeviceTensor, delta: &DeviceTensor,
-                       weight: &DeviceTensor, eps: f64, normed: &DeviceTensor) -> Result<()> {
-        check(unsafe {
-            fhip_add_rmsnorm(self.h, &desc(residual)?, &desc(delta)?, &desc(weight)?, eps,
-                             &desc(normed)?)
-        })
-    }
-
-    /// Greedy tokens of logits [rows, vocab] fp32 (the sampler's argmax, sampling.rs:131-158).
-    pub fn argmax_rows(&self, logits: &DeviceTensor) -> Result<Vec<u32>> {
-        let rows = if logits.shape.is_empty() { 0 } else { logits.numel() / logits.shape[logits.shape.len() - 1].max(1) };
-        let mut out = vec![0u32; rows];
-        check(unsafe { fhip_argmax_rows(self.h, &desc(logits)?, out.as_mut_ptr(), rows) })?;
-        Ok(out)
     }
 
     /// Capture the launches issued between graph_begin and graph_end into a replayable graph
@@ -374,5 +370,66 @@ impl Backend for HipBackend {
                                     &desc(k_centroids)?, &desc(v_centroids)?, key_bits,
                                     value_bits, num_kv_heads, kv_len, start_pos, &desc(out)?)
         })
+    }
+}
+
+/// The additive ops on this backend's fused kernels.
+impl BackendExt for HipBackend {
+    /// One pass: residual += delta (rounded), normed = rmsnorm(residual).
+    fn add_rmsnorm(&self, residual: &DeviceTensor, delta: &DeviceTensor,
+                   weight: &DeviceTensor, eps: f64, normed: &DeviceTensor) -> Result<()> {
+        check(unsafe {
+            fhip_add_rmsnorm(self.h, &desc(residual)?, &desc(delta)?, &desc(weight)?, eps,
+                             &desc(normed)?)
+        })
+    }
+
+    fn softmax_rows(&self, logits: &DeviceTensor, temperature: f32,
+                    probs: &DeviceTensor) -> Result<()> {
+        check(unsafe { fhip_softmax_rows(self.h, &desc(logits)?, temperature, &desc(probs)?) })
+    }
+
+    fn argmax_rows(&self, logits: &DeviceTensor) -> Result<Vec<u32>> {
+        let cols = logits.shape.last().copied().unwrap_or(0);
+        let rows = if cols == 0 { 0 } else { logits.numel() / cols };
+        let mut out = vec![0u32; rows];
+        check(unsafe { fhip_argmax_rows(self.h, &desc(logits)?, out.as_mut_ptr(), rows) })?;
+        Ok(out)
+    }
+
+    fn tq_dequantize(&self, packed: &DeviceTensor, norms: &DeviceTensor,
+                     rotation: &DeviceTensor, centroids: &DeviceTensor, bits: u8,
+                     out: &DeviceTensor) -> Result<()> {
+        check(unsafe {
+            fhip_tq_dequantize(self.h, &desc(packed)?, &desc(norms)?, &desc(rotation)?,
+                               &desc(centroids)?, bits, &desc(out)?)
+        })
+    }
+
+    fn tq_quantize_pack(&self, y: &DeviceTensor, centroids: &DeviceTensor, bits: u8,
+                        packed_out: &DeviceTensor) -> Result<()> {
+        check(unsafe {
+            fhip_tq_quantize_pack(self.h, &desc(y)?, &desc(centroids)?, bits, &desc(packed_out)?)
+        })
+    }
+
+    /// The whole batch in one launch sequence: the block lists are registered as a pool for
+    /// the call (their device address arrays built once), then released. Callers that keep
+    /// a pool across steps use `page_pool_create` and `attention_paged_tq_batched_pool`.
+    fn attention_paged_tq_batched(&self, q: &DeviceTensor, block_tables: &[i32],
+                                  max_blocks: usize, seq_lens: &[u32],
+                                  k_packed: &[&DeviceTensor], k_norms: &[&DeviceTensor],
+                                  v_packed: &[&DeviceTensor], v_norms: &[&DeviceTensor],
+                                  k_rotation: &DeviceTensor, v_rotation: &DeviceTensor,
+                                  k_centroids: &DeviceTensor, v_centroids: &DeviceTensor,
+                                  key_bits: u8, value_bits: u8, num_kv_heads: usize,
+                                  out: &DeviceTensor) -> Result<()> {
+        let pool = self.page_pool_create(&[k_packed, k_norms, v_packed, v_norms])?;
+        let run = self.attention_paged_tq_batched_pool(q, block_tables, max_blocks, seq_lens,
+                                                       pool, k_rotation, v_rotation,
+                                                       k_centroids, v_centroids, key_bits,
+                                                       value_bits, num_kv_heads, out);
+        let done = self.page_pool_destroy(pool);
+        run.and(done)
     }
 }

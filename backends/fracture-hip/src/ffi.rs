@@ -1,8 +1,24 @@
-//! The handle runtime of libfracture_hip.so (include/fracture_hip.h, section 2): the C mirror
-//! of the Backend trait that `HipBackend` wraps. Status codes are `FHIP_*`; the message of a
-//! thread's last failing call is `fhip_last_error()`.
+//! The C ABI of libfracture_hip.so (include/fracture_hip.h).
+//!
+//! * Section 1, the raw launchers: `fhip_launch_*`, one for one with the `launch_*` block of
+//!   backends/fracture-cuda/src/ffi.rs:141-274 (device pointers, `c_int` dims, a stream; they
+//!   return a HIP error code, 0 on success). Each is also re-exported under the reference's
+//!   name (`launch_rmsnorm` ..), so code that calls `fracture_cuda::ffi::launch_*` with
+//!   `backend.stream()` (bins/fracture-server-cuda/tests/turboquant_gpu.rs:127-143) compiles
+//!   against `fracture_hip::ffi::*` unchanged.
+//! * Section 2, the handle runtime: the C mirror of the Backend trait that `HipBackend` wraps.
+//!   Status codes are `FHIP_*`; the message of a thread's last failing call is
+//!   `fhip_last_error()`.
 
 use std::ffi::{c_char, c_int, c_void};
+
+/// The stream every launch of a backend goes to (`cudaStream_t` in the CUDA backend).
+#[allow(non_camel_case_types)]
+pub type hipStream_t = *mut c_void;
+/// A HIP runtime status code (`cudaError_t` in the CUDA backend); 0 is success.
+#[allow(non_camel_case_types)]
+pub type hipError_t = c_int;
+pub const HIP_SUCCESS: hipError_t = 0;
 
 pub const FHIP_OK: c_int = 0;
 pub const FHIP_ERR_BACKEND: c_int = 1;
@@ -128,8 +144,8 @@ unsafe extern "C" {
                              block_table: *const i32, num_blocks: usize,
                              start_pos: usize) -> c_int;
     pub fn fhip_attention_paged_tq_batched(b: *mut FhipBackend, q: *const FhipTensor,
-                                           block_tables: *const i32, max_blocks: usize,
-                                           seq_lens: *const u32, pool: u64,
+                                           block_tables: *const i32, num_seqs: usize,
+                                           max_blocks: usize, seq_lens: *const u32, pool: u64,
                                            k_rotation: *const FhipTensor,
                                            v_rotation: *const FhipTensor,
                                            k_centroids: *const FhipTensor,
@@ -141,6 +157,15 @@ unsafe extern "C" {
                             normed_out: *const FhipTensor) -> c_int;
     pub fn fhip_argmax_rows(b: *mut FhipBackend, logits: *const FhipTensor,
                             tokens_out: *mut u32, rows: usize) -> c_int;
+    pub fn fhip_softmax_rows(b: *mut FhipBackend, logits: *const FhipTensor, temperature: f32,
+                             probs: *const FhipTensor) -> c_int;
+    pub fn fhip_tq_dequantize(b: *mut FhipBackend, packed: *const FhipTensor,
+                              norms: *const FhipTensor, rotation: *const FhipTensor,
+                              centroids: *const FhipTensor, bits: u8,
+                              out: *const FhipTensor) -> c_int;
+    pub fn fhip_tq_quantize_pack(b: *mut FhipBackend, y: *const FhipTensor,
+                                 centroids: *const FhipTensor, bits: u8,
+                                 packed_out: *const FhipTensor) -> c_int;
 
     // graph capture of a decode step's device-resident launches
     pub fn fhip_rope_dev(b: *mut FhipBackend, q: *const FhipTensor, k: *const FhipTensor,
@@ -154,3 +179,128 @@ unsafe extern "C" {
     pub fn fhip_graph_launch(b: *mut FhipBackend, graph: u64) -> c_int;
     pub fn fhip_graph_destroy(b: *mut FhipBackend, graph: u64) -> c_int;
 }
+
+// ── Section 1: raw launchers (ffi.rs:141-274 and the additive ones) ────────────────────
+
+unsafe extern "C" {
+    pub fn fhip_launch_rmsnorm(output: *mut c_void, input: *const c_void, weight: *const c_void,
+                               eps: f32, rows: c_int, cols: c_int,
+                               stream: hipStream_t) -> hipError_t;
+    pub fn fhip_launch_rope(q: *mut c_void, k: *mut c_void, positions: *const u32,
+                            freq_table: *const f32, num_tokens: c_int, num_q_heads: c_int,
+                            num_kv_heads: c_int, head_dim: c_int,
+                            stream: hipStream_t) -> hipError_t;
+    pub fn fhip_launch_silu_mul(output: *mut c_void, gate: *const c_void, up: *const c_void,
+                                n: c_int, stream: hipStream_t) -> hipError_t;
+    pub fn fhip_launch_attention(output: *mut c_void, q: *const c_void, k_cache: *const c_void,
+                                 v_cache: *const c_void, num_tokens: c_int, num_q_heads: c_int,
+                                 num_kv_heads: c_int, head_dim: c_int, kv_len: c_int,
+                                 start_pos: c_int, stream: hipStream_t) -> hipError_t;
+    pub fn fhip_launch_paged_attention(output: *mut c_void, q: *const c_void,
+                                       block_table: *const c_int,
+                                       k_block_ptrs: *const *const c_void,
+                                       v_block_ptrs: *const *const c_void, num_tokens: c_int,
+                                       num_q_heads: c_int, num_kv_heads: c_int,
+                                       head_dim: c_int, kv_len: c_int, start_pos: c_int,
+                                       num_blocks_in_seq: c_int,
+                                       stream: hipStream_t) -> hipError_t;
+    pub fn fhip_launch_embedding(output: *mut c_void, table: *const c_void,
+                                 token_ids: *const u32, num_tokens: c_int, hidden_dim: c_int,
+                                 vocab_size: c_int, stream: hipStream_t) -> hipError_t;
+    pub fn fhip_launch_add(output: *mut c_void, a: *const c_void, b: *const c_void, n: c_int,
+                           stream: hipStream_t) -> hipError_t;
+    pub fn fhip_launch_turboquant_compress(input: *const c_void, rotation: *const f32,
+                                           centroids: *const f32, packed_out: *mut c_void,
+                                           norms_out: *mut c_void, num_tokens: c_int,
+                                           num_kv_heads: c_int, head_dim: c_int,
+                                           n_levels: c_int, bits: c_int,
+                                           packed_dim_per_head: c_int,
+                                           stream: hipStream_t) -> hipError_t;
+    pub fn fhip_launch_turboquant_decompress(packed_in: *const c_void, norms_in: *const c_void,
+                                             rotation: *const f32, centroids: *const f32,
+                                             output: *mut c_void, num_tokens: c_int,
+                                             num_kv_heads: c_int, head_dim: c_int, bits: c_int,
+                                             packed_dim_per_head: c_int,
+                                             stream: hipStream_t) -> hipError_t;
+    pub fn fhip_launch_attention_paged_tq(output: *mut c_void, q: *const c_void,
+                                          block_table: *const c_int,
+                                          k_packed_ptrs: *const *const c_void,
+                                          k_norms_ptrs: *const *const c_void,
+                                          v_packed_ptrs: *const *const c_void,
+                                          v_norms_ptrs: *const *const c_void,
+                                          k_rotation: *const f32, v_rotation: *const f32,
+                                          k_centroids: *const f32, v_centroids: *const f32,
+                                          num_tokens: c_int, num_q_heads: c_int,
+                                          num_kv_heads: c_int, head_dim: c_int, kv_len: c_int,
+                                          start_pos: c_int, key_bits: c_int,
+                                          value_bits: c_int, k_packed_dim_per_head: c_int,
+                                          v_packed_dim_per_head: c_int,
+                                          stream: hipStream_t) -> hipError_t;
+    /// CudaBackend::matmul's GEMM (cuda/src/backend.rs:75-128 calls cuBLAS directly).
+    pub fn fhip_launch_matmul(c: *mut c_void, a: *const c_void, b: *const c_void, m: c_int,
+                              n: c_int, k: c_int, stream: hipStream_t) -> hipError_t;
+
+    // additive raw launchers
+    pub fn fhip_launch_attention_paged_tq_ws(output: *mut c_void, q: *const c_void,
+                                             block_table: *const c_int,
+                                             k_packed_ptrs: *const *const c_void,
+                                             k_norms_ptrs: *const *const c_void,
+                                             v_packed_ptrs: *const *const c_void,
+                                             v_norms_ptrs: *const *const c_void,
+                                             k_rotation: *const f32, v_rotation: *const f32,
+                                             k_centroids: *const f32, v_centroids: *const f32,
+                                             num_tokens: c_int, num_q_heads: c_int,
+                                             num_kv_heads: c_int, head_dim: c_int,
+                                             kv_len: c_int, start_pos: c_int, key_bits: c_int,
+                                             value_bits: c_int, k_packed_dim_per_head: c_int,
+                                             v_packed_dim_per_head: c_int,
+                                             workspace: *mut c_void, workspace_bytes: usize,
+                                             stream: hipStream_t) -> hipError_t;
+    pub fn fhip_launch_attention_paged_tq_noalloc(output: *mut c_void, q: *const c_void,
+                                                  block_table: *const c_int,
+                                                  k_packed_ptrs: *const *const c_void,
+                                                  k_norms_ptrs: *const *const c_void,
+                                                  v_packed_ptrs: *const *const c_void,
+                                                  v_norms_ptrs: *const *const c_void,
+                                                  k_rotation: *const f32,
+                                                  v_rotation: *const f32,
+                                                  k_centroids: *const f32,
+                                                  v_centroids: *const f32, num_tokens: c_int,
+                                                  num_q_heads: c_int, num_kv_heads: c_int,
+                                                  head_dim: c_int, kv_len: c_int,
+                                                  start_pos: c_int, key_bits: c_int,
+                                                  value_bits: c_int,
+                                                  k_packed_dim_per_head: c_int,
+                                                  v_packed_dim_per_head: c_int,
+                                                  stream: hipStream_t) -> hipError_t;
+    pub fn fhip_attention_tq_workspace_bytes(batch: c_int, num_q_heads: c_int, head_dim: c_int,
+                                             max_blocks: c_int) -> usize;
+    pub fn fhip_launch_add_rmsnorm(residual: *mut c_void, delta: *const c_void,
+                                   weight: *const c_void, eps: f32, normed_out: *mut c_void,
+                                   rows: c_int, cols: c_int, dtype: c_int,
+                                   stream: hipStream_t) -> hipError_t;
+    pub fn fhip_rows_workspace_bytes(rows: c_int, cols: c_int) -> usize;
+    pub fn fhip_launch_softmax_rows(logits: *const f32, probs: *mut f32, rows: c_int,
+                                    cols: c_int, temperature: f32, workspace: *mut c_void,
+                                    stream: hipStream_t) -> hipError_t;
+    pub fn fhip_launch_argmax_rows(logits: *const f32, index_out: *mut i32,
+                                   flags_out: *mut u32, rows: c_int, cols: c_int,
+                                   workspace: *mut c_void, stream: hipStream_t) -> hipError_t;
+    pub fn fhip_launch_tq_quantize_pack(y: *const f32, centroids: *const f32, n_levels: c_int,
+                                        bits: c_int, packed_out: *mut c_void, rows: c_int,
+                                        head_dim: c_int, packed_dim_per_head: c_int,
+                                        stream: hipStream_t) -> hipError_t;
+}
+
+// The reference's launcher names (ffi.rs:141-274), for callers written against
+// `fracture_cuda::ffi::*`.
+pub use self::fhip_launch_add as launch_add;
+pub use self::fhip_launch_attention as launch_attention;
+pub use self::fhip_launch_attention_paged_tq as launch_attention_paged_tq;
+pub use self::fhip_launch_embedding as launch_embedding;
+pub use self::fhip_launch_paged_attention as launch_paged_attention;
+pub use self::fhip_launch_rmsnorm as launch_rmsnorm;
+pub use self::fhip_launch_rope as launch_rope;
+pub use self::fhip_launch_silu_mul as launch_silu_mul;
+pub use self::fhip_launch_turboquant_compress as launch_turboquant_compress;
+pub use self::fhip_launch_turboquant_decompress as launch_turboquant_decompress;

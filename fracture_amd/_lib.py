@@ -126,7 +126,7 @@ SIGNATURES = {
     "fhip_attention_paged_tq_pool": (I, [P, TP, P, SZ, U64, TP, TP, TP, TP, C.c_uint8,
                                          C.c_uint8, SZ, SZ, SZ, TP]),
     "fhip_tq_append_kv": (I, [P, U64, TP, TP, TP, TP, TP, TP, C.c_uint8, C.c_uint8, P, SZ, SZ]),
-    "fhip_attention_paged_tq_batched": (I, [P, TP, P, SZ, P, U64, TP, TP, TP, TP, C.c_uint8,
+    "fhip_attention_paged_tq_batched": (I, [P, TP, P, SZ, SZ, P, U64, TP, TP, TP, TP, C.c_uint8,
                                             C.c_uint8, SZ, TP]),
     "fhip_add_rmsnorm": (I, [P, TP, TP, TP, D, TP]),
     "fhip_rope_dev": (I, [P, TP, TP, TP, SZ, SZ]),

@@ -438,8 +438,12 @@ class HipBackend:
             for i, row in enumerate(block_tables):
                 bt[i, :len(row)] = row
         width = bt.shape[1]
+        nq = q.shape[0] if q.shape else 0
+        if lens.ndim != 1 or lens.size != nq or bt.shape[0] != nq:
+            raise InvalidShape(f"attention_paged_tq_batched: {lens.size} lengths and "
+                               f"{bt.shape[0]} block-table rows for {nq} queries")
         _check(self._L.fhip_attention_paged_tq_batched(
-            self._h, C.byref(q._c()), bt.ctypes.data, width, lens.ctypes.data, pool,
+            self._h, C.byref(q._c()), bt.ctypes.data, nq, width, lens.ctypes.data, pool,
             C.byref(k_rotation._c()), C.byref(v_rotation._c()), C.byref(k_centroids._c()),
             C.byref(v_centroids._c()), key_bits, value_bits, num_kv_heads, C.byref(out._c())))
 

@@ -245,6 +245,8 @@ paged_attn_split_kernel(const uint16_t* __restrict__ q, PQueries qs, Pages pg, i
         const float mref = m_new == -__builtin_inff() ? 0.0f : m_new;
         const float alpha = __builtin_amdgcn_exp2f(m_run - mref);  // 0 while m_run is -inf
         float psum = 0.0f;
+        // the previous chunk's reads of pbuf / abuf (other lanes' words) stay above these writes
+        wave_lds_sync();
 #pragma unroll
         for (int tt = 0; tt < kTiles; ++tt)
 #pragma unroll
@@ -258,9 +260,10 @@ paged_attn_split_kernel(const uint16_t* __restrict__ q, PQueries qs, Pages pg, i
         l_run = l_run * alpha + psum;
         m_run = m_new;
         abuf[wave][lane] = alpha;
+        // every lane's pbuf / abuf writes stay above the cross-lane reads below
+        wave_lds_sync();
 
-        // ---- PV (this wave's LDS writes above complete before its reads below: one wave's
-        // LDS instructions execute in order)
+        // ---- PV
         float al[kHeadsMax];
         {
             const f4_t a0 = *(const f4_t*)&abuf[wave][0];
@@ -516,9 +519,7 @@ paged_attn_prefill_mfma_kernel(const uint16_t* __restrict__ q, PQueries qs, Page
         l_run = l_run * alpha + psum;
         m_run = m_new;
         abuf[wave][lane] = alpha;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        wave_lds_sync();
         // ---- PV: rescale rows 4 kg + e (columns 8h + 4 (kg % 2) + e), then accumulate
         const f4_t al0 = *(const f4_t*)&abuf[wave][4 * (kg & 1)];
         const f4_t al1 = *(const f4_t*)&abuf[wave][8 + 4 * (kg & 1)];

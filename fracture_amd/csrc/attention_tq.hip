@@ -669,11 +669,7 @@ __device__ __forceinline__ uint64_t split_pages(const Pages& pg, const int32_t* 
     PageAddrs a;
     pg.addrs(ok ? id : first, a.k, a.kn, a.v, a.vn);
     if (lane < kSplitPages) pages[lane] = a;
-    // the wave reads other lanes' entries next: LDS operations of one wave complete in order,
-    // and this keeps the compiler from moving those reads above the write
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    wave_lds_sync();  // the wave reads other lanes' entries next
     return vmask;
 }
 // Loads through global-address-space pointers: addresses read back from LDS lose their
@@ -1019,8 +1015,11 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
             }
         }
         // ---- K norms; then the K and norm registers are free: all loads of the next chunk,
-        // its V codes into the other V buffer
+        // its V codes into the other V buffer. The previous chunk's nb reads are above the
+        // transposed V reads' asm (a compiler barrier); the sync after the write keeps the
+        // cross-lane reads below it also when no copy asm follows (the last chunk).
         nb[nb_idx] = nreg.pack();
+        wave_lds_sync();
         uint8_t* vnext = vb + (par ^ 1) * (kChunkM * 64);
         if (tn < t_end) {
             dma_v(pages, jn, v_lane_off, vnext, lane);

@@ -176,6 +176,18 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Ordering point for an LDS exchange between the lanes of one wave (no other wave involved).
+// The hardware performs one wave's LDS instructions in program order, so no wait is needed;
+// the fences and the barrier stop the compiler from moving a lane's LDS accesses across this
+// point, which it may otherwise do whenever it can show that the lane's own addresses differ
+// (it reasons per lane, not per wave). Place one between the writes and the cross-lane
+// reads, and one between those reads and the next overwrite of the same words.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Workgroup sum of one float per thread. `scratch` holds one float per wave; the result is
 // returned to every thread. Contains two barriers.
 __device__ __forceinline__ float block_sum(float v, float* scratch) {

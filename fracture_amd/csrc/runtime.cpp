@@ -1713,8 +1713,8 @@ int fhip_tq_append_kv(fhip_backend* b, uint64_t pool, const fhip_tensor* keys,
 // engine dispatches Backend::attention_paged_tq once per sequence instead
 // (crates/fracture-engine/src/batched.rs:145-194); the kernels here run the whole batch.
 int fhip_attention_paged_tq_batched(fhip_backend* b, const fhip_tensor* q,
-                                    const int32_t* block_tables, size_t max_blocks,
-                                    const uint32_t* seq_lens, uint64_t pool,
+                                    const int32_t* block_tables, size_t num_seqs,
+                                    size_t max_blocks, const uint32_t* seq_lens, uint64_t pool,
                                     const fhip_tensor* k_rotation, const fhip_tensor* v_rotation,
                                     const fhip_tensor* k_centroids,
                                     const fhip_tensor* v_centroids, uint8_t key_bits,
@@ -1739,6 +1739,14 @@ int fhip_attention_paged_tq_batched(fhip_backend* b, const fhip_tensor* q,
         return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged_tq_batched q %s out %s",
                     shape_str(q).c_str(), shape_str(out).c_str());
     const uint64_t B = q->shape[0], qh = q->shape[1], hd = q->shape[2];
+    // the host arrays hold num_seqs rows: never read past them for a q with more rows
+    if (num_seqs != B)
+        return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged_tq_batched: %zu sequences in the "
+                    "block tables and lengths, %llu queries in q %s", num_seqs,
+                    (unsigned long long)B, shape_str(q).c_str());
+    if (B > 0 && (block_tables == nullptr || seq_lens == nullptr))
+        return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged_tq_batched: null block tables or "
+                    "lengths");
     if (num_kv_heads == 0 || qh % num_kv_heads != 0 || qh / num_kv_heads > 8 || key_bits < 1 ||
         key_bits > 8 || value_bits < 1 || value_bits > 8 || numel(k_rotation) != hd * hd ||
         numel(v_rotation) != hd * hd || numel(k_centroids) < (1ull << key_bits) ||

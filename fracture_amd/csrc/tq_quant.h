@@ -161,6 +161,9 @@ __device__ inline void quantizer_finish(Quantizer& q, int L) {
     const int tid = kOneWave ? (int)(threadIdx.x & 63) : (int)threadIdx.x;
     const int bs = kOneWave ? 64 : (int)blockDim.x;
     const int lane = tid & 63, wave = tid >> 6, nw = bs >> 6;
+    // kOneWave callers write q.c from the same wave just before: lane i reads c[i + 1] below,
+    // another lane's word (the other callers put a workgroup barrier there)
+    if constexpr (kOneWave) build_sync<true>();
     bool ok = true;
     float gmin = __builtin_inff(), cmax = 0.0f;
     for (int i = tid; i < L; i += bs) {

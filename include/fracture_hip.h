@@ -511,10 +511,12 @@ int fhip_tq_append_kv(fhip_backend* b, uint64_t pool, const fhip_tensor* keys,
  * dispatches Backend::attention_paged_tq per sequence, crates/fracture-engine/src/
  * batched.rs:145-194): q [B, qh, hd] fp16, one query per sequence at its last position;
  * sequence i attends seq_lens[i] positions through row i of block_tables (host,
- * [B, max_blocks]); out [B, qh, hd] fp16. max_blocks is at most 65536. */
+ * [num_seqs, max_blocks]); seq_lens holds num_seqs entries; out [B, qh, hd] fp16. num_seqs
+ * must equal B (q's first dimension): the host arrays are read only up to it. max_blocks is
+ * at most 65536. */
 int fhip_attention_paged_tq_batched(fhip_backend* b, const fhip_tensor* q,
-                                    const int32_t* block_tables, size_t max_blocks,
-                                    const uint32_t* seq_lens, uint64_t pool,
+                                    const int32_t* block_tables, size_t num_seqs,
+                                    size_t max_blocks, const uint32_t* seq_lens, uint64_t pool,
                                     const fhip_tensor* k_rotation, const fhip_tensor* v_rotation,
                                     const fhip_tensor* k_centroids,
                                     const fhip_tensor* v_centroids, uint8_t key_bits,

@@ -136,6 +136,27 @@ def test_raw_launchers_reject_bad_arguments_on_host():
     assert lib.fhip_launch_matmul(None, None, None, 0, 4, 4, None) == 0
 
 
+def test_batched_attention_wrapper_rejects_length_mismatch():
+    """The Python wrapper refuses lengths or block-table rows that do not match q's rows before
+    the library reads either host array; matching ones reach the library (which here, with no
+    backend, refuses the null handle)."""
+    from fracture_amd import BackendError, DeviceTensor, DType, HipBackend, InvalidShape, TensorId
+
+    b = HipBackend.__new__(HipBackend)
+    b._L, b._h = _lib.load(), None
+    q = DeviceTensor(TensorId(1), (3, 32, 128), DType.FP16)
+    t = DeviceTensor(TensorId(2), (128, 128), DType.FP32)
+    args = (1, t, t, t, t, 4, 4, 8, q)
+    with pytest.raises(InvalidShape, match="2 lengths"):
+        b.attention_paged_tq_batched(q, [[0], [1], [2]], [16, 16], *args)
+    with pytest.raises(InvalidShape, match="2 block-table rows"):
+        b.attention_paged_tq_batched(q, [[0], [1]], [16, 16, 16], *args)
+    with pytest.raises(InvalidShape, match="4 block-table rows"):
+        b.attention_paged_tq_batched(q, np.zeros((4, 2), np.int32), [16, 16, 16], *args)
+    with pytest.raises(BackendError, match="null backend"):
+        b.attention_paged_tq_batched(q, [[0], [1], [2]], [16, 16, 16], *args)
+
+
 def test_kernels_module_requires_device_tensors():
     import torch
 
@@ -167,3 +188,115 @@ def test_rust_shim_declarations_match_header():
         assert m, f"{name} is not declared in the header"
         n_rust = 0 if not args.strip() else args.count(":")
         assert n_rust == _c_params("(" + m.group(1) + ")"), name
+
+
+# The CUDA backend's raw launchers (backends/fracture-cuda/src/ffi.rs:141-274): name and
+# parameter types in order, the types the HIP crate must mirror (c_int dims, device pointers,
+# a trailing stream).
+REF_LAUNCHERS = {
+    "launch_rmsnorm": ["*mut c_void", "*const c_void", "*const c_void", "f32", "c_int", "c_int",
+                       "stream"],
+    "launch_rope": ["*mut c_void", "*mut c_void", "*const u32", "*const f32", "c_int", "c_int",
+                    "c_int", "c_int", "stream"],
+    "launch_silu_mul": ["*mut c_void", "*const c_void", "*const c_void", "c_int", "stream"],
+    "launch_attention": ["*mut c_void", "*const c_void", "*const c_void", "*const c_void",
+                         "c_int", "c_int", "c_int", "c_int", "c_int", "c_int", "stream"],
+    "launch_paged_attention": ["*mut c_void", "*const c_void", "*const c_int",
+                               "*const *const c_void", "*const *const c_void", "c_int", "c_int",
+                               "c_int", "c_int", "c_int", "c_int", "c_int", "stream"],
+    "launch_embedding": ["*mut c_void", "*const c_void", "*const u32", "c_int", "c_int", "c_int",
+                         "stream"],
+    "launch_add": ["*mut c_void", "*const c_void", "*const c_void", "c_int", "stream"],
+    "launch_turboquant_compress": ["*const c_void", "*const f32", "*const f32", "*mut c_void",
+                                   "*mut c_void", "c_int", "c_int", "c_int", "c_int", "c_int",
+                                   "c_int", "stream"],
+    "launch_turboquant_decompress": ["*const c_void", "*const c_void", "*const f32",
+                                     "*const f32", "*mut c_void", "c_int", "c_int", "c_int",
+                                     "c_int", "c_int", "stream"],
+    "launch_attention_paged_tq": ["*mut c_void", "*const c_void", "*const c_int"]
+    + ["*const *const c_void"] * 4 + ["*const f32"] * 4 + ["c_int"] * 10 + ["stream"],
+}
+
+
+def _rust_fns(src):
+    """name -> list of parameter types of each `pub fn` declared in an extern block."""
+    import re
+
+    out = {}
+    for name, args in re.findall(r"pub fn (\w+)\(([^;{]*?)\)\s*(?:->[^;{]*)?;", src, re.S):
+        types = [a.split(":", 1)[1].strip() for a in args.split(",") if ":" in a]
+        out[name] = types
+    return out
+
+
+def _rust_src(name):
+    from pathlib import Path
+
+    return (Path(__file__).resolve().parents[1] / "backends/fracture-hip/src" / name).read_text()
+
+
+def test_rust_raw_launchers_match_reference_block():
+    """Every launch_* of the reference block exists in the crate's ffi module under its own
+    name (a re-export of fhip_launch_*), with the reference's parameter types and a stream."""
+    ffi = _rust_src("ffi.rs")
+    fns = _rust_fns(ffi)
+    for ref_name, ref_types in REF_LAUNCHERS.items():
+        assert f"pub use self::fhip_{ref_name} as {ref_name};" in ffi, ref_name
+        got = fns["fhip_" + ref_name]
+        want = [("hipStream_t" if t == "stream" else t) for t in ref_types]
+        assert got == want, (ref_name, got)
+    # the stream and status types callers pass and compare (backend.stream(), err == 0)
+    assert "pub type hipStream_t = *mut c_void;" in ffi
+    assert "pub type hipError_t = c_int;" in ffi
+
+
+def test_rust_inherent_api_matches_cuda_backend():
+    """HipBackend's inherent methods have CudaBackend's signatures (cuda/src/lib.rs:76-161),
+    as the bins and tests call them: new(i32), get_ptr(TensorId), stream(),
+    precompute_rope_freqs(&mut self, usize, f64)."""
+    import re
+
+    be = re.sub(r"\s+", " ", _rust_src("backend.rs"))
+    assert "pub fn new(device_id: i32) -> Result<Self>" in be
+    assert "pub fn get_ptr(&self, id: TensorId) -> Result<*mut c_void>" in be
+    assert "pub fn stream(&self) -> hipStream_t" in be
+    assert "pub fn precompute_rope_freqs(&mut self, head_dim: usize, theta: f64) -> Result<()>" in be
+    assert "impl Backend for HipBackend" in be and "impl BackendExt for HipBackend" in be
+
+
+def test_rust_backend_ext_has_defaults_and_overrides():
+    """BackendExt declares each additive op with a default body (other backends need no
+    change), and HipBackend overrides every one of them."""
+    import re
+
+    ext = _rust_src("ext.rs")
+    trait = ext[ext.index("pub trait BackendExt: Backend {"):]
+    ops = re.findall(r"\n    fn (\w+)\(", trait)
+    assert sorted(ops) == sorted(["add_rmsnorm", "softmax_rows", "argmax_rows", "tq_dequantize",
+                                  "tq_quantize_pack", "attention_paged_tq_batched"])
+    for op in ops:  # a body, not a bare declaration
+        sig_end = re.search(r"\n    fn " + op + r"\([^{;]*?\)\s*->\s*Result<[^{;]*?>\s*([{;])", trait, re.S)
+        assert sig_end and sig_end.group(1) == "{", op
+    be = _rust_src("backend.rs")
+    impl = be[be.index("impl BackendExt for HipBackend {"):]
+    assert sorted(re.findall(r"\n    fn (\w+)\(", impl)) == sorted(ops)
+
+
+def test_rust_sources_are_balanced():
+    """A cheap syntax screen (no Rust toolchain in the image): brackets balance in every crate
+    source once strings, chars and comments are removed."""
+    import re
+
+    for name in ("lib.rs", "ffi.rs", "backend.rs", "ext.rs"):
+        s = _rust_src(name)
+        s = re.sub(r"//[^\n]*", "", s)
+        s = re.sub(r'"(?:\\[\s\S]|[^"\\])*"', '""', s)  # a \<newline> continues a string
+        s = re.sub(r"'(?:\\.|[^'\\])'", "''", s)
+        stack = []
+        pairs = {")": "(", "]": "[", "}": "{"}
+        for ch in s:
+            if ch in "([{":
+                stack.append(ch)
+            elif ch in ")]}":
+                assert stack and stack.pop() == pairs[ch], name
+        assert not stack, name

@@ -1,11 +1,14 @@
 """Graph capture of the handle runtime: a decode step's elementwise chain (embedding, add +
 RMSNorm, RoPE, SwiGLU, add, RMSNorm, copy_rows; the per-layer sequence of engine.rs:621-706
-without its GEMMs and attention) recorded once and replayed with fresh inputs, every replay
-bit-identical to the same ops run eagerly; the ops that cannot be recorded are refused and
-record nothing."""
+without its GEMMs and attention) recorded once and replayed with fresh inputs. Every replay is
+bit-identical to the same ops run eagerly, and every op of every replay matches the oracle on
+that op's own inputs (bit-exact for the gather, the adds and the row copy; the 1e-3 rule for
+RMSNorm, RoPE and SwiGLU). The ops that cannot be recorded are refused and record nothing."""
 import numpy as np
 import pytest
 
+import oracle
+from conftest import assert_close
 from fracture_amd import BackendError, DType, HipBackend
 
 pytestmark = pytest.mark.gpu
@@ -42,7 +45,8 @@ def _tensors(b):
 
 def _inputs(seed):
     rng = np.random.default_rng(100 + seed)
-    ids = rng.integers(0, VOCAB + 5, T).astype(np.uint32)  # some ids past the vocabulary
+    ids = rng.integers(0, VOCAB, T).astype(np.uint32)
+    ids[seed % T] = VOCAB + seed % 5  # one id past the vocabulary: a zero row
     pos = rng.integers(0, 8192, T).astype(np.uint32)
     h = rng.standard_normal((T, HID)).astype(np.float16)
     q = rng.standard_normal((T, QH, HD)).astype(np.float16)
@@ -74,11 +78,31 @@ def _read(b, t):
     return {n: b.download(t[n]).copy() for n in OUTS}
 
 
+def _check_vs_oracle(got, inp, table, w, freqs, what):
+    """Each op of one chain run against the oracle, fed the inputs that op saw on the GPU."""
+    def same(a, b, name):
+        assert np.array_equal(a.view(np.uint16), b.view(np.uint16)), f"{what}: {name}"
+
+    same(got["x"], oracle.embedding(table, inp["ids"]), "embedding")
+    h_ref, n1_ref = oracle.add_rmsnorm(inp["h"], got["x"], w, EPS)
+    same(got["h"], h_ref, "add+RMSNorm residual")
+    assert_close(got["n1"], n1_ref, 1e-3, 1e-3, f"{what}: add+RMSNorm")
+    assert_close(got["q"], oracle.rope(inp["q"], inp["pos"], freqs), 1e-3, 1e-3, f"{what}: RoPE q")
+    assert_close(got["k"], oracle.rope(inp["k"], inp["pos"], freqs), 1e-3, 1e-3, f"{what}: RoPE k")
+    assert_close(got["mid"], oracle.silu_mul(inp["gate"], inp["up"]), 1e-3, 1e-3, f"{what}: SwiGLU")
+    same(got["h2"], oracle.add(got["h"], got["n1"]), "add")
+    assert_close(got["n2"], oracle.rmsnorm(got["h2"], w, EPS), 1e-3, 1e-3, f"{what}: RMSNorm")
+    same(got["save"][:T], np.zeros((T, HID), np.float16), "copy_rows (rows left alone)")
+    same(got["save"][T:], got["n2"], "copy_rows")
+
+
 def test_graph_replays_match_eager():
     with HipBackend(0) as b:
         b.precompute_rope_freqs(HD, 500000.0)
         t = _tensors(b)
         table = b.download(t["table"]).copy()
+        w = b.download(t["w"]).copy()
+        freqs = oracle.rope_freqs(HD, 500000.0)
         side = b.upload(np.random.default_rng(9).standard_normal((4, 3000)).astype(np.float32))
         probs = b.alloc([4, 3000], DType.FP32)
         _load(b, t, _inputs(0))
@@ -90,6 +114,7 @@ def test_graph_replays_match_eager():
                 b.graph_launch(g)
                 b.synchronize()
                 got = _read(b, t)
+                _check_vs_oracle(got, inp, table, w, freqs, f"replay {it}")
                 # eager work between replays, then the same ops eagerly on the same inputs
                 b.softmax_rows(side, 1.0, probs)
                 b.synchronize()
@@ -105,6 +130,7 @@ def test_graph_replays_match_eager():
                 rows = np.where((ids < VOCAB)[:, None], table[np.minimum(ids, VOCAB - 1)], 0)
                 assert np.array_equal(got["x"].view(np.uint16),
                                       rows.astype(np.float16).view(np.uint16))
+                assert (ids >= VOCAB).any() and (ids < VOCAB).any()
             # two replays back to back apply RoPE twice in place, like two eager passes
             inp = _inputs(7)
             _load(b, t, inp)

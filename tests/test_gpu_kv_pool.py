@@ -197,6 +197,18 @@ def test_attention_batched_pool(backend, hd, kb, vb):
         bad[2][3] = P + 1
         backend.attention_paged_tq_batched(tq_, bad, lens, pool, tkr, tvr, tkc, tvc, kb, vb, kvh,
                                            out)
+    # the C entry reads the host arrays only up to num_seqs, which must equal q's rows
+    import ctypes as C
+    from fracture_amd import _lib
+    bt = np.full((B, max(nbs)), -1, np.int32)
+    for i, t in enumerate(tables):
+        bt[i, :len(t)] = t
+    lens_u = np.array(lens, np.uint32)
+    rc = _lib.load().fhip_attention_paged_tq_batched(
+        backend._h, C.byref(tq_._c()), bt.ctypes.data, B - 1, bt.shape[1], lens_u.ctypes.data,
+        pool, C.byref(tkr._c()), C.byref(tvr._c()), C.byref(tkc._c()), C.byref(tvc._c()), kb, vb,
+        kvh, C.byref(out._c()))
+    assert rc == 2 and b"sequences in the block tables" in _lib.load().fhip_last_error()
     # the block table and lengths travel through the backend's ring of 16 host staging slots,
     # read by the device in place: alternate two different batches for more than a turn of
     # the ring, queued back to back, and each call must give its batch's first output again

@@ -70,6 +70,7 @@ class PagedCache:
 
     def __init__(self, backend, layers, kvh, hd, pool=6, order=(4, 1, 5, 0, 2, 3)):
         self.b = backend
+        self.kvh = kvh
         self.k = [[backend.alloc([16, kvh, hd], DType.FP16) for _ in range(pool)]
                   for _ in range(layers)]
         self.v = [[backend.alloc([16, kvh, hd], DType.FP16) for _ in range(pool)]
@@ -91,6 +92,11 @@ class PagedCache:
             self.b.copy_rows(k_mh, self.k[layer][blk], t, off, cnt)
             self.b.copy_rows(v_mh, self.v[layer][blk], t, off, cnt)
             t += cnt
+
+    def attention(self, layer, q_mh, n, start, out_mh):
+        """Backend::attention_paged of the T queries at start .. start + T over n positions."""
+        self.b.attention_paged(q_mh, self.table(n), self.k[layer], self.v[layer], self.kvh, n,
+                               start, out_mh)
 
     def free(self):
         for lst in self.k + self.v:
@@ -129,8 +135,7 @@ def forward(b, W, cfg, ids, cache, record):
         record("k_rope", L, k)
         cache.append(L, k_mh, v_mh, start)
         n = start + T
-        b.attention_paged(q_mh, cache.table(n), cache.k[L], cache.v[L], nkv, n, start,
-                          attn.reshape([T, nq, hd]))
+        cache.attention(L, q_mh, n, start, attn.reshape([T, nq, hd]))
         b.matmul(attn, w.o_proj, proj)
         record("attn_output", L, proj)
         b.add(h, proj, h)

@@ -441,8 +441,11 @@ def test_kv_planned_dequant_vs_oracle(dev, kb, vb):
 
 
 def test_kv_planned_layer_scale(dev):
-    """The K+V launch at one layer of Llama-3.1-8B (32768 tokens x 8 kv heads, 4 bits): bytes
-    equal the per-tensor planned launches, which the oracle pins above."""
+    """The K+V launch at one layer of Llama-3.1-8B (32768 tokens x 8 kv heads, 4 bits), the
+    launch the compress / dequantize benchmark times: bytes equal the oracle's quantize-pack of
+    the rotate entry's fp32 y and norms for every one of the 262,144 vectors of each tensor,
+    and the K+V dequantize equals the oracle's dequantize within the 1e-3 rule; both also
+    equal the per-tensor planned launches bit for bit."""
     rng = np.random.default_rng(77)
     N, H = 32768, 8
     xs = [(rng.standard_normal((N, H, 128), dtype=np.float32) *
@@ -455,7 +458,13 @@ def test_kv_planned_layer_scale(dev):
     fused = [(torch.empty((N, H * 64), dtype=torch.uint8, device=dev),
               torch.empty((N, H), dtype=torch.float16, device=dev)) for _ in range(2)]
     K.tq_compress_kv_planned(plans[0], plans[1], tx[0], tx[1], *fused[0], *fused[1])
+    torch.cuda.synchronize()
     for i in range(2):
+        y, yn = rotate(xs[i], rots[i], dev)
+        got = fused[i][0].cpu().numpy().reshape(N * H, 64)
+        assert np.array_equal(got, oracle.tq_quantize_pack(y, cent, 4)), f"tensor {i} bytes"
+        assert np.array_equal(fused[i][1].cpu().numpy().reshape(-1).view(np.uint16),
+                              yn.view(np.uint16)), f"tensor {i} norms"
         single = torch.empty_like(fused[i][0]), torch.empty_like(fused[i][1])
         K.tq_compress_planned(plans[i], tx[i], *single)
         torch.cuda.synchronize()
@@ -463,7 +472,12 @@ def test_kv_planned_layer_scale(dev):
         assert torch.equal(single[1].view(torch.int16), fused[i][1].view(torch.int16))
     outs = [torch.empty((N, H, 128), dtype=torch.float16, device=dev) for _ in range(2)]
     K.tq_dequant_kv_planned(plans[0], plans[1], *fused[0], *fused[1], outs[0], outs[1])
+    torch.cuda.synchronize()
     for i in range(2):
+        ref = oracle.tq_dequant(fused[i][0].cpu().numpy().reshape(N * H, 64),
+                                fused[i][1].cpu().numpy().reshape(-1), rots[i], cent, 4, 128)
+        assert_close(outs[i].cpu().numpy().reshape(-1, 128).astype(np.float32),
+                     ref.astype(np.float32), 1e-3, 1e-3, f"K+V dequantize tensor {i} vs oracle")
         want = torch.empty_like(outs[i])
         K.tq_dequant_planned(plans[i], *fused[i], want)
         torch.cuda.synchronize()
