@@ -64,6 +64,9 @@ struct F16PtrPages {
     }
     __device__ const uint8_t* k_at(const Lane& l, int j, int) const { return rl(l.k, j); }
     __device__ const uint8_t* v_at(const Lane& l, int j, int) const { return rl(l.v, j); }
+    // one lane's own page (any page id per lane)
+    __device__ const uint8_t* k_page(int p) const { return k[p]; }
+    __device__ const uint8_t* v_page(int p) const { return v[p]; }
 };
 struct F16PoolPages {
     const uint8_t* k;
@@ -75,6 +78,8 @@ struct F16PoolPages {
     __device__ Lane lane_load(int) const { return Lane{}; }
     __device__ const uint8_t* k_at(const Lane&, int, int p) const { return k + p * sk; }
     __device__ const uint8_t* v_at(const Lane&, int, int p) const { return v + p * sv; }
+    __device__ const uint8_t* k_page(int p) const { return k + p * sk; }
+    __device__ const uint8_t* v_page(int p) const { return v + p * sv; }
 };
 
 // Query i reads block-table row i (stride 0: one shared table) and attends to seq_lens[i]
@@ -575,6 +580,83 @@ paged_attn_prefill_mfma_kernel(const uint16_t* __restrict__ q, PQueries qs, Page
     }
 }
 
+// Any other head_dim (1 .. 256; the reference kernel takes any width): one wave per (query,
+// q head, 1024-position split), same partials as paged_attn_split_kernel. Per 64-position
+// chunk, lane l scores position t0 + l against the query (fp32 dot over the dims in order,
+// the query staged in LDS), the wave updates the online softmax (natural-log units), and each
+// lane accumulates its dims l, l + 64, .. over the chunk's positions, their weights and row
+// addresses broadcast from the lanes that scored them. A fallback for widths no model on this
+// path uses at scale (the tiny test models' 16, odd widths): no MFMA, no vector loads.
+constexpr int kGenWaves = 4;
+template <class Pages>
+__global__ __launch_bounds__(64 * kGenWaves) void paged_attn_generic_kernel(
+    const uint16_t* __restrict__ q, PQueries qs, Pages pg, int qh, int kvh, int hd,
+    float scale, float* __restrict__ part_ml, float* __restrict__ part_acc, int nsplit,
+    int64_t items) {
+    __shared__ float qbuf[kGenWaves][256];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t item = (int64_t)blockIdx.x * kGenWaves + wave;
+    if (item >= items) return;
+    const int split = (int)(item % nsplit);
+    const int64_t vec = item / nsplit;  // query qi, q head h
+    const int qi = (int)(vec / qh), h = (int)(vec % qh);
+    const int clen = qs.causal_len(qi);
+    const int t_begin = split * kPSplit;
+    if (t_begin >= clen) return;  // not read by the combine (splits below the length only)
+    const int t_end = min(clen, t_begin + kPSplit);
+    const int g = h / (qh / kvh);
+    const int32_t* table = qs.table + (int64_t)qi * qs.table_stride;
+    float* qv = qbuf[wave];
+    for (int d = lane; d < hd; d += 64) qv[d] = h2f(q[vec * hd + d]);
+    wave_lds_sync();  // every lane reads every dim below
+    float m_run = -__builtin_inff(), l_run = 0.0f;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // dims lane + 64 i
+    const int64_t row_bytes = (int64_t)hd * 2;
+    for (int t0 = t_begin; t0 < t_end; t0 += 64) {
+        const int pos = t0 + lane;
+        const int id = pos < t_end ? table[pos / FHIP_PAGE_TOKENS] : -1;
+        const bool ok = pos < t_end && pg.valid(id);
+        const int64_t roff = ((int64_t)(pos % FHIP_PAGE_TOKENS) * kvh + g) * row_bytes;
+        const uint16_t* krow = ok ? (const uint16_t*)(pg.k_page(id) + roff) : nullptr;
+        const uint16_t* vrow = ok ? (const uint16_t*)(pg.v_page(id) + roff) : nullptr;
+        float s = -__builtin_inff();
+        if (ok) {
+            float dot = 0.0f;
+            for (int d = 0; d < hd; ++d) dot = fmaf(qv[d], h2f(krow[d]), dot);
+            s = dot * scale;
+        }
+        const float cmax = wave_max(s);
+        const float m_new = fmaxf(m_run, cmax);
+        const float alpha = m_run == -__builtin_inff() ? 0.0f : expf(m_run - m_new);
+        const float p = ok ? expf(s - m_new) : 0.0f;
+        l_run = l_run * alpha + wave_sum(p);
+        m_run = m_new;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] *= alpha;
+        const int n = min(64, t_end - t0);
+        for (int j = 0; j < n; ++j) {
+            const float pj = __shfl(p, j);
+            const uint64_t vj = (uint64_t)__shfl((long long)(uintptr_t)vrow, j);
+            if (vj == 0) continue;  // uniform: position j is masked
+            const uint16_t* vr = (const uint16_t*)(uintptr_t)vj;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = lane + 64 * i;
+                if (d < hd) acc[i] = fmaf(pj, h2f(vr[d]), acc[i]);
+            }
+        }
+    }
+    if (lane == 0) {
+        part_ml[(vec * nsplit + split) * 2 + 0] = m_run;
+        part_ml[(vec * nsplit + split) * 2 + 1] = l_run;
+    }
+    float* dst = part_acc + (vec * nsplit + split) * hd;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (lane + 64 * i < hd) dst[lane + 64 * i] = acc[i];
+}
+
 // Merge of the splits of one (query, q head) vector per workgroup:
 // out = (sum_s w_s acc_s) / (sum_s w_s l_s), w_s = exp(m_s - max m); zeros when the query
 // attends to no position. The split weights are computed once, in parallel, into LDS; each
@@ -672,9 +754,9 @@ size_t paged_ws_layout(int nq, int qh, int hd, int max_tokens, size_t* off_acc, 
     return al(ml) + al(acc);
 }
 
+// head_dim 32 / 64 / 128 / 256 run the MFMA kernels, any other width up to 256 the generic one
 bool paged_shape_ok(int qh, int kvh, int hd) {
-    return kvh > 0 && qh > 0 && qh % kvh == 0 &&
-           (hd == 32 || hd == 64 || hd == 128 || hd == 256);
+    return kvh > 0 && qh > 0 && qh % kvh == 0 && hd >= 1 && hd <= 256;
 }
 
 template <int HD, int NH, class Pages>
@@ -733,6 +815,14 @@ int launch_paged(void* out, const void* q, const PQueries& qs, int nq, const Pag
     PQueries q2 = qs;
     q2.count = nq;
     const uint16_t* qp = (const uint16_t*)q;
+    if (hd != 32 && hd != 64 && hd != 128 && hd != 256) {
+        const int64_t gitems = (int64_t)nq * qh * nsplit;
+        const int64_t gwgs = ceil_div(gitems, kGenWaves);
+        if (gwgs > 0x7fffffff) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((paged_attn_generic_kernel<Pages>), dim3((unsigned)gwgs),
+                           dim3(64 * kGenWaves), 0, s, qp, q2, pg, qh, kvh, hd,
+                           1.0f / sqrtf((float)hd), ml, acc, nsplit, gitems);
+    } else {
     switch (hd) {
         case 32:
             launch_split_hd<32>(qp, q2, pg, qh, kvh, nhb, ml, acc, nsplit, tok, groups, s);
@@ -746,6 +836,7 @@ int launch_paged(void* out, const void* q, const PQueries& qs, int nq, const Pag
         default:
             launch_split_hd<256>(qp, q2, pg, qh, kvh, nhb, ml, acc, nsplit, tok, groups, s);
             break;
+    }
     }
     const int64_t nvec = (int64_t)nq * qh;
     if (nsplit <= kCombWaveMaxSplits)

@@ -1485,9 +1485,9 @@ int fhip_attention_paged_pool(fhip_backend* b, const fhip_tensor* q, const int32
                     shape_str(q).c_str(), shape_str(out).c_str());
     const uint64_t T = q->shape[0], qh = q->shape[1], hd = q->shape[2];
     if (num_kv_heads == 0 || qh % num_kv_heads != 0 ||
-        !(hd == 32 || hd == 64 || hd == 128 || hd == 256))
+        hd == 0 || hd > 256)
         return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged: %zu q heads, %zu kv heads, "
-                    "head_dim %zu (32, 64, 128 or 256)", (size_t)qh, num_kv_heads, (size_t)hd);
+                    "head_dim %zu (1 to 256)", (size_t)qh, num_kv_heads, (size_t)hd);
     if (kv_len > 0x7fffffffu || start_pos > 0x7fffffffu || T > 0x7fffffffu)
         return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged: sizes beyond int32");
     const uint64_t needed_blocks = (kv_len + FHIP_PAGE_TOKENS - 1) / FHIP_PAGE_TOKENS;
@@ -1835,9 +1835,9 @@ int fhip_attention_paged(fhip_backend* b, const fhip_tensor* q, const int32_t* b
                     shape_str(q).c_str(), shape_str(out).c_str());
     const uint64_t T = q->shape[0], qh = q->shape[1], hd = q->shape[2];
     if (num_kv_heads == 0 || qh % num_kv_heads != 0 ||
-        !(hd == 32 || hd == 64 || hd == 128 || hd == 256))
+        hd == 0 || hd > 256)
         return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged: %zu q heads, %zu kv heads, "
-                    "head_dim %zu (32, 64, 128 or 256)", (size_t)qh, num_kv_heads, (size_t)hd);
+                    "head_dim %zu (1 to 256)", (size_t)qh, num_kv_heads, (size_t)hd);
     if (kv_len > 0x7fffffffu || start_pos > 0x7fffffffu || T > 0x7fffffffu)
         return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged: sizes beyond int32");
     const uint64_t needed_blocks = (kv_len + FHIP_PAGE_TOKENS - 1) / FHIP_PAGE_TOKENS;

@@ -123,9 +123,10 @@ int fhip_launch_attention_paged_tq(void* output, const void* q, const int* block
 /* ffi.rs:186-200 `launch_paged_attention` (attention_paged.cu:172-185): causal GQA attention
  * of q [T, qh, hd] fp16 over FP16 pages given as per-block pointer arrays (device memory,
  * indexed by the physical block ids of block_table), each block [16, kvh, hd] fp16. head_dim
- * is 32, 64, 128 or 256. Unlike the reference kernel it keeps no kv_len-sized score row: a
- * block table may describe up to 1,048,576 positions. The split partials come from a
- * stream-ordered allocation on `stream` (see fhip_launch_paged_attention_ws). */
+ * is 1 to 256 (32, 64, 128 and 256 run MFMA kernels, other widths a generic one). Unlike the
+ * reference kernel it keeps no kv_len-sized score row: a block table may describe up to
+ * 1,048,576 positions. The split partials come from a stream-ordered allocation on `stream`
+ * (see fhip_launch_paged_attention_ws). */
 int fhip_launch_paged_attention(void* output, const void* q, const int* block_table,
                                 const void** k_block_ptrs, const void** v_block_ptrs,
                                 int num_tokens, int num_q_heads, int num_kv_heads, int head_dim,

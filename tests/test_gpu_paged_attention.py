@@ -3,8 +3,9 @@
 
 Covers the batched decode entry over contiguous page pools (one query per sequence,
 per-sequence lengths around page and 1024-position split edges, permuted block tables, GQA
-groups of 1 to 12 q heads, head_dim 32 / 64 / 128 / 256, masked pages, empty sequences) and the
-reference-interface entry with per-block pointer arrays and causal prefill queries.
+groups of 1 to 12 q heads, head_dim 32 / 64 / 128 / 256 on the MFMA kernels and 16 / 20 / 80 /
+96 on the generic kernel, masked pages, empty sequences) and the reference-interface entry with
+per-block pointer arrays and causal prefill queries.
 """
 import numpy as np
 import pytest
@@ -51,7 +52,7 @@ def run_decode(dev, q, table, lens, kp, vp, kvh):
     return out.cpu().numpy()
 
 
-@pytest.mark.parametrize("hd", [32, 64, 128, 256])
+@pytest.mark.parametrize("hd", [32, 64, 128, 256, 16, 20, 96])
 @pytest.mark.parametrize("qh,kvh", [(32, 8), (8, 8), (16, 1), (24, 2)])
 def test_decode_small_contexts(dev, hd, qh, kvh):
     rng = np.random.default_rng(hd * 100 + qh + kvh)
@@ -65,7 +66,7 @@ def test_decode_small_contexts(dev, hd, qh, kvh):
                      f"seq {b} len {n}")
 
 
-@pytest.mark.parametrize("hd", [128, 64])
+@pytest.mark.parametrize("hd", [128, 64, 80])
 def test_decode_split_edges(dev, hd):
     """Lengths around the 1024-position splits: the combine merges 1 to 3 splits."""
     rng = np.random.default_rng(7 + hd)
@@ -123,7 +124,9 @@ def test_decode_empty_sequence_and_masked_pages(dev):
     (1050, 19, 1020, 4, 4, 128), (300, 13, 0, 8, 4, 32), (1100, 11, 1019, 6, 2, 256),
     (70, 70, 0, 8, 2, 128), (2100, 9, 2040, 16, 16, 64), (50, 7, 43, 16, 2, 64),
     # 16 / G queries per wave on the MFMA prefill kernel: G = 8 (2 queries), G = 1 (16)
-    (2100, 33, 2067, 32, 4, 128), (600, 37, 563, 4, 4, 64), (1030, 21, 1010, 24, 3, 32)])
+    (2100, 33, 2067, 32, 4, 128), (600, 37, 563, 4, 4, 64), (1030, 21, 1010, 24, 3, 32),
+    # the generic kernel (other head_dims): one query per wave
+    (5, 5, 0, 4, 2, 16), (1040, 9, 1031, 8, 2, 96), (40, 17, 23, 6, 3, 20)])
 def test_reference_interface_prefill_causal(dev, kv_len, T, start_pos, qh, kvh, hd):
     """fhip_launch_paged_attention: T queries at start_pos.. over per-block pointer arrays;
     query i attends to min(start_pos + i + 1, kv_len) positions."""
@@ -154,7 +157,7 @@ def test_reference_interface_prefill_causal(dev, kv_len, T, start_pos, qh, kvh, 
 
 
 def test_reference_interface_rejects_unsupported_head_dim(dev):
-    q = torch.zeros((1, 4, 96), dtype=torch.float16, device=dev)
+    q = torch.zeros((1, 4, 264), dtype=torch.float16, device=dev)
     out = torch.empty_like(q)
     bt = torch.zeros(1, dtype=torch.int32, device=dev)
     ptr = torch.zeros(1, dtype=torch.int64, device=dev)
@@ -162,7 +165,7 @@ def test_reference_interface_rejects_unsupported_head_dim(dev):
         K.paged_attention(out, q, bt, ptr, ptr, 4, 1, 0)
 
 
-@pytest.mark.parametrize("qh,kvh,hd", [(32, 8, 128), (8, 8, 64), (12, 2, 256)])
+@pytest.mark.parametrize("qh,kvh,hd", [(32, 8, 128), (8, 8, 64), (12, 2, 256), (4, 2, 16)])
 def test_reference_interface_prefill_masked_page_and_no_blocks(dev, qh, kvh, hd):
     """Causal prefill with a negative page id in the block table: its 16 positions are masked
     for every query whose causal length covers them, which equals attending without that page
