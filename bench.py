@@ -1062,6 +1062,17 @@ def cpu_config_baselines(seconds: float):
                 "GB/s_1core": round(gbs(nbytes, t1 * scale * 1e6), 3),
                 "GB/s_all_cores": round(gbs(nbytes, tN * scale * 1e6), 3), "sample": sample}
 
+    # the CPU configuration itself: fp32 add + RMSNorm on [32, 4096], X and the residual
+    # ~N(0,1), weight ~U(0.5,1.5), seed 0, eps 1e-5 (the whole workload, no scaling)
+    r1 = np.random.default_rng(0)
+    x1 = r1.standard_normal((32, 4096)).astype(np.float32)
+    res1 = r1.standard_normal((32, 4096)).astype(np.float32)
+    w1 = r1.uniform(0.5, 1.5, 4096).astype(np.float32)
+    out["c1_add_rmsnorm_fp32_32x4096"] = both(
+        lambda: oracle.add_rmsnorm(res1, x1, w1, 1e-5),
+        lambda: par_rows(lambda a, b: oracle.add_rmsnorm(a, b, w1, 1e-5), [res1, x1], 32, th),
+        1.0, 4 * 32 * 4096 * 4 + 4096 * 4, "the whole workload (32 rows)")
+
     R = 512
     h = rng.standard_normal((R, 4096)).astype(np.float16)
     d = rng.standard_normal((R, 4096)).astype(np.float16)

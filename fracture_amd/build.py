@@ -6,6 +6,12 @@ Every HIP source under ``csrc/`` compiles to an object under ``_build/`` and lin
 is built with ``-ffp-contract=off`` so its double arithmetic is not fused.
 
 Usage: ``python -m fracture_amd.build`` (or ``build()`` from Python).
+
+``python -m fracture_amd.build --host-sanitize`` builds a second copy,
+``fracture_amd/_san/libfracture_hip.so``, whose host code carries AddressSanitizer and
+UndefinedBehaviorSanitizer (the device code is unchanged): a CPU-only check of the host-side
+argument handling and table code, loaded with ``FHIP_LIBRARY`` and clang's ASan runtime
+preloaded (``oracle/Makefile``'s ``sanitize`` target builds the oracle to match).
 """
 from __future__ import annotations
 
@@ -47,10 +53,19 @@ def _clean(text: str) -> str:
     return "\n".join(l for l in text.splitlines() if _NOISE not in l).strip()
 
 
-def _compile(src: str) -> Path:
-    obj = BUILD / (src.replace(".", "_") + ".o")
+# host code only: each option behind -Xarch_host, so no GPU code is built with a sanitizer
+HOST_SAN = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+            "-Xarch_host", "-fno-omit-frame-pointer", "-Xarch_host", "-fno-sanitize-recover=all"]
+SAN_BUILD = PKG / "_build_san"
+SAN_LIB = PKG / "_san" / "libfracture_hip.so"
+
+
+def _compile(src: str, san: bool = False) -> Path:
+    obj = (SAN_BUILD if san else BUILD) / (src.replace(".", "_") + ".o")
     lang = ["-x", "hip"] if src.endswith(".hip") else []
-    cmd = [HIPCC, *COMMON, *PER_FILE.get(src, []), *lang, "-c", str(CSRC / src), "-o", str(obj)]
+    extra = HOST_SAN if san else []
+    cmd = [HIPCC, *COMMON, *extra, *PER_FILE.get(src, []), *lang, "-c", str(CSRC / src), "-o",
+           str(obj)]
     p = subprocess.run(cmd, capture_output=True, text=True)
     msg = _clean(p.stdout + p.stderr)
     if p.returncode != 0:
@@ -60,25 +75,31 @@ def _compile(src: str) -> Path:
     return obj
 
 
-def build(jobs: int | None = None, verbose: bool = True) -> Path:
-    """Compile every HIP source for gfx950 and link libfracture_hip.so (always rebuilds)."""
-    BUILD.mkdir(exist_ok=True)
+def build(jobs: int | None = None, verbose: bool = True, host_sanitize: bool = False) -> Path:
+    """Compile every HIP source for gfx950 and link libfracture_hip.so (always rebuilds);
+    host_sanitize builds the host-sanitized copy instead (see the module docstring)."""
+    out = SAN_LIB if host_sanitize else LIB
+    (SAN_BUILD if host_sanitize else BUILD).mkdir(exist_ok=True)
+    out.parent.mkdir(exist_ok=True)
     jobs = jobs or min(len(SOURCES), max(1, min(16, os.cpu_count() or 1)))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB.with_suffix(".so.tmp")
+        objs = list(ex.map(lambda src: _compile(src, host_sanitize), SOURCES))
+    tmp = out.with_suffix(".so.tmp")
     # -z defs: a symbol that no object or linked library defines fails the link here rather
-    # than the library's load on the device host
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", "-o", str(tmp),
+    # than the library's load on the device host (the sanitized copy takes its runtime's
+    # symbols from the shared ASan runtime, preloaded when it is used)
+    link = (["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+             "-Xarch_host", "-shared-libasan"] if host_sanitize else ["-Wl,-z,defs"])
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *link, "-o", str(tmp),
            *map(str, objs), "-lrocblas", "-ldl"]
     p = subprocess.run(cmd, capture_output=True, text=True)
     if p.returncode != 0:
         raise RuntimeError("link failed:\n" + _clean(p.stdout + p.stderr))
-    os.replace(tmp, LIB)
+    os.replace(tmp, out)
     if verbose:
-        print(f"[build] {LIB.relative_to(ROOT)} ({LIB.stat().st_size // 1024} KiB)")
-    return LIB
+        print(f"[build] {out.relative_to(ROOT)} ({out.stat().st_size // 1024} KiB)")
+    return out
 
 
 if __name__ == "__main__":
-    build()
+    build(host_sanitize="--host-sanitize" in sys.argv[1:])

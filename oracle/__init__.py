@@ -11,13 +11,14 @@ Parity status of each function and the checks that pin it are listed in the head
 from __future__ import annotations
 
 import ctypes as C
+import os
 import subprocess
 from pathlib import Path
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB_PATH = HERE / "liboracle.so"
+LIB_PATH = Path(os.environ.get("FHIP_ORACLE_LIBRARY", HERE / "liboracle.so"))
 
 _lib = None
 

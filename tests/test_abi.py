@@ -117,8 +117,9 @@ def test_raw_launchers_reject_bad_arguments_on_host():
     # zero-size work is a no-op success
     assert lib.fhip_launch_add(None, None, None, 0, None) == 0
     assert lib.fhip_rows_workspace_bytes(64, 128256) == 64 * 32 * 32
-    # FP16 paged attention: head_dim 32/64/128/256, heads divisible, context bound
-    assert lib.fhip_launch_paged_attention(1, 1, 1, 1, 1, 1, 8, 2, 96, 16, 0, 1, None) == 1
+    # FP16 paged attention: head_dim 1 to 256, heads divisible, context bound
+    assert lib.fhip_launch_paged_attention(1, 1, 1, 1, 1, 1, 8, 2, 264, 16, 0, 1, None) == 1
+    assert lib.fhip_launch_paged_attention(1, 1, 1, 1, 1, 1, 8, 2, 0, 16, 0, 1, None) == 1
     assert lib.fhip_launch_paged_attention(1, 1, 1, 1, 1, 1, 6, 4, 128, 16, 0, 1, None) == 1
     assert lib.fhip_launch_paged_attention(1, 1, 1, 1, 1, -1, 8, 2, 128, 16, 0, 1, None) == 1
     assert lib.fhip_launch_paged_attention(None, None, None, None, None, 0, 8, 2, 128, 16, 0, 1,
