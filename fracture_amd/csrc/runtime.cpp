@@ -20,6 +20,7 @@
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <unordered_set>
 #include <vector>
 
 #include "fracture_hip.h"
@@ -133,7 +134,9 @@ struct StageSlot {
 
 // Device memory for small tensors. Tensors of at most kMaxBytes are carved out of large
 // chunks in power-of-two size classes (256 B to 64 KB) and recycled through per-class free
-// lists. A KV cache of one tensor per (block, layer), as the reference's cache managers
+// lists. A chunk that cannot be allocated is retried at half the size down to one tensor, and
+// a tensor the arena cannot place gets its own hipMalloc. Freed arena memory stays with the
+// backend for reuse until it is destroyed (fhip_available_memory does not count it). A KV cache of one tensor per (block, layer), as the reference's cache managers
 // allocate it (quantized_paged_kv_cache.rs:82-133), then lies in a few large mappings instead
 // of one small mapping per tensor: on MI355X the TurboQuant decode kernel over such blocks
 // measured ~7% faster (the per-tensor mappings cost address-translation misses).
@@ -167,7 +170,14 @@ struct SmallArena {
                 next_chunk[c] = n < kMaxChunk ? 2 * n : kMaxChunk;
                 void* chunk = nullptr;
                 hipError_t e = hipMalloc(&chunk, n);
+                // a chunk that does not fit: halve it down to one tensor of the class
+                while (e != hipSuccess && n > sz) {
+                    n = n / 2 > sz ? n / 2 : sz;
+                    e = hipMalloc(&chunk, n);
+                }
                 if (e != hipSuccess) return e;
+                (void)hipGetLastError();  // the failed attempts leave no error behind
+                next_chunk[c] = n < kMaxChunk ? 2 * n : kMaxChunk;
                 chunks.push_back(chunk);
                 cur[c] = (char*)chunk;
                 left[c] = n;
@@ -216,7 +226,16 @@ struct fhip_backend {
     // recorded into a graph instead of running, and only the ops whose arguments are all
     // device-resident and that never wait on the host are accepted
     std::atomic<bool> capturing{false};
-    std::unordered_map<uint64_t, hipGraphExec_t> graphs;  // under mu
+    // A graph keeps the device addresses of the tensors its launches used: the ids resolved
+    // while capturing are kept with it, and fhip_free refuses a tensor that a live graph uses
+    // (its block could be handed to another tensor, which a replay would then overwrite).
+    struct GraphRec {
+        hipGraphExec_t exec;
+        std::vector<uint64_t> ids;
+    };
+    std::unordered_map<uint64_t, GraphRec> graphs;  // under mu
+    std::unordered_set<uint64_t> capture_ids;       // under mu
+    std::unordered_map<uint64_t, int> graph_refs;   // tensor id -> live graphs using it (mu)
     uint64_t next_graph = 1;
     // launch lock: staging ring and workspace are per backend
     std::mutex launch_mu;
@@ -259,6 +278,12 @@ struct fhip_backend {
     fhip_tq_plan* plan_for(uint64_t rot_id, const void* rot, uint64_t cent_id, const void* cent,
                            int levels, int bits, int head_dim) {
         if (head_dim != 128) return nullptr;
+        {
+            // no plan from a tensor of a registered pool: the pool's writers (append_kv) do
+            // not check for plans
+            std::lock_guard<std::mutex> g(mu);
+            if (pooled.count(rot_id) || pooled.count(cent_id)) return nullptr;
+        }
         for (const PlanEntry& e : plans)
             if (e.rot == rot_id && e.cent == cent_id && e.bits == bits && e.levels == levels)
                 return e.plan;
@@ -269,10 +294,17 @@ struct fhip_backend {
         plans.push_back(PlanEntry{rot_id, cent_id, bits, levels, p});
         return p;
     }
-    void drop_plans(uint64_t id) {
+    // Called for every tensor an op writes (and for a freed one): a plan built from it is
+    // stale and is destroyed. Destroying one waits for its kernels and frees device memory,
+    // which a graph capture cannot do, so such a write is refused while capturing.
+    int drop_plans(uint64_t id) {
         std::lock_guard<std::mutex> g(plan_mu);
         for (size_t i = 0; i < plans.size();) {
             if (plans[i].rot == id || plans[i].cent == id) {
+                if (capturing)
+                    return fail(FHIP_ERR_BACKEND, "tensor id %llu holds the tables of a "
+                                "TurboQuant plan: it cannot be written during graph capture",
+                                (unsigned long long)id);
                 fhip_tq_plan_destroy(plans[i].plan);  // waits for kernels still using it
                 plans[i] = plans.back();
                 plans.pop_back();
@@ -280,6 +312,7 @@ struct fhip_backend {
                 ++i;
             }
         }
+        return FHIP_OK;
     }
 
     int get_ptr(uint64_t id, void** out) {
@@ -288,6 +321,7 @@ struct fhip_backend {
         if (it == tensors.end())
             return fail(FHIP_ERR_TENSOR_NOT_FOUND, "tensor id %llu",
                         (unsigned long long)id);
+        if (capturing) capture_ids.insert(id);
         *out = it->second;
         return FHIP_OK;
     }
@@ -407,6 +441,13 @@ namespace {
         if (r_ != FHIP_OK) return r_;            \
     }
 
+// An op's output tensor: a TurboQuant plan built from it is dropped (see drop_plans).
+#define WRITES(b, t)                              \
+    {                                             \
+        int w_ = (b)->drop_plans((t)->id);        \
+        if (w_ != FHIP_OK) return w_;             \
+    }
+
 int set_device(fhip_backend* b) {
     HIP_TRY(hipSetDevice(b->device));
     return FHIP_OK;
@@ -447,7 +488,7 @@ void fhip_backend_destroy(fhip_backend* b) {
         b->capturing = false;
     }
     (void)hipStreamSynchronize(b->stream);
-    for (auto& kv : b->graphs) (void)hipGraphExecDestroy(kv.second);
+    for (auto& kv : b->graphs) (void)hipGraphExecDestroy(kv.second.exec);
     for (auto& kv : b->tensors)
         if (!b->arena.owns(kv.second)) (void)hipFree(kv.second);
     b->arena.destroy();
@@ -531,10 +572,11 @@ int fhip_alloc(fhip_backend* b, const uint64_t* shape, int ndim, int dtype, fhip
     std::lock_guard<std::mutex> g(b->mu);
     // small tensors (a zero-byte one included, so that its id still resolves) come from the
     // arena
-    if (bytes <= SmallArena::kMaxBytes)
-        HIP_TRY(b->arena.alloc(bytes, &p));
-    else
-        HIP_TRY(hipMalloc(&p, bytes));
+    if (bytes <= SmallArena::kMaxBytes && b->arena.alloc(bytes, &p) == hipSuccess) {
+    } else {
+        (void)hipGetLastError();
+        HIP_TRY(hipMalloc(&p, bytes ? bytes : 1));
+    }
     t.id = b->next_id++;
     b->tensors[t.id] = p;
     *out = t;
@@ -556,11 +598,14 @@ int fhip_free(fhip_backend* b, const fhip_tensor* t) {
         if (b->pooled.count(t->id))
             return fail(FHIP_ERR_BACKEND, "tensor id %llu is in a registered page pool",
                         (unsigned long long)t->id);
+        if (b->graph_refs.count(t->id))
+            return fail(FHIP_ERR_BACKEND, "tensor id %llu is used by a captured graph "
+                        "(destroy the graph first)", (unsigned long long)t->id);
         p = it->second;
         b->tensors.erase(it);
     }
     set_device(b);
-    b->drop_plans(t->id);
+    (void)b->drop_plans(t->id);  // not capturing (NO_CAPTURE above)
     // Kernels on the backend's stream may still read the buffer.
     HIP_TRY(hipStreamSynchronize(b->stream));
     {
@@ -582,7 +627,7 @@ int fhip_copy_to_device(fhip_backend* b, const fhip_tensor* dst, const void* src
                     src_len, (unsigned long long)size);
     if (size == 0) return FHIP_OK;
     set_device(b);
-    b->drop_plans(dst->id);
+    WRITES(b, dst);
     HIP_TRY(hipMemcpyAsync(p, src, size, hipMemcpyHostToDevice, b->stream));
     HIP_TRY(hipStreamSynchronize(b->stream));
     return FHIP_OK;
@@ -614,6 +659,7 @@ int fhip_rmsnorm(fhip_backend* b, const fhip_tensor* input, const fhip_tensor* w
     GET_PTR(b, input, pin);
     GET_PTR(b, weight, pw);
     GET_PTR(b, out, pout);
+    WRITES(b, out);
     if (input->ndim < 1)
         return fail(FHIP_ERR_INVALID_SHAPE, "rmsnorm input must be 2-D");
     const uint64_t cols = input->shape[input->ndim - 1];
@@ -645,6 +691,7 @@ int fhip_matmul(fhip_backend* b, const fhip_tensor* a, const fhip_tensor* bm,
     GET_PTR(b, a, pa);
     GET_PTR(b, bm, pb);
     GET_PTR(b, out, pc);
+    WRITES(b, out);
     if (a->ndim != 2 || bm->ndim != 2)
         return fail(FHIP_ERR_INVALID_SHAPE, "matmul: A %s and B %s must be 2-D",
                     shape_str(a).c_str(), shape_str(bm).c_str());
@@ -675,9 +722,11 @@ int fhip_add_rmsnorm(fhip_backend* b, const fhip_tensor* residual, const fhip_te
     CHECK_T(weight);
     CHECK_T(normed_out);
     GET_PTR(b, residual, ph);
+    WRITES(b, residual);
     GET_PTR(b, delta, pd);
     GET_PTR(b, weight, pw);
     GET_PTR(b, normed_out, po);
+    WRITES(b, normed_out);
     if (residual->ndim < 1)
         return fail(FHIP_ERR_INVALID_SHAPE, "add_rmsnorm needs 2-D input");
     const uint64_t cols = residual->shape[residual->ndim - 1];
@@ -711,7 +760,9 @@ int rope_common(fhip_backend* b, const fhip_tensor* q, const fhip_tensor* k,
     CHECK_T(q);
     CHECK_T(k);
     GET_PTR(b, q, pq);
+    WRITES(b, q);
     GET_PTR(b, k, pk);
+    WRITES(b, k);
     if (!b->rope_freq)
         return fail(FHIP_ERR_BACKEND,
                     "RoPE frequency table not initialized. Call precompute_rope_freqs() first.");
@@ -754,6 +805,7 @@ int embedding_common(fhip_backend* b, const uint32_t* host_ids, const void* dev_
     CHECK_T(out);
     GET_PTR(b, table, pt);
     GET_PTR(b, out, po);
+    WRITES(b, out);
     if (table->ndim != 2 || (dtype_size(table->dtype) != 2 && dtype_size(table->dtype) != 4))
         return fail(FHIP_ERR_INVALID_SHAPE, "embedding table %s",
                     shape_str(table).c_str());
@@ -839,6 +891,7 @@ int fhip_silu_mul(fhip_backend* b, const fhip_tensor* gate, const fhip_tensor* u
     GET_PTR(b, gate, pg);
     GET_PTR(b, up, pu);
     GET_PTR(b, out, po);
+    WRITES(b, out);
     if (numel(out) < numel(gate) || up->dtype != gate->dtype || out->dtype != gate->dtype)
         return fail(FHIP_ERR_INVALID_SHAPE, "silu_mul: out %s too small",
                     shape_str(out).c_str());
@@ -858,6 +911,7 @@ int fhip_add(fhip_backend* b, const fhip_tensor* a, const fhip_tensor* bt, const
     GET_PTR(b, a, pa);
     GET_PTR(b, bt, pb);
     GET_PTR(b, out, po);
+    WRITES(b, out);
     if (numel(out) < numel(a) || bt->dtype != a->dtype || out->dtype != a->dtype)
         return fail(FHIP_ERR_INVALID_SHAPE, "add: out %s too small",
                     shape_str(out).c_str());
@@ -890,6 +944,10 @@ int fhip_graph_begin(fhip_backend* b) {
     set_device(b);
     std::lock_guard<std::mutex> g(b->launch_mu);
     if (b->capturing) return fail(FHIP_ERR_BACKEND, "graph capture already in progress");
+    {
+        std::lock_guard<std::mutex> g2(b->mu);
+        b->capture_ids.clear();
+    }
     HIP_TRY(hipStreamBeginCapture(b->stream, hipStreamCaptureModeThreadLocal));
     b->capturing = true;
     return FHIP_OK;
@@ -901,10 +959,16 @@ int fhip_graph_end(fhip_backend* b, uint64_t* graph_out) {
     *graph_out = 0;
     set_device(b);
     hipGraph_t graph = nullptr;
+    std::vector<uint64_t> ids;
     {
         std::lock_guard<std::mutex> g(b->launch_mu);
         if (!b->capturing) return fail(FHIP_ERR_BACKEND, "no graph capture in progress");
         b->capturing = false;
+        {
+            std::lock_guard<std::mutex> g2(b->mu);
+            ids.assign(b->capture_ids.begin(), b->capture_ids.end());
+            b->capture_ids.clear();
+        }
         hipError_t e = hipStreamEndCapture(b->stream, &graph);
         if (e != hipSuccess) {
             if (graph) (void)hipGraphDestroy(graph);
@@ -917,7 +981,8 @@ int fhip_graph_end(fhip_backend* b, uint64_t* graph_out) {
     if (e != hipSuccess) return hip_fail(e);
     std::lock_guard<std::mutex> g(b->mu);
     const uint64_t id = b->next_graph++;
-    b->graphs[id] = exec;
+    for (uint64_t t : ids) ++b->graph_refs[t];
+    b->graphs[id] = fhip_backend::GraphRec{exec, std::move(ids)};
     *graph_out = id;
     return FHIP_OK;
 }
@@ -931,7 +996,7 @@ int fhip_graph_launch(fhip_backend* b, uint64_t graph) {
         auto it = b->graphs.find(graph);
         if (it == b->graphs.end())
             return fail(FHIP_ERR_BACKEND, "graph %llu not found", (unsigned long long)graph);
-        exec = it->second;
+        exec = it->second.exec;
     }
     set_device(b);
     std::lock_guard<std::mutex> g(b->launch_mu);
@@ -948,7 +1013,9 @@ int fhip_graph_destroy(fhip_backend* b, uint64_t graph) {
         auto it = b->graphs.find(graph);
         if (it == b->graphs.end())
             return fail(FHIP_ERR_BACKEND, "graph %llu not found", (unsigned long long)graph);
-        exec = it->second;
+        exec = it->second.exec;
+        for (uint64_t t : it->second.ids)
+            if (--b->graph_refs[t] == 0) b->graph_refs.erase(t);
         b->graphs.erase(it);
     }
     set_device(b);
@@ -987,7 +1054,7 @@ int fhip_copy_rows(fhip_backend* b, const fhip_tensor* src, const fhip_tensor* d
     const uint64_t row = row_elems * dtype_size(src->dtype);
     if (count == 0 || row == 0) return FHIP_OK;
     set_device(b);
-    b->drop_plans(dst->id);
+    WRITES(b, dst);
     HIP_TRY(hipMemcpyAsync((char*)pdst + dst_offset * row, (const char*)ps + src_offset * row,
                            count * row, hipMemcpyDeviceToDevice, b->stream));
     return FHIP_OK;
@@ -1105,7 +1172,9 @@ int fhip_turboquant_compress(fhip_backend* b, const fhip_tensor* input, const fh
     GET_PTR(b, rotation, prot);
     GET_PTR(b, centroids, pc);
     GET_PTR(b, packed_out, pp);
+    WRITES(b, packed_out);
     GET_PTR(b, norms_out, pn);
+    WRITES(b, norms_out);
     if (input->ndim != 3 || input->dtype != FHIP_FP16)
         return fail(FHIP_ERR_INVALID_SHAPE,
                     "turboquant_compress input must be [N, kv_heads, head_dim] FP16, got %s %s",
@@ -1144,6 +1213,7 @@ int fhip_tq_quantize_pack(fhip_backend* b, const fhip_tensor* y, const fhip_tens
     GET_PTR(b, y, py);
     GET_PTR(b, centroids, pc);
     GET_PTR(b, packed_out, pp);
+    WRITES(b, packed_out);
     if (y->ndim < 1 || y->dtype != FHIP_FP32)
         return fail(FHIP_ERR_INVALID_SHAPE, "tq_quantize_pack y %s",
                     shape_str(y).c_str());
@@ -1178,6 +1248,7 @@ int fhip_tq_dequantize(fhip_backend* b, const fhip_tensor* packed, const fhip_te
     GET_PTR(b, rotation, prot);
     GET_PTR(b, centroids, pc);
     GET_PTR(b, out, po);
+    WRITES(b, out);
     if (out->ndim != 3 || out->dtype != FHIP_FP16)
         return fail(FHIP_ERR_INVALID_SHAPE, "dequantize out must be [N, kv_heads, head_dim] FP16");
     const uint64_t N = out->shape[0], H = out->shape[1], hd = out->shape[2];
@@ -1208,6 +1279,7 @@ int fhip_softmax_rows(fhip_backend* b, const fhip_tensor* logits, float temperat
     CHECK_T(probs);
     GET_PTR(b, logits, pl);
     GET_PTR(b, probs, pp);
+    WRITES(b, probs);
     if (logits->ndim < 1 || logits->dtype != FHIP_FP32 || probs->dtype != FHIP_FP32 ||
         numel(probs) != numel(logits))
         return fail(FHIP_ERR_INVALID_SHAPE, "softmax logits %s probs %s",
@@ -1289,6 +1361,7 @@ int fhip_attention_paged_tq(fhip_backend* b, const fhip_tensor* q, const int32_t
     CHECK_T(out);
     GET_PTR(b, q, pq);
     GET_PTR(b, out, po);
+    WRITES(b, out);
     GET_PTR(b, k_rotation, pkr);
     GET_PTR(b, v_rotation, pvr);
     GET_PTR(b, k_centroids, pkc);
@@ -1401,17 +1474,22 @@ int fhip_page_pool_create(fhip_backend* b, const fhip_tensor* blocks, size_t nli
         return hip_fail(e);
     }
     pp.dev = (const void**)dev;
-    std::lock_guard<std::mutex> g(b->mu);
-    for (uint64_t tid : pp.ids) {
-        if (!b->tensors.count(tid)) {  // freed while the pool was being built
-            (void)hipFree(dev);
-            return fail(FHIP_ERR_TENSOR_NOT_FOUND, "tensor id %llu", (unsigned long long)tid);
+    const std::vector<uint64_t> ids = pp.ids;
+    {
+        std::lock_guard<std::mutex> g(b->mu);
+        for (uint64_t tid : pp.ids) {
+            if (!b->tensors.count(tid)) {  // freed while the pool was being built
+                (void)hipFree(dev);
+                return fail(FHIP_ERR_TENSOR_NOT_FOUND, "tensor id %llu", (unsigned long long)tid);
+            }
         }
+        for (uint64_t tid : pp.ids) ++b->pooled[tid];
+        const uint64_t id = b->next_pool++;
+        b->pools.emplace(id, std::move(pp));
+        *pool_out = id;
     }
-    for (uint64_t tid : pp.ids) ++b->pooled[tid];
-    const uint64_t id = b->next_pool++;
-    b->pools.emplace(id, std::move(pp));
-    *pool_out = id;
+    // the pool's writers do not look for plans: none may be built from its tensors
+    for (uint64_t tid : ids) (void)b->drop_plans(tid);
     return FHIP_OK;
 }
 
@@ -1479,6 +1557,7 @@ int fhip_attention_paged_pool(fhip_backend* b, const fhip_tensor* q, const int32
     CHECK_T(out);
     GET_PTR(b, q, pq);
     GET_PTR(b, out, po);
+    WRITES(b, out);
     if (q->ndim != 3 || q->dtype != FHIP_FP16 || out->dtype != FHIP_FP16 ||
         numel(out) != numel(q))
         return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged q %s out %s",
@@ -1543,6 +1622,7 @@ int fhip_attention_paged_tq_pool(fhip_backend* b, const fhip_tensor* q,
     CHECK_T(out);
     GET_PTR(b, q, pq);
     GET_PTR(b, out, po);
+    WRITES(b, out);
     GET_PTR(b, k_rotation, pkr);
     GET_PTR(b, v_rotation, pvr);
     GET_PTR(b, k_centroids, pkc);
@@ -1730,6 +1810,7 @@ int fhip_attention_paged_tq_batched(fhip_backend* b, const fhip_tensor* q,
     CHECK_T(out);
     GET_PTR(b, q, pq);
     GET_PTR(b, out, po);
+    WRITES(b, out);
     GET_PTR(b, k_rotation, pkr);
     GET_PTR(b, v_rotation, pvr);
     GET_PTR(b, k_centroids, pkc);
@@ -1829,6 +1910,7 @@ int fhip_attention_paged(fhip_backend* b, const fhip_tensor* q, const int32_t* b
     CHECK_T(out);
     GET_PTR(b, q, pq);
     GET_PTR(b, out, po);
+    WRITES(b, out);
     if (q->ndim != 3 || q->dtype != FHIP_FP16 || out->dtype != FHIP_FP16 ||
         numel(out) != numel(q))
         return fail(FHIP_ERR_INVALID_SHAPE, "attention_paged q %s out %s",

@@ -10,6 +10,7 @@ import pytest
 import oracle
 from conftest import assert_close
 from fracture_amd import BackendError, DType, HipBackend
+from fracture_amd import turboquant as tq
 
 pytestmark = pytest.mark.gpu
 
@@ -234,3 +235,57 @@ def test_contiguous_attention_not_supported(backend):
     with pytest.raises(BackendError, match="not supported"):
         backend.attention(q, q, q, 2, 0, q)
     backend.free(q)
+
+
+def test_free_refused_while_a_graph_uses_the_tensor():
+    """A graph keeps the device addresses of the tensors it used: freeing one of them (whose
+    block the next allocation could reuse) is refused until the graph is destroyed."""
+    with HipBackend(0) as b:
+        t = _tensors(b)
+        _load(b, t, _inputs(2))
+        g = b.capture(lambda: b.silu_mul(t["gate"], t["up"], t["mid"]))
+        for name in ("gate", "up", "mid"):
+            with pytest.raises(BackendError, match="captured graph"):
+                b.free(t[name])
+        b.free(t["x"])  # not used by the graph
+        b.graph_launch(g)
+        b.synchronize()
+        b.graph_destroy(g)
+        for name in ("gate", "up", "mid"):
+            b.free(t[name])
+
+
+def test_writing_plan_tables_refused_during_capture():
+    """A TurboQuant plan cached from a rotation cannot be dropped under graph capture (that
+    frees device memory), so an op writing that rotation is refused while capturing and
+    records nothing; outside a capture the same write drops the plan."""
+    rng = np.random.default_rng(3)
+    with HipBackend(0) as b:
+        t = _tensors(b)
+        _load(b, t, _inputs(4))
+        rot = b.upload(tq.rotation_matrix(128, 1))
+        cent = b.upload(tq.codebook(128, 4)[0])
+        x = b.upload(rng.standard_normal((4, 8, 128)).astype(np.float16))
+        packed = b.alloc([4, 8 * 64], DType.INT8)
+        norms = b.alloc([4, 8], DType.FP16)
+        b.turboquant_compress(x, rot, cent, 4, packed, norms)  # builds and caches the plan
+        before = b.download(packed).copy()
+        zero = b.upload(np.zeros((128, 128), np.float32))
+        b.graph_begin()
+        try:
+            with pytest.raises(BackendError, match="TurboQuant plan"):
+                b.add(zero, zero, rot)
+            b.silu_mul(t["gate"], t["up"], t["mid"])
+        finally:
+            g = b.graph_end()
+        b.graph_launch(g)
+        b.synchronize()
+        b.graph_destroy(g)
+        b.turboquant_compress(x, rot, cent, 4, packed, norms)
+        assert np.array_equal(b.download(packed), before)  # rot was left alone
+        b.add(zero, zero, rot)  # rot := 0 outside a capture: allowed, the plan is dropped
+        b.turboquant_compress(x, rot, cent, 4, packed, norms)
+        # every rotated coordinate is 0 now: each code is the one nearest 0
+        c = tq.codebook(128, 4)[0]
+        code0 = int(np.argmin(np.abs(c)))
+        assert (b.download(packed) == (code0 << 4 | code0)).all()

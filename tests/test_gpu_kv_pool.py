@@ -45,7 +45,10 @@ def kernel_y(x16, rot):
     return y.cpu().numpy(), yn.cpu().numpy()
 
 
-def test_planned_trait_compress_and_rebuild(backend):
+@pytest.mark.parametrize("writer", ["copy_to_device", "add", "copy_rows"])
+def test_planned_trait_compress_and_rebuild(backend, writer):
+    """The backend's cached plan for a (rotation, codebook) pair is dropped by any op that
+    writes either tensor: the next call rebuilds it from the new contents."""
     rng = np.random.default_rng(11)
     N, H, hd, bits = 70, 8, 128, 4
     x = (rng.standard_normal((N, H, hd)) * 3).astype(np.float16)
@@ -57,8 +60,19 @@ def test_planned_trait_compress_and_rebuild(backend):
     norms = backend.alloc([N, H], DType.FP16)
     out = backend.alloc([N, H, hd], DType.FP16)
     for rot in (r1, r2):
-        if rot is r2:
-            backend.copy_to_device(tr, rot)  # same tensor id, new contents: the plan is rebuilt
+        if rot is r2:  # same tensor id, new contents: the plan is rebuilt
+            if writer == "copy_to_device":
+                backend.copy_to_device(tr, rot)
+            else:
+                src = backend.upload(rot)
+                if writer == "add":
+                    zero = backend.upload(np.zeros_like(rot))
+                    backend.add(src, zero, tr)  # exact in fp32
+                    backend.free(zero)
+                else:
+                    backend.copy_rows(src, tr, 0, 0, hd)
+                backend.synchronize()
+                backend.free(src)
         for _ in range(2):  # second call reuses the cached plan
             backend.turboquant_compress(tx, tr, tc, bits, packed, norms)
             y, yn = kernel_y(x, rot)
