@@ -24,6 +24,9 @@ Other workloads (parity-tested configurations, printed as their own JSON lines):
   --workload attention    decode attention over a K4/V4 page pool, B=64, 32/8 heads, ctx U[1024,32768],
                           and causal prefill of one sequence (2048 over 2048, 512 over 8192 positions)
   --workload paged        the same decode attention and prefill over FP16 pages (attention_paged.cu)
+  --workload floors       the floors the decode-chain kernels and the [64,128256] reductions are
+                          compared with: an empty kernel, and probes that move each kernel's bytes
+                          and compute nothing (also part of the default and prefill lines)
 
 HBM traffic (the roofline's "traffic" field, from profiles/traffic.json):
   rocprofv3 --pmc FETCH_SIZE -d <F> -o pmc -- python3 bench.py --workload pmc
@@ -55,7 +58,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "prefill", "tq", "attention", "paged", "all", "pmc"])
+                    choices=["decode", "prefill", "tq", "attention", "paged", "floors", "all",
+                             "pmc"])
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn two rocprofv3 --pmc runs of --workload pmc into "
                          "profiles/traffic.json")
@@ -357,6 +361,97 @@ def cpu_decode_baseline(seconds: float, threads: int = 1):
     return med * 1e6, n
 
 
+# What each measured kernel moves (inputs read, outputs written, bytes of each), for the probe
+# that stands for it: the same traffic with no arithmetic (fhip_probe_stream).
+FLOOR_TRAFFIC = {
+    "embedding": (1, 1, 64 * 4096 * 2),                 # 64 table rows in, 64 rows out
+    "rope": (1, 1, 64 * (32 + 8) * 128 * 2),            # Q and K in place
+    "silu_mul": (2, 1, 64 * 14336 * 2),
+    "add_rmsnorm": (2, 2, 64 * 4096 * 2),               # h, delta in; h, normed out
+    "softmax_64x128256": (1, 1, 64 * 128256 * 4),       # one read, one write
+    "argmax_64x128256": (1, 0, 64 * 128256 * 4),        # one read
+}
+FLOOR_GRIDS = (64, 128, 256, 512, 1024, 2048, 4096, 8192)
+
+
+def graph_seq_time_us(torch, fns, replays: int = 20) -> float:
+    """Average launch duration of the calls `fns` captured in order in one HIP graph."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for f in fns[:3]:
+            f()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for f in fns:
+            f()
+    g.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(replays):
+        g.replay()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) * 1e3 / (replays * len(fns))
+
+
+def run_floors(torch, K, dev):
+    """The floors each kernel is compared with, timed the way the kernels are (a HIP graph of
+    50 back-to-back launches, replayed): an empty kernel, and for each kernel a probe that
+    moves the same bytes (inputs read, outputs written) and computes nothing, at the best of
+    a sweep of grid sizes. `cold` variants cycle over buffers larger in total than the MALL
+    (256 MB), so every launch reads from HBM."""
+    timer = Timer(torch)
+    out = {"empty_kernel_us": {f"grid_{g}": round(timer.graph_time_us(lambda g=g: K.probe_empty(g)), 3)
+                               for g in (1, 64, 256, 1024)}}
+    sink = torch.empty(256, dtype=torch.int32, device=dev)
+    big = 64 * 128256 * 4
+    pool = [torch.empty(big // 4, dtype=torch.int32, device=dev).fill_(i) for i in range(5)]
+
+    def probe(nin, nout, nb, bufs=pool):
+        best = None
+        for g in FLOOR_GRIDS:
+            if g > max(1, nb // 16 // 256) * 2:
+                break
+            us = timer.graph_time_us(lambda g=g: K.probe_stream(bufs[:nin], bufs[nin:nin + nout],
+                                                                 nb, g, sink))
+            if best is None or us < best[0]:
+                best = (us, g)
+        return {"us": round(best[0], 3), "grid": best[1], "bytes": nb * (nin + nout),
+                "GB/s": round(gbs(nb * (nin + nout), best[0]), 1)}
+
+    for name, (nin, nout, nb) in FLOOR_TRAFFIC.items():
+        out[name] = probe(nin, nout, nb)
+    for mib in (1, 2, 6):
+        out[f"copy_{mib}MiB"] = probe(1, 1, mib << 20)
+    # cold: 12 sets of the 32.8 MB logits-sized buffers (394 MB), one per launch
+    sets = [torch.empty(big // 4, dtype=torch.int32, device=dev).fill_(i) for i in range(12)]
+    grid = out["argmax_64x128256"]["grid"]
+    us = graph_seq_time_us(torch, [lambda b=b: K.probe_stream([b], [], big, grid, sink)
+                                   for b in sets * 4])
+    out["argmax_64x128256_cold"] = {"us": round(us, 3), "grid": grid, "bytes": big,
+                                    "GB/s": round(gbs(big, us), 1)}
+    outs = [torch.empty_like(sets[0]) for _ in range(12)]
+    grid = out["softmax_64x128256"]["grid"]
+    us = graph_seq_time_us(torch, [lambda i=i: K.probe_stream([sets[i]], [outs[(i + 5) % 12]],
+                                                              big, grid, sink)
+                                   for i in range(12)] * 4)
+    out["softmax_64x128256_cold"] = {"us": round(us, 3), "grid": grid, "bytes": 2 * big,
+                                     "GB/s": round(gbs(2 * big, us), 1)}
+    del sets, outs, pool
+    torch.cuda.synchronize()
+    return out
+
+
+def with_floor(entry, floor):
+    """entry (a kernel's us) beside the floor of its traffic: floor_us / us."""
+    entry["floor_us"] = floor["us"]
+    entry["frac_of_floor"] = round(floor["us"] / entry["us"], 3)
+    return entry
+
+
 def run_decode(args, torch, K, dev):
     x = decode_inputs(torch, dev)
     ops = decode_ops(K, x)
@@ -441,6 +536,9 @@ def run_decode(args, torch, K, dev):
                      "traffic": traffic_of({"embedding": "decode_embedding", "rope": "decode_rope",
                                             "silu_mul": "silu_mul_64x14336",
                                             "add_rmsnorm": "decode_add_rmsnorm"}[name])}
+    floors = run_floors(torch, K, dev)
+    for name, e in per.items():
+        with_floor(e, floors[name])
     # the roofline kernel: the one that takes the most time per step (launches x duration)
     for name, e in per.items():
         e["launches_per_step"] = DECODE_COUNTS[name]
@@ -454,9 +552,11 @@ def run_decode(args, torch, K, dev):
             "traffic": traffic_of(traffic_key), "algorithmic_bytes": nbytes[dom],
             "avg_launch_us": per[dom]["us"],
             "launches_per_step": DECODE_COUNTS[dom],
+            "floor_us": per[dom]["floor_us"], "frac_of_floor": per[dom]["frac_of_floor"],
             "note": "average launch duration from a HIP graph of 50 back-to-back launches "
-                    "(HIP events on the launch stream); an empty kernel costs ~1.7 us per "
-                    "launch the same way"}
+                    "(HIP events on the launch stream); floor_us is a kernel that moves the "
+                    "same bytes and computes nothing, timed the same way (floors.add_rmsnorm); "
+                    "an empty kernel costs floors.empty_kernel_us per launch"}
 
     result = {
         "metric": METRIC,
@@ -483,6 +583,7 @@ def run_decode(args, torch, K, dev):
             "input_sets": 40},
         "kernels": per,
         "roofline": roof,
+        "floors": floors,
     }
     if not args.eager:
         rt_us = runtime_decode_graph(per_graph, max(1, args.steps // per_graph))
@@ -562,6 +663,10 @@ def run_prefill(args, torch, K, dev):
         out[name] = {"us": round(us, 2), "GB/s": round(gbs(nb, us), 1),
                      "frac_of_peak": round(gbs(nb, us) / PEAK_HBM_GBS, 4), "bytes": nb,
                      "traffic": traffic_of(name)}
+    floors = run_floors(torch, K, dev)
+    for name in ("softmax_64x128256", "argmax_64x128256"):
+        with_floor(out[name], floors[name])
+        out[name]["floor_cold_us"] = floors[name + "_cold"]["us"]
     return {"workload": "prefill-shaped reductions (fp16 in, fp32 accumulate)", "kernels": out}
 
 
@@ -1005,7 +1110,8 @@ def run_configs(args, torch, K, dev):
     """Compact results of the other configurations for the default JSON line."""
     out = {}
     pre = run_prefill(args, torch, K, dev)["kernels"]
-    out["c3_prefill_reductions"] = {k: {f: v[f] for f in ("us", "GB/s", "frac_of_peak")}
+    out["c3_prefill_reductions"] = {k: {f: v[f] for f in ("us", "GB/s", "frac_of_peak",
+                                                          "floor_us", "frac_of_floor") if f in v}
                                     for k, v in pre.items()}
     tqr = run_tq(args, torch, K, dev)["kernels"]
     out["c4_turboquant_kv_32768x8x128"] = {
@@ -1363,6 +1469,9 @@ def main():
         print(json.dumps(run_attention(args, torch, K, dev)), flush=True)
     if wl in ("paged", "all"):
         print(json.dumps(run_paged(args, torch, K, dev)), flush=True)
+    if wl in ("floors", "all"):
+        print(json.dumps({"workload": "floors: empty kernel and traffic-only probes",
+                          "floors": run_floors(torch, K, dev)}), flush=True)
     if wl == "pmc":
         print(json.dumps(run_pmc(torch, K, dev)), flush=True)
 

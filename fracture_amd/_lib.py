@@ -55,6 +55,9 @@ SIGNATURES = {
     "fhip_launch_attention_paged_tq_noalloc": (I, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I,
                                                    I, I, I, I, I, I, P]),
     "fhip_launch_rmsnorm_ex": (I, [P, P, P, F, I, I, I, P]),
+    # measurement probes
+    "fhip_probe_empty": (I, [I, P]),
+    "fhip_probe_stream": (I, [P, I, P, I, I64, P, I, P]),
     "fhip_launch_add_ex": (I, [P, P, P, I64, I, P]),
     "fhip_launch_silu_mul_ex": (I, [P, P, P, I64, I, P]),
     "fhip_launch_rope_ex": (I, [P, P, P, P, I, I, I, I, I, P]),

@@ -43,7 +43,7 @@ PER_FILE = {
     "tq_host.cpp": ["-ffp-contract=off"],
 }
 SOURCES = ["elementwise.hip", "reduce.hip", "turboquant.hip", "attention_tq.hip",
-           "attention_paged.hip", "matmul.cpp",
+           "attention_paged.hip", "probes.hip", "matmul.cpp",
            "tq_host.cpp", "runtime.cpp"]
 
 _NOISE = "'-packed-fp32-ops' is not a recognized feature for this target"

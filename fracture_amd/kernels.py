@@ -462,3 +462,24 @@ def matmul(c: torch.Tensor, a: torch.Tensor, b: torch.Tensor) -> None:
           tuple(c.shape) == (a.shape[0], b.shape[0]), "shapes")
     _ok(_L().fhip_launch_matmul(_p(c), _p(a), _p(b), a.shape[0], b.shape[0], a.shape[1],
                                 _stream()), "matmul")
+
+
+# ---------------------------------------------------------------------------------------
+# Measurement probes (floors for the benchmark; no counterpart in the reference)
+# ---------------------------------------------------------------------------------------
+def probe_empty(grid: int) -> None:
+    """An empty kernel of `grid` workgroups on torch's current stream."""
+    _ok(_L().fhip_probe_empty(grid, _stream()), "probe_empty")
+
+
+def probe_stream(inputs, outputs, nbytes: int, grid: int, sink: torch.Tensor | None = None) -> None:
+    """Read `nbytes` of each input tensor and write their XOR to each output (device
+    tensors of at least nbytes each): the memory traffic of a kernel, nothing else."""
+    for t in list(inputs) + list(outputs):
+        _need(t.is_cuda and t.numel() * t.element_size() >= nbytes, "probe buffer")
+    ins = (C.c_void_p * 3)(*[_p(t) for t in inputs])
+    outs = (C.c_void_p * 2)(*[_p(t) for t in outputs])
+    _need(bool(outputs) or sink is not None, "a read-only probe needs a sink")
+    _ok(_L().fhip_probe_stream(ins, len(inputs), outs, len(outputs), nbytes,
+                               _p(sink) if sink is not None else None, grid, _stream()),
+        "probe_stream")

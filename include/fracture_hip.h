@@ -572,6 +572,22 @@ int fhip_tq_quantize_pack(fhip_backend* b, const fhip_tensor* y, const fhip_tens
                           uint8_t bits, const fhip_tensor* packed_out);
 
 /* =====================================================================================
+ * Measurement probes (no counterpart in the reference): the floors a launch reaches on this
+ * device, timed the same way as the kernels above, for the benchmark's floor fractions.
+ * ===================================================================================== */
+
+/* An empty kernel of `grid` workgroups of 256 lanes. */
+int fhip_probe_empty(int grid, fhip_stream_t stream);
+/* A kernel that only moves memory: it reads bytes_each bytes of each of num_inputs (0-3)
+ * device buffers and writes the XOR of them to each of num_outputs (0-2) buffers, in 16-byte
+ * vectors over `grid` workgroups of 256 lanes; with no output it reads only (`sink`, 1 KiB of
+ * device memory, is then written only if the XOR hits an impossible value). bytes_each is a
+ * positive multiple of 16. */
+int fhip_probe_stream(const void* const* inputs, int num_inputs, void* const* outputs,
+                      int num_outputs, int64_t bytes_each, void* sink, int grid,
+                      fhip_stream_t stream);
+
+/* =====================================================================================
  * 3. Host-only helpers (no GPU)
  * ===================================================================================== */
 

@@ -132,6 +132,12 @@ def test_raw_launchers_reject_bad_arguments_on_host():
     assert lib.fhip_attention_paged_workspace_bytes(0, 32, 128, 2048) == 0
     # contiguous-cache attention (ffi.rs:172-184) is a stub: hipErrorNotSupported (801)
     assert lib.fhip_launch_attention(1, 1, 1, 1, 1, 8, 2, 128, 16, 0, None) == 801
+    # measurement probes: arguments are checked before any launch
+    assert lib.fhip_probe_empty(0, None) == 1
+    assert lib.fhip_probe_stream(None, 0, None, 0, 16, None, 1, None) == 1  # moves nothing
+    assert lib.fhip_probe_stream(None, 1, None, 0, 16, None, 1, None) == 1  # null input list
+    assert lib.fhip_probe_stream(None, 4, None, 0, 16, None, 1, None) == 1  # > 3 inputs
+    assert lib.fhip_probe_stream(None, 0, None, 1, 24, None, 1, None) == 1  # not 16-byte units
     # matmul sizes
     assert lib.fhip_launch_matmul(None, None, None, -1, 4, 4, None) == 1
     assert lib.fhip_launch_matmul(None, None, None, 0, 4, 4, None) == 0
