@@ -15,7 +15,12 @@
 //    an exact float threshold t_q, found by bisection over the float ordering.
 //  * A bucket map j(y) = clamp(int(fma(y, s, o))) is monotone, so thresholds in lower
 //    buckets are < y and in higher buckets > y; with at most one threshold per bucket,
-//    code = base[j] + (y > t[j]).
+//    code = base[j] + (y > t[j]). J = 2L buckets span the thresholds (at least 16): for the
+//    Lloyd-Max codebooks of 2-8 bits no bucket then holds two. With at most 256 buckets the
+//    map is one saturating float-to-byte conversion (v_cvt_pk_u8_f32: round, clamp to
+//    [0, 255], NaN to 0) over a table of 256 entries; larger tables clamp, then truncate.
+//    At 4 bits the 32 entries of 8 bytes cover the 64 LDS banks once, so the lanes of a
+//    lookup never conflict.
 //  Anything outside those conditions (NaN, +-inf, huge |y|, unsorted or repeated centroids,
 //  a bucket holding two thresholds) takes the reference's linear scan.
 #pragma once
@@ -97,9 +102,16 @@ __device__ inline float threshold_walk4(float c0, float c1) {
     return __builtin_nanf("");
 }
 
+constexpr int kBucketsU8 = 256;  // tables of at most this many buckets use bucket_u8
+__device__ __forceinline__ int bucket_u8(float jf) {
+    return (int)__builtin_amdgcn_cvt_pk_u8_f32(jf, 0u, 0u);
+}
+__device__ __forceinline__ int bucket_wide(float jf, float jmax) {
+    return (int)__builtin_amdgcn_fmed3f(jf, 0.0f, jmax);
+}
 __device__ __forceinline__ int bucket_of(const Quantizer& q, float y) {
     const float jf = fmaf(y, q.scale, q.offset);
-    return (int)__builtin_amdgcn_fmed3f(jf, 0.0f, q.jmax);
+    return q.J <= kBucketsU8 ? bucket_u8(jf) : bucket_wide(jf, q.jmax);
 }
 
 // The reference's linear scan.
@@ -200,11 +212,11 @@ __device__ inline void quantizer_finish(Quantizer& q, int L) {
         }
         q.ybound = yb;
         q.L = L;
-        int J = 4 * L;
+        int J = 2 * L;
         if (J < 16) J = 16;
         if (J > kMaxBuckets) J = kMaxBuckets;
         q.J = J;
-        q.jmax = (float)(J - 1);
+        q.jmax = (float)(J <= kBucketsU8 ? kBucketsU8 - 1 : J - 1);
     }
     build_sync<kOneWave>();
     const bool fast = q.ybound > 0.0f;
@@ -244,7 +256,9 @@ __device__ inline void quantizer_finish(Quantizer& q, int L) {
         for (int i = tid; i < L - 1; i += bs) q.jt[i] = bucket_of(q, q.t[i]);
         build_sync<kOneWave>();
         const int n = L - 1;
-        for (int j = tid; j < q.J; j += bs) {
+        // every entry the bucket map can return: J, or all 256 of the byte map
+        const int nent = q.J <= kBucketsU8 ? kBucketsU8 : q.J;
+        for (int j = tid; j < nent; j += bs) {
             int lo = 0, hi = n;  // first q with jt[q] >= j
             while (lo < hi) {
                 const int mid = (lo + hi) >> 1;

@@ -301,8 +301,15 @@ struct TileQuant {
                 *(f32x4*)&y_out[yrow + 32 * c + 8 * (v >> 2) + 4 * (threadIdx.x >> 5 & 1)] =
                     f32x4{y[v - 3], y[v - 2], y[v - 1], y[v]};
         } else if constexpr (kUnitFast) {
+            // the quantizer's bucket map (bucket_of), with its table size known here: at most
+            // 7 bits the table has at most 256 buckets; at 8 bits jmax tells which map it is
             const float jf = fmaf(y[v], scale, offset);
-            ent[v] = qz.ent[(int)__builtin_amdgcn_fmed3f(jf, 0.0f, jmax)];
+            int j;
+            if constexpr (kBits <= 7)
+                j = bucket_u8(jf);
+            else
+                j = jmax <= (float)(kBucketsU8 - 1) ? bucket_u8(jf) : bucket_wide(jf, jmax);
+            ent[v] = qz.ent[j];
         }
     }
     // Phase B of value v: the code, packed MSB first into the half-group of group v / 4.

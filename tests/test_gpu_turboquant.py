@@ -212,6 +212,54 @@ def test_zero_vectors(dev):
     assert not np.isnan(o).any() and not o.any()
 
 
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_compress_nonfinite_rows(dev, bits):
+    """Vectors holding inf, -inf or NaN rotate to NaN and take code 0 everywhere, which is
+    what the reference's scan returns for NaN (no distance compares below the first); vectors
+    at the fp16 maximum rotate to finite values. Bytes equal the oracle's quantize-pack of the kernel's own
+    rotated vectors, and the oracle's compress on the nonfinite ones, flat and through the K+V
+    planned launch."""
+    rng = np.random.default_rng(bits + 40)
+    N, H, hd = 40, 8, 128
+    x = kv(rng, N, H, hd)
+    x[3, 1, 7] = np.inf
+    x[5, 0, 0] = -np.inf
+    x[9, 7, 127] = np.nan
+    x[13, 4, :] = np.inf
+    x[14, 5, :] = np.nan
+    x[11, 2, :] = np.float16(65504)
+    x[12, 3, ::2] = np.float16(-65504)
+    rot = tq.rotation_matrix(hd, 42)
+    cent = tq.codebook(hd, bits)[0]
+    packed, norms = compress(x, rot, cent, bits, dev)
+    packed = packed.reshape(N * H, -1)
+    with np.errstate(invalid="ignore", over="ignore"):
+        po, no, _ = oracle.tq_compress(x, rot, cent, bits)
+        bad = ~np.isfinite(x.astype(np.float32)).all(-1).reshape(-1)
+    assert bad.sum() == 5
+    y, _ = rotate(x, rot, dev)
+    assert np.isnan(y[bad]).all() and np.isfinite(y[~bad]).all()
+    assert np.array_equal(packed, oracle.tq_quantize_pack(y, cent, bits))
+    assert np.array_equal(packed[bad], po[bad]) and not packed[bad].any()
+    n, want = norms.reshape(-1).astype(np.float32), no.astype(np.float32)
+    assert np.array_equal(np.isnan(n), np.isnan(want)) and np.isnan(n[bad]).sum() == 2
+    inf_rows = bad & ~np.isnan(want)  # the vectors holding an inf and no NaN
+    assert np.isinf(n[inf_rows]).all() and np.array_equal(n[inf_rows], want[inf_rows])
+    # the vectors at the fp16 maximum keep finite rotated values, but their norms (~7e5)
+    # overflow fp16 to inf, as the oracle's do
+    assert np.array_equal(np.isinf(n), np.isinf(want)) and np.isinf(n[~bad]).sum() == 2
+    plan = K.TqPlan(dev_t(rot, dev), dev_t(cent, dev), bits)
+    tx = dev_t(x, dev)
+    out = [(torch.empty((N, H * K.packed_dim(hd, bits)), dtype=torch.uint8, device=dev),
+            torch.empty((N, H), dtype=torch.float16, device=dev)) for _ in range(2)]
+    K.tq_compress_kv_planned(plan, plan, tx, tx, *out[0], *out[1])
+    torch.cuda.synchronize()
+    for p, nn in out:
+        assert np.array_equal(p.cpu().numpy().reshape(N * H, -1), packed)
+        assert np.array_equal(nn.cpu().numpy().reshape(-1).view(np.uint16),
+                              norms.reshape(-1).view(np.uint16))
+
+
 @pytest.mark.parametrize("bits", [4, 3])
 def test_layer_scale_kv_compress(dev, bits):
     """One layer of Llama-3.1-8B K at 32768 tokens x 8 kv heads: bytes bit-exact given the
