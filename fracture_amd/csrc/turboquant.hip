@@ -686,15 +686,188 @@ __global__ __launch_bounds__(256) void tq_quantize_pack_kernel(const float* __re
 // MFMA dequantize, head_dim 128 (turboquant_decompress.cu:21-94):
 //   unpack -> c[idx] -> x_hat = Pi^T y_hat -> fp16(x_hat * float(norm)).
 // ---------------------------------------------------------------------------------------
-struct DequantLds {
-    uint32_t tab[kMaxLevels];  // c -> fp16 bits of (c_hi | c_lo << 16), c = c_hi + c_lo*2^-12
-    u32x2 pair[256];           // 4-bit: byte -> {hi(c[b>>4]) | hi(c[b&15])<<16, same for lo}
+// x_hat = Pi_hi^T c_hi + 2^-12 (Pi_lo'^T c_hi + Pi_hi^T c_lo'). The main product runs on fp16
+// MFMA (v_mfma_f32_32x32x16_f16, exact products). The two correction products, each ~2^-11
+// of it, run on fp8 E4M3 MFMA (v_mfma_scale_f32_32x32x64_f8f6f4: 64 coordinates per
+// instruction at twice the fp16 rate), which cuts the kernel's MFMA time by a third. Their
+// operands are prescaled by powers of two into fp8's normal range when the tables are built
+// (f8_prescale) and the instruction's E8M0 operand scales undo that exactly. fp8 rounds a
+// correction term to 2^-4 of itself: ~2^-15 of the term |Pi||c|, against 2^-11 (half an
+// fp16 ulp) for the stored output.
+// fp8 operand u (0, 1) of lane (i or r, h) is 8 registers: byte b is coordinate 64h + 32u + b.
+// The A and B operands use the same map, so the product sums over exactly those coordinates,
+// in whatever order the instruction assigns them to K.
+// ---------------------------------------------------------------------------------------
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+// Power-of-two exponent that brings max |v| into [128, 256): fp8 E4M3's normal range, under
+// its 448 maximum. 0 for a zero or non-finite maximum.
+__device__ inline int f8_prescale(float maxabs) {
+    if (!(maxabs > 0.0f) || !(maxabs <= 3.0e38f)) return 0;
+    int e;
+    (void)frexpf(maxabs, &e);  // maxabs = f 2^e, f in [0.5, 1)
+    return min(max(8 - e, -120), 120);
+}
+// The instruction's E8M0 scale that undoes a prescale by 2^p: 2^(scale - 127) = 2^-p.
+__device__ __forceinline__ int f8_scale(int p) { return 127 - p; }
+// fp8 E4M3 bytes of 2^p a and 2^p b (v_cvt_pk_fp8_f32, round to nearest even), in the low
+// (kHi = false) or high half of old.
+template <bool kHi>
+__device__ __forceinline__ uint32_t f8_pk(float a, float b, int p, uint32_t old) {
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(a, p), ldexpf(b, p), (int)old, kHi);
+}
+
+// Dequantize A operands (A[i][k] = Pi[k][32c + i]) for lane (i, h):
+//   hi[c][s][lane]         8 fp16 of Pi_hi, coordinates 64h + 8s + 0..7;
+//   f8[c][u][t][q][lane]   16 fp8 bytes of 2^p Pi_lo' (t = 0) or 2^p Pi_hi (t = 1),
+//                          coordinates 64h + 32u + 16q + 0..15.
+struct DeqLds {
+    u32x4 hi[4][8][64];        // 32 KB
+    u32x4 f8[4][2][2][2][64];  // 32 KB
 };
 
-// fp16 hi and lo operand halves of two codes' table entries.
-__device__ __forceinline__ void split_pair(uint32_t t0, uint32_t t1, uint32_t& vh, uint32_t& vl) {
-    vh = __builtin_amdgcn_perm(t1, t0, 0x05040100u);
-    vl = __builtin_amdgcn_perm(t1, t0, 0x07060302u);
+// The dequantize's code-side tables and the four operand scales (E8M0).
+enum { kScaleALo = 0, kScaleAHi = 1, kScaleBHi = 2, kScaleBLo = 3 };
+struct DequantLds {
+    // code -> fp16 c_hi | fp8 2^p c_hi << 16 | fp8 2^p' c_lo' << 24 (c = c_hi + 2^-12 c_lo')
+    uint32_t tab[kMaxLevels];
+    // 4 bits: byte b (codes b >> 4, b & 15) -> {the two fp16 c_hi, fp8 [hi, hi, lo', lo']}
+    u32x2 pair[256];
+    int scale[4];
+};
+
+// fp8 quad [hi(c0), hi(c1), lo'(c0), lo'(c1)] of two table entries.
+__device__ __forceinline__ uint32_t f8_quad(uint32_t t0, uint32_t t1) {
+    return __builtin_amdgcn_perm(t1, t0, 0x07030602u);
+}
+// fp16 hi pair of two table entries.
+__device__ __forceinline__ uint32_t hi_pair(uint32_t t0, uint32_t t1) {
+    return __builtin_amdgcn_perm(t1, t0, 0x05040100u);
+}
+
+// Maxima of non-negative floats across the workgroup (kN of them per thread): each wave's go
+// to its own slots, and after the barrier every thread folds all of them. Compared as
+// integers, so a NaN (any non-negative NaN pattern is above +inf) survives to the result.
+template <int kN>
+__device__ __forceinline__ void block_max(float (&m)[kN], int (*slots)[kN], int nwaves) {
+    const int w = (int)(threadIdx.x >> 6);
+#pragma unroll
+    for (int j = 0; j < kN; ++j) {
+        const int v = wave_max_int(__float_as_int(m[j]));
+        if ((threadIdx.x & 63) == 0) slots[w][j] = v;
+    }
+    lds_barrier();
+#pragma unroll
+    for (int j = 0; j < kN; ++j) {
+        int v = 0;
+        for (int k = 0; k < nwaves; ++k) v = max(v, slots[k][j]);
+        m[j] = __int_as_float(v);
+    }
+}
+
+// Staging of the dequantize A operands in two steps (load() issues this thread's reads of
+// Pi, store() writes LDS), with the operand maxima in between. kThreads is the block size.
+template <int kThreads>
+struct DeqStage {
+    static constexpr int kFrags = 4 * 8 * 64;
+    static constexpr int kN = (kFrags + kThreads - 1) / kThreads;
+    float v[kN][8];  // Pi[64h + 8s + e][32c + i] for fragment (c, s, lane = (i, h))
+    __device__ __forceinline__ void load(const float* __restrict__ rot) {
+#pragma unroll
+        for (int n = 0; n < kN; ++n) {
+            const int idx = (int)threadIdx.x + n * kThreads;
+            if (kFrags % kThreads != 0 && idx >= kFrags) break;
+            const int lane = idx & 63, s = (idx >> 6) & 7, c = idx >> 9;
+            const int row = 32 * c + (lane & 31), k0 = 64 * (lane >> 5) + 8 * s;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[n][e] = rot[(k0 + e) * kHd + row];
+        }
+    }
+    // this thread's maxima of |Pi_lo'| and |Pi_hi|, folded into mlo and mhi
+    __device__ __forceinline__ void maxima(float& mlo, float& mhi) const {
+#pragma unroll
+        for (int n = 0; n < kN; ++n) {
+            const int idx = (int)threadIdx.x + n * kThreads;
+            if (kFrags % kThreads != 0 && idx >= kFrags) break;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float x = v[n][e];
+                const float hi = (float)(_Float16)x;
+                mhi = fmaxf(mhi, fabsf(hi));
+                mlo = fmaxf(mlo, fabsf((x - hi) * kLoScale));
+            }
+        }
+    }
+    // p_lo, p_hi: the prescales of Pi_lo' and Pi_hi (f8_prescale of their maxima)
+    __device__ __forceinline__ void store(DeqLds& L, int p_lo, int p_hi) const {
+#pragma unroll
+        for (int n = 0; n < kN; ++n) {
+            const int idx = (int)threadIdx.x + n * kThreads;
+            if (kFrags % kThreads != 0 && idx >= kFrags) break;
+            const int lane = idx & 63, s = (idx >> 6) & 7, c = idx >> 9;
+            uint32_t hw[4], l8[2], h8[2];
+            float hi[8], lo[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const _Float16 h = (_Float16)v[n][e];
+                hi[e] = (float)h;
+                lo[e] = (v[n][e] - hi[e]) * kLoScale;
+            }
+#pragma unroll
+            for (int e2 = 0; e2 < 4; ++e2)
+                hw[e2] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi[2 * e2]) |
+                         ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi[2 * e2 + 1]) << 16);
+#pragma unroll
+            for (int d = 0; d < 2; ++d) {
+                l8[d] = f8_pk<true>(lo[4 * d + 2], lo[4 * d + 3], p_lo,
+                                    f8_pk<false>(lo[4 * d], lo[4 * d + 1], p_lo, 0u));
+                h8[d] = f8_pk<true>(hi[4 * d + 2], hi[4 * d + 3], p_hi,
+                                    f8_pk<false>(hi[4 * d], hi[4 * d + 1], p_hi, 0u));
+            }
+            L.hi[c][s][lane] = u32x4{hw[0], hw[1], hw[2], hw[3]};
+            // coordinates 64h + 8s + 0..7 = chunk q = (s >> 1) & 1 of operand u = s >> 2, at
+            // byte 8 (s & 1) of it
+            const int u = s >> 2, q = (s >> 1) & 1, off = 2 * (s & 1);
+            uint32_t* dl = (uint32_t*)&L.f8[c][u][0][q][lane] + off;
+            uint32_t* dh = (uint32_t*)&L.f8[c][u][1][q][lane] + off;
+            *(u32x2*)dl = u32x2{l8[0], l8[1]};
+            *(u32x2*)dh = u32x2{h8[0], h8[1]};
+        }
+    }
+};
+
+// This thread's centroid's |c_hi| and |c_lo'| (zero past the codebook).
+__device__ __forceinline__ void centroid_maxima(float c, float& mhi, float& mlo) {
+    const float hi = (float)(_Float16)c;
+    mhi = fabsf(hi);
+    mlo = fabsf((c - hi) * kLoScale);
+}
+// Table entry of centroid c (DequantLds::tab) for prescales p_hi, p_lo of c_hi and c_lo'.
+__device__ __forceinline__ uint32_t dq_tab_entry(float c, int p_hi, int p_lo) {
+    const _Float16 h = (_Float16)c;
+    const float hi = (float)h, lo = (c - hi) * kLoScale;
+    const uint32_t f8 = f8_pk<false>(hi, 0.0f, p_hi, 0u) & 0xffu;
+    const uint32_t l8 = f8_pk<false>(lo, 0.0f, p_lo, 0u) & 0xffu;
+    return (uint32_t)__builtin_bit_cast(uint16_t, h) | (f8 << 16) | (l8 << 24);
+}
+// The workgroup's tables from the four maxima {|Pi_lo'|, |Pi_hi|, |c_hi|, |c_lo'|}: the
+// scales, and the entry of centroid c_own for thread i < kMaxLevels (c_own = 0 past L).
+// The 4-bit pair table needs the entries: build_pairs after a barrier.
+__device__ __forceinline__ void dq_tables(DequantLds& t, const float (&m)[4], float c_own) {
+    const int p_hi = f8_prescale(m[2]), p_lo = f8_prescale(m[3]);
+    if (threadIdx.x == 0) {
+        t.scale[kScaleALo] = f8_scale(f8_prescale(m[0]));
+        t.scale[kScaleAHi] = f8_scale(f8_prescale(m[1]));
+        t.scale[kScaleBHi] = f8_scale(p_hi);
+        t.scale[kScaleBLo] = f8_scale(p_lo);
+    }
+    if ((int)threadIdx.x < kMaxLevels) t.tab[threadIdx.x] = dq_tab_entry(c_own, p_hi, p_lo);
+}
+__device__ __forceinline__ void dq_pairs(DequantLds& t) {
+    for (int b = threadIdx.x; b < 256; b += blockDim.x) {
+        const uint32_t t0 = t.tab[b >> 4], t1 = t.tab[b & 15];
+        t.pair[b] = u32x2{hi_pair(t0, t1), f8_quad(t0, t1)};
+    }
 }
 
 // One lane's codes of a tile: row r = lane & 31, groups [8h, 8h+8) (8*kBits bytes at byte
@@ -734,18 +907,25 @@ __device__ __forceinline__ void load_code_half(const uint8_t* __restrict__ packe
     cw.norm = norms[row];
 }
 
-// The 8 codes of group s of this lane's half as fp16 hi / lo B fragments.
+// The B operands of a tile's codes: bh[s] the fp16 c_hi of coordinates 64h + 8s + 0..7;
+// b8[u][0 | 1] the fp8 c_hi / c_lo' of coordinates 64h + 32u + 0..31.
+struct CodeOps {
+    f16x8 bh[8];
+    i32x8 b8[2][2];
+};
+
+// Group s (8 codes) of this lane's half into the B operands.
 template <int kBits>
 __device__ __forceinline__ void decode_group(const DequantLds& t, const CodeHalf<kBits>& cw,
-                                             int s, f16x8& bh, f16x8& bl) {
-    uint32_t vh[4], vl[4];
+                                             int s, CodeOps& ops) {
+    uint32_t vh[4], fq[4];  // per code pair p: fp16 hi pair, fp8 quad
     if constexpr (kBits == 4) {
         const uint32_t g = cw.w[s];  // byte p: coordinates (2p, 2p+1) in (high, low) nibbles
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
             const u32x2 e = t.pair[(g >> (8 * p)) & 0xffu];
             vh[p] = e[0];
-            vl[p] = e[1];
+            fq[p] = e[1];
         }
     } else {
         uint64_t word = 0;  // big-endian group word of kBits bytes
@@ -758,11 +938,18 @@ __device__ __forceinline__ void decode_group(const DequantLds& t, const CodeHalf
         for (int p = 0; p < 4; ++p) {
             const uint32_t c0 = (uint32_t)(word >> (kBits * (7 - 2 * p))) & ((1u << kBits) - 1u);
             const uint32_t c1 = (uint32_t)(word >> (kBits * (6 - 2 * p))) & ((1u << kBits) - 1u);
-            split_pair(t.tab[c0], t.tab[c1], vh[p], vl[p]);
+            const uint32_t t0 = t.tab[c0], t1 = t.tab[c1];
+            vh[p] = hi_pair(t0, t1);
+            fq[p] = f8_quad(t0, t1);
         }
     }
-    bh = __builtin_bit_cast(f16x8, u32x4{vh[0], vh[1], vh[2], vh[3]});
-    bl = __builtin_bit_cast(f16x8, u32x4{vl[0], vl[1], vl[2], vl[3]});
+    ops.bh[s] = __builtin_bit_cast(f16x8, u32x4{vh[0], vh[1], vh[2], vh[3]});
+    const int u = s >> 2, j = 2 * (s & 3);  // registers j, j + 1 of operand u
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+        ops.b8[u][0][j + d] = (int)__builtin_amdgcn_perm(fq[2 * d + 1], fq[2 * d], 0x05040100u);
+        ops.b8[u][1][j + d] = (int)__builtin_amdgcn_perm(fq[2 * d + 1], fq[2 * d], 0x07060302u);
+    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -771,7 +958,32 @@ __device__ __forceinline__ void decode_group(const DequantLds& t, const CodeHalf
 // Lane (r, h) ends block c holding coordinates 32c + 8g + 4h + e of row r; neighbouring
 // chunks are exchanged with the partner lane so every lane stores 16 contiguous bytes.
 // ---------------------------------------------------------------------------------------
-// x = Pi^T y of the lane's row from the (hi, lo') B fragments of y, stored as fp16(x * nrm).
+// Block c of the lane's row: fp16((acc1 + 2^-12 acc2) * nrm) to orow[32c .. 32c + 31].
+__device__ __forceinline__ void store_block(const f32x16& acc1, const f32x16& acc2, float nrm,
+                                            uint16_t* __restrict__ orow, int c, bool row_ok) {
+    uint32_t ch[4][2];  // chunk g: coordinates 32c + 8g + 4h + 0..3 as fp16 pairs
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const float x0 = fmaf(acc2[4 * g + 2 * e], kLoInv, acc1[4 * g + 2 * e]) * nrm;
+            const float x1 = fmaf(acc2[4 * g + 2 * e + 1], kLoInv, acc1[4 * g + 2 * e + 1]) * nrm;
+            ch[g][e] = f2h(x0) | (f2h(x1) << 16);
+        }
+    }
+    // chunks (2m, 2m+1): lane h = 0 takes coordinates 16m + 0..7, lane h = 1 16m + 8..15
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) swap_halves(ch[2 * m][e], ch[2 * m + 1][e]);
+        if (row_ok)
+            *(u32x4*)&orow[32 * c + 16 * m] =
+                u32x4{ch[2 * m][0], ch[2 * m][1], ch[2 * m + 1][0], ch[2 * m + 1][1]};
+    }
+}
+
+// x = Pi^T y of the lane's row from the (hi, lo') fp16 B fragments of y (three fp16
+// products per step), stored as fp16(x * nrm).
 __device__ __forceinline__ void rotate_back_store(const RotLds& L, const f16x8 (&bh)[8],
                                                   const f16x8 (&bl)[8], float nrm,
                                                   uint16_t* __restrict__ out, int64_t m0,
@@ -789,36 +1001,50 @@ __device__ __forceinline__ void rotate_back_store(const RotLds& L, const f16x8 (
             acc2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh[s], acc2, 0, 0, 0);
             acc2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bl[s], acc2, 0, 0, 0);
         }
-        uint32_t ch[4][2];  // chunk g: coordinates 32c + 8g + 4h + 0..3 as fp16 pairs
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const float x0 = fmaf(acc2[4 * g + 2 * e], kLoInv, acc1[4 * g + 2 * e]) * nrm;
-                const float x1 =
-                    fmaf(acc2[4 * g + 2 * e + 1], kLoInv, acc1[4 * g + 2 * e + 1]) * nrm;
-                ch[g][e] = f2h(x0) | (f2h(x1) << 16);
-            }
-        }
-        // chunks (2m, 2m+1): lane h = 0 takes coordinates 16m + 0..7, lane h = 1 16m + 8..15
-#pragma unroll
-        for (int m = 0; m < 2; ++m) {
-#pragma unroll
-            for (int e = 0; e < 2; ++e) swap_halves(ch[2 * m][e], ch[2 * m + 1][e]);
-            if (r < nvalid)
-                *(u32x4*)&orow[32 * c + 16 * m] =
-                    u32x4{ch[2 * m][0], ch[2 * m][1], ch[2 * m + 1][0], ch[2 * m + 1][1]};
-        }
+        store_block(acc1, acc2, nrm, orow, c, r < nvalid);
     }
 }
+
+// fp8 A operand (u, t) of block c: 8 registers.
+__device__ __forceinline__ i32x8 deq_a8(const DeqLds& L, int c, int u, int t, int lane) {
+    const u32x4 a = L.f8[c][u][t][0][lane], b = L.f8[c][u][t][1][lane];
+    return i32x8{(int)a[0], (int)a[1], (int)a[2], (int)a[3],
+                 (int)b[0], (int)b[1], (int)b[2], (int)b[3]};
+}
+
 template <int kBits>
-__device__ __forceinline__ void dequant_tile(const DequantLds& t, const RotLds& L,
+__device__ __forceinline__ void dequant_tile(const DequantLds& t, const DeqLds& L,
                                              const CodeHalf<kBits>& cw,
                                              uint16_t* __restrict__ out, int64_t m0, int nvalid) {
-    f16x8 bh[8], bl[8];
+    const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
+    CodeOps ops;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) decode_group<kBits>(t, cw, s, bh[s], bl[s]);
-    rotate_back_store(L, bh, bl, h2f(cw.norm), out, m0, nvalid);
+    for (int s = 0; s < 8; ++s) decode_group<kBits>(t, cw, s, ops);
+    const int sa_lo = t.scale[kScaleALo], sa_hi = t.scale[kScaleAHi];
+    const int sb_hi = t.scale[kScaleBHi], sb_lo = t.scale[kScaleBLo];
+    const float nrm = h2f(cw.norm);
+    uint16_t* orow = out + m0 * kHd + (r * kHd + 8 * h);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        __builtin_amdgcn_sched_barrier(0);  // keep each block's fragment loads within it
+        f32x16 acc1 = {}, acc2 = {};
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const f16x8 ah = __builtin_bit_cast(f16x8, L.hi[c][s][lane]);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, ops.bh[s], acc1, 0, 0, 0);
+            if (s & 1) {  // one correction product every second step: (u, t) = (s / 4, s / 2 % 2)
+                const int u = s >> 2, tt = (s >> 1) & 1;
+                const i32x8 a8 = deq_a8(L, c, u, tt, lane);
+                if (tt == 0)  // Pi_lo' c_hi
+                    acc2 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                        a8, ops.b8[u][0], acc2, 0, 0, 0, sa_lo, 0, sb_hi);
+                else  // Pi_hi c_lo'
+                    acc2 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                        a8, ops.b8[u][1], acc2, 0, 0, 0, sa_hi, 0, sb_lo);
+            }
+        }
+        store_block(acc1, acc2, nrm, orow, c, r < nvalid);
+    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -888,18 +1114,10 @@ tq_rotate_back_kernel(const float* __restrict__ y, const float* __restrict__ rot
     }
 }
 
-// Table entry of centroid c: fp16 bits of c_hi | c_lo' << 16 (c = c_hi + c_lo' 2^-12).
-__device__ __forceinline__ uint32_t dq_tab_entry(float c) {
-    const _Float16 hi = (_Float16)c;
-    const uint32_t hb = __builtin_bit_cast(uint16_t, hi);
-    const uint32_t lb = __builtin_bit_cast(uint16_t, (_Float16)((c - (float)hi) * kLoScale));
-    return hb | (lb << 16);
-}
-
 // The wave's tile loop: ca holds its first tile (loads issued); each tile's successor is in
 // flight while it computes.
 template <int kBits>
-__device__ __forceinline__ void dequant_waves(const DequantLds& t, const RotLds& rl,
+__device__ __forceinline__ void dequant_waves(const DequantLds& t, const DeqLds& rl,
                                               const uint8_t* __restrict__ packed,
                                               const uint16_t* __restrict__ norms,
                                               uint16_t* __restrict__ out, int64_t rows,
@@ -925,7 +1143,7 @@ __device__ __forceinline__ void dequant_waves(const DequantLds& t, const RotLds&
 // ---------------------------------------------------------------------------------------
 struct TqPlanDev {
     RotLds comp;         // compress fragments (hi scaled by 2^12, lo')
-    RotLds deq;          // dequantize fragments (transposed, hi, lo')
+    DeqLds deq;          // dequantize A operands (fp16 Pi_hi, fp8 Pi_lo' and Pi_hi)
     Quantizer qz;        // the built quantizer
     DequantLds dt;       // dequantize centroid tables
     float rot[kHd * kHd];
@@ -939,7 +1157,7 @@ __device__ __forceinline__ const RotLds& plan_compress_frags(const TqPlanDev* p)
 // The planned dequantize of one tensor by workgroup blk of nblk: the tables and fragments are
 // copied from the plan into LDS while the first tile's loads are in flight.
 template <int kBits>
-__device__ __forceinline__ void dequant_planned(DequantLds& t, RotLds& rl,
+__device__ __forceinline__ void dequant_planned(DequantLds& t, DeqLds& rl,
                                                 const uint8_t* __restrict__ packed,
                                                 const uint16_t* __restrict__ norms,
                                                 const TqPlanDev* __restrict__ plan,
@@ -949,7 +1167,7 @@ __device__ __forceinline__ void dequant_planned(DequantLds& t, RotLds& rl,
     const int64_t stride = nblk * kWavesD;
     const int64_t tile = blk * kWavesD + wave_id();
     LdsCopy<64 * kWavesD, (int)sizeof(DequantLds)> tc;
-    LdsCopy<64 * kWavesD, (int)sizeof(RotLds)> rc;
+    LdsCopy<64 * kWavesD, (int)sizeof(DeqLds)> rc;
     tc.load(&plan->dt);
     rc.load(&plan->deq);
     __builtin_amdgcn_sched_barrier(0);
@@ -969,11 +1187,12 @@ tq_dequant_mfma_kernel(const uint8_t* __restrict__ packed, const uint16_t* __res
                        const TqPlanDev* __restrict__ plan, uint16_t* __restrict__ out,
                        int64_t rows) {
     __shared__ DequantLds t;
-    __shared__ RotLds rl;
+    __shared__ DeqLds rl;
     if constexpr (kPlanned) {
         dequant_planned<kBits>(t, rl, packed, norms, plan, out, rows, blockIdx.x, gridDim.x);
         return;
     }
+    __shared__ int mx[kWavesD][4];
     const int64_t ntiles = ceil_div(rows, kTile);
     const int64_t stride = (int64_t)gridDim.x * kWavesD;
     int64_t tile = (int64_t)blockIdx.x * kWavesD + wave_id();
@@ -981,19 +1200,19 @@ tq_dequant_mfma_kernel(const uint8_t* __restrict__ packed, const uint16_t* __res
     // first tile, which stays in flight through the set-up (whose barriers order LDS only).
     static_assert(kMaxLevels <= 64 * kWavesD, "one centroid per thread");
     const float c_own = (int)threadIdx.x < L ? cent[threadIdx.x] : 0.0f;
-    RotStage<true, 64 * kWavesD, false> rs;
+    DeqStage<64 * kWavesD> rs;
     rs.load(rot);
     CodeHalf<kBits> ca, cb;
     load_code_half<kBits>(packed, norms, tile, ntiles, rows, ca);
-    if ((int)threadIdx.x < kMaxLevels) t.tab[threadIdx.x] = dq_tab_entry(c_own);
-    rs.store(rl);
+    float m[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // |Pi_lo'|, |Pi_hi|, |c_hi|, |c_lo'|
+    rs.maxima(m[0], m[1]);
+    centroid_maxima(c_own, m[2], m[3]);
+    block_max(m, mx, kWavesD);
+    dq_tables(t, m, c_own);
+    rs.store(rl, f8_prescale(m[0]), f8_prescale(m[1]));
     lds_barrier();
     if constexpr (kBits == 4) {
-        for (int b = threadIdx.x; b < 256; b += blockDim.x) {
-            uint32_t vh, vl;
-            split_pair(t.tab[b >> 4], t.tab[b & 15], vh, vl);
-            t.pair[b] = u32x2{vh, vl};
-        }
+        dq_pairs(t);
         lds_barrier();
     }
     dequant_waves<kBits>(t, rl, packed, norms, out, rows, tile, stride, ntiles, ca, cb);
@@ -1009,7 +1228,7 @@ tq_dequant_kv_mfma_kernel(const uint8_t* __restrict__ k_packed, const uint16_t* 
                           uint16_t* __restrict__ k_out, uint16_t* __restrict__ v_out,
                           int64_t rows) {
     __shared__ DequantLds t;
-    __shared__ RotLds rl;
+    __shared__ DeqLds rl;
     const int64_t blk = blockIdx.x >> 1, nblk = gridDim.x >> 1;
     if (blockIdx.x & 1)
         dequant_planned<kVBits>(t, rl, v_packed, v_norms, vplan, v_out, rows, blk, nblk);
@@ -1032,23 +1251,22 @@ __global__ __launch_bounds__(kPlanThreads) void tq_plan_kernel(const float* __re
         rs.store(p->comp);
     }
     {
-        RotStage<true, kPlanThreads, false> rs;
-        rs.load(rot);
-        rs.store(p->deq);
+        static_assert(kMaxLevels <= kPlanThreads, "one centroid per thread");
+        __shared__ int mx[kPlanThreads / 64][4];
+        DeqStage<kPlanThreads> ds;
+        ds.load(rot);
+        const float c_own = (int)threadIdx.x < L ? cent[threadIdx.x] : 0.0f;
+        float m[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // |Pi_lo'|, |Pi_hi|, |c_hi|, |c_lo'|
+        ds.maxima(m[0], m[1]);
+        centroid_maxima(c_own, m[2], m[3]);
+        block_max(m, mx, kPlanThreads / 64);
+        ds.store(p->deq, f8_prescale(m[0]), f8_prescale(m[1]));
+        dq_tables(p->dt, m, c_own);
     }
     for (int i = threadIdx.x; i < kHd * kHd; i += kPlanThreads) p->rot[i] = rot[i];
-    for (int i = threadIdx.x; i < kMaxLevels; i += kPlanThreads) {
-        const float c = i < L ? cent[i] : 0.0f;
-        p->cent[i] = c;
-        p->dt.tab[i] = dq_tab_entry(c);
-    }
-    for (int b = threadIdx.x; b < 256; b += kPlanThreads) {
-        const float c0 = (b >> 4) < L ? cent[b >> 4] : 0.0f;
-        const float c1 = (b & 15) < L ? cent[b & 15] : 0.0f;
-        uint32_t vh, vl;
-        split_pair(dq_tab_entry(c0), dq_tab_entry(c1), vh, vl);
-        p->dt.pair[b] = u32x2{vh, vl};
-    }
+    for (int i = threadIdx.x; i < kMaxLevels; i += kPlanThreads) p->cent[i] = i < L ? cent[i] : 0.0f;
+    __syncthreads();  // the table entries, written to the plan by other threads
+    dq_pairs(p->dt);
     __syncthreads();
     const uint32_t* q = (const uint32_t*)&qz;
     uint32_t* d = (uint32_t*)&p->qz;
