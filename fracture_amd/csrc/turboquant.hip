@@ -120,12 +120,15 @@ __device__ __forceinline__ int wave_id() {
 }
 
 // ---------------------------------------------------------------------------------------
-// Rotation fragments in LDS. MFMA step s of a 32-coordinate block takes K = 16 coordinates,
-// ordered so that lane half h, element e of step s is coordinate 64h + 8s + e: a lane's B
-// operand over the 8 steps is then one contiguous half of its vector (128 bytes of fp16
-// input, or 8 consecutive code groups), which it loads with wide loads.
-//   compress   (y = Pi x):      A[i][k] = Pi[32c + i][k]
-//   dequantize (x = Pi^T y):    A[i][k] = Pi[k][32c + i]
+// Rotation fragments in LDS. MFMA step s of a 32-coordinate block takes K = 16 coordinates;
+// lane half h holds 8 of them (element e):
+//   compress   (y = Pi x):      A[i][k] = Pi[32c + i][k], coordinate 16s + 8h + e. The two
+//              lanes of an input row load adjacent 16-byte pieces of it in each step, so a
+//              load instruction touches 32 cache lines, not 64 (the L1's per-line work was
+//              what slowed the tiles while loads were in flight: 50.4 -> 46.4 us for a
+//              layer's K+V);
+//   back-rotation of fp32 rows (x = Pi^T y):  A[i][k] = Pi[k][32c + i], coordinate
+//              64h + 8s + e (one contiguous half of the row per lane).
 // frag[c][s][0|1][lane] = 8 fp16 of the hi / lo' part, lane = (i = lane & 31, h = lane >> 5).
 // ---------------------------------------------------------------------------------------
 struct RotLds {
@@ -146,7 +149,8 @@ struct RotStage {
             const int idx = (int)threadIdx.x + n * kThreads;
             if (kFrags % kThreads != 0 && idx >= kFrags) break;
             const int lane = idx & 63, s = (idx >> 6) & 7, c = idx >> 9;
-            const int row = 32 * c + (lane & 31), k0 = 64 * (lane >> 5) + 8 * s;
+            const int row = 32 * c + (lane & 31);
+            const int k0 = kTranspose ? 64 * (lane >> 5) + 8 * s : 16 * s + 8 * (lane >> 5);
             if constexpr (kTranspose) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[n][e] = rot[(k0 + e) * kHd + row];
@@ -246,7 +250,7 @@ __device__ __forceinline__ void store_bytes(uint8_t* dst, const uint32_t (&w)[16
 }
 
 // One lane's half of a 32 x 128 fp16 input tile: row r = lane & 31, coordinates
-// [64h, 64h + 64) as 8 MFMA B fragments. Rows past the end (or a tile past the last) read
+// 16s + 8h + 0..7 as MFMA B fragment s (s = 0..7). Rows past the end (or a tile past the last) read
 // row 0 instead: their MFMA columns and results are discarded, and unconditional loads
 // never make the compiler wait for a register's earlier loads before reusing it.
 __device__ __forceinline__ const uint16_t* x_half_src(const uint16_t* __restrict__ in,
@@ -255,13 +259,13 @@ __device__ __forceinline__ const uint16_t* x_half_src(const uint16_t* __restrict
     const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
     const int64_t m0 = tile * kTile;
     const bool ok = tile < ntiles && r < rows - m0;
-    return in + (ok ? m0 * kHd + r * kHd : 0) + 64 * h;
+    return in + (ok ? m0 * kHd + r * kHd : 0) + 8 * h;
 }
 __device__ __forceinline__ void load_x_half(const uint16_t* __restrict__ in, int64_t tile,
                                             int64_t ntiles, int64_t rows, f16x8 (&x)[8]) {
     const uint16_t* src = x_half_src(in, tile, ntiles, rows);
 #pragma unroll
-    for (int s = 0; s < 8; ++s) x[s] = __builtin_bit_cast(f16x8, ld16(src + 8 * s));
+    for (int s = 0; s < 8; ++s) x[s] = __builtin_bit_cast(f16x8, ld16(src + 16 * s));
 }
 
 // ---------------------------------------------------------------------------------------
@@ -365,7 +369,7 @@ __device__ __forceinline__ void compress_tile(const Quantizer& qz, const RotLds&
     for (int q = 0; q < 32; ++q) {
         const int c = q >> 3, s = q & 7, b = c & 1;
         __builtin_amdgcn_sched_barrier(0);
-        if ((q & 3) == 0) pf[q >> 2] = __builtin_bit_cast(f16x8, ld16(pf_src + 8 * (q >> 2)));
+        if ((q & 3) == 0) pf[q >> 2] = __builtin_bit_cast(f16x8, ld16(pf_src + 16 * (q >> 2)));
         if (q + kAhead < 32) {
             const int n = q + kAhead;
             fh[n % kRing] = frag(L, n >> 3, n & 7, 0, lane);
