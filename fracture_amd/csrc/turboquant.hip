@@ -735,7 +735,8 @@ enum { kScaleALo = 0, kScaleAHi = 1, kScaleBHi = 2, kScaleBLo = 3 };
 struct DequantLds {
     // code -> fp16 c_hi | fp8 2^p c_hi << 16 | fp8 2^p' c_lo' << 24 (c = c_hi + 2^-12 c_lo')
     uint32_t tab[kMaxLevels];
-    // 4 bits: byte b (codes b >> 4, b & 15) -> {the two fp16 c_hi, fp8 [hi, hi, lo', lo']}
+    // 2, 3 or 4 bits: code pair b (codes b >> bits, b & (2^bits - 1); at 4 bits a code byte)
+    // -> {the two fp16 c_hi, fp8 [hi, hi, lo', lo']}; 2^(2 bits) entries
     u32x2 pair[256];
     int scale[4];
 };
@@ -867,9 +868,12 @@ __device__ __forceinline__ void dq_tables(DequantLds& t, const float (&m)[4], fl
     }
     if ((int)threadIdx.x < kMaxLevels) t.tab[threadIdx.x] = dq_tab_entry(c_own, p_hi, p_lo);
 }
-__device__ __forceinline__ void dq_pairs(DequantLds& t) {
-    for (int b = threadIdx.x; b < 256; b += blockDim.x) {
-        const uint32_t t0 = t.tab[b >> 4], t1 = t.tab[b & 15];
+// The pair table of a bits-wide code (2 to 4; none at other widths).
+__device__ __forceinline__ void dq_pairs(DequantLds& t, int bits) {
+    if (bits < 2 || bits > 4) return;
+    const int n = 1 << (2 * bits), m = (1 << bits) - 1;
+    for (int b = threadIdx.x; b < n; b += blockDim.x) {
+        const uint32_t t0 = t.tab[b >> bits], t1 = t.tab[b & m];
         t.pair[b] = u32x2{hi_pair(t0, t1), f8_quad(t0, t1)};
     }
 }
@@ -928,6 +932,22 @@ __device__ __forceinline__ void decode_group(const DequantLds& t, const CodeHalf
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
             const u32x2 e = t.pair[(g >> (8 * p)) & 0xffu];
+            vh[p] = e[0];
+            fq[p] = e[1];
+        }
+    } else if constexpr (kBits == 2 || kBits == 3) {
+        // big-endian group word of kBits bytes; codes 2p, 2p + 1 are its 2 kBits bits at
+        // 2 kBits (3 - p), the pair table's index
+        uint32_t word = 0;
+#pragma unroll
+        for (int k = 0; k < kBits; ++k) {
+            const int byte = s * kBits + k;
+            word = (word << 8) | ((cw.w[byte >> 2] >> (8 * (byte & 3))) & 0xffu);
+        }
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const u32x2 e =
+                t.pair[(word >> (2 * kBits * (3 - p))) & ((1u << (2 * kBits)) - 1u)];
             vh[p] = e[0];
             fq[p] = e[1];
         }
@@ -1215,8 +1235,8 @@ tq_dequant_mfma_kernel(const uint8_t* __restrict__ packed, const uint16_t* __res
     dq_tables(t, m, c_own);
     rs.store(rl, f8_prescale(m[0]), f8_prescale(m[1]));
     lds_barrier();
-    if constexpr (kBits == 4) {
-        dq_pairs(t);
+    if constexpr (kBits >= 2 && kBits <= 4) {
+        dq_pairs(t, kBits);
         lds_barrier();
     }
     dequant_waves<kBits>(t, rl, packed, norms, out, rows, tile, stride, ntiles, ca, cb);
@@ -1246,7 +1266,8 @@ tq_dequant_kv_mfma_kernel(const uint8_t* __restrict__ k_packed, const uint16_t* 
 constexpr int kPlanThreads = 64 * kWavesC;
 __global__ __launch_bounds__(kPlanThreads) void tq_plan_kernel(const float* __restrict__ rot,
                                                                const float* __restrict__ cent,
-                                                               int L, TqPlanDev* __restrict__ p) {
+                                                               int L, int bits,
+                                                               TqPlanDev* __restrict__ p) {
     __shared__ Quantizer qz;
     quantizer_build(qz, cent, L);
     {
@@ -1270,7 +1291,7 @@ __global__ __launch_bounds__(kPlanThreads) void tq_plan_kernel(const float* __re
     for (int i = threadIdx.x; i < kHd * kHd; i += kPlanThreads) p->rot[i] = rot[i];
     for (int i = threadIdx.x; i < kMaxLevels; i += kPlanThreads) p->cent[i] = i < L ? cent[i] : 0.0f;
     __syncthreads();  // the table entries, written to the plan by other threads
-    dq_pairs(p->dt);
+    dq_pairs(p->dt, bits);
     __syncthreads();
     const uint32_t* q = (const uint32_t*)&qz;
     uint32_t* d = (uint32_t*)&p->qz;
@@ -1606,7 +1627,7 @@ int fhip_tq_plan_create(const float* rotation, const float* centroids, int n_lev
     hipError_t e = hipMalloc((void**)&dev, sizeof(TqPlanDev));
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(tq_plan_kernel, dim3(1), dim3(kPlanThreads), 0,
-                       fhip_host::as_stream(stream), rotation, centroids, n_levels, dev);
+                       fhip_host::as_stream(stream), rotation, centroids, n_levels, bits, dev);
     e = hipGetLastError();
     if (e != hipSuccess) {
         (void)hipFree(dev);
