@@ -371,7 +371,7 @@ __global__ __launch_bounds__(256) void tq_attn_split_kernel(
 //            splits per step, each item summed in split order;
 //   phase 3: the matvec, one output coordinate for 4 vectors per thread and step.
 // Dynamic LDS: hd * hd rotation floats (kRotLds), then kCombHeads * nsplit weights.
-constexpr int kCombHeads = 8;
+constexpr int kCombHeads = 4;  // two workgroups per CU at the decode workload's 2048 vectors
 constexpr int kRotLdsMaxHd = 128;
 constexpr int kMaxTokensTq = kSplit * kSplit;  // 1024 splits: 32 KB of combine weights
 size_t combine_lds_bytes(int hd, int nsplit, bool merge_only = false) {
@@ -441,10 +441,12 @@ __global__ __launch_bounds__(256) void tq_attn_combine_kernel(
         }
     }
     {
-        const int hh = tid >> 5, l32 = tid & 31;
+        // a half-wave per vector (the half-waves past kCombHeads only join the shuffles)
+        const int hh = min(tid >> 5, kCombHeads - 1), l32 = tid & 31;
+        const bool mine = (tid >> 5) < kCombHeads;
         const int64_t head = h0 + hh;
         int ns = 0;
-        if (head < nvec) {
+        if (mine && head < nvec) {
             const int clen = qs.causal_len((int)(head / qh));
             ns = (clen + kSplit - 1) / kSplit;
         }
@@ -462,7 +464,7 @@ __global__ __launch_bounds__(256) void tq_attn_combine_kernel(
         }
 #pragma unroll
         for (int off = 16; off >= 1; off >>= 1) L += __shfl_xor(L, off);
-        if (l32 == 0) {
+        if (mine && l32 == 0) {
             linv[hh] = L > 0.0f ? 1.0f / L : 0.0f;
             nsv[hh] = ns;
         }
