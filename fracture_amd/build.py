@@ -58,6 +58,10 @@ HOST_SAN = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=unde
             "-Xarch_host", "-fno-omit-frame-pointer", "-Xarch_host", "-fno-sanitize-recover=all"]
 SAN_BUILD = PKG / "_build_san"
 SAN_LIB = PKG / "_san" / "libfracture_hip.so"
+# The host build of the decode-attention kernel's index helpers (tq_attn_index.h), which the
+# CPU bounds check of that kernel's accesses calls. Plain C++: no GPU code, no HIP runtime.
+INDEX_LIB = PKG / "libfracture_hip_index.so"
+CXX = os.environ.get("CXX", "g++")
 
 
 def _compile(src: str, san: bool = False) -> Path:
@@ -98,7 +102,23 @@ def build(jobs: int | None = None, verbose: bool = True, host_sanitize: bool = F
     os.replace(tmp, out)
     if verbose:
         print(f"[build] {out.relative_to(ROOT)} ({out.stat().st_size // 1024} KiB)")
+    if not host_sanitize:
+        build_index(verbose)
     return out
+
+
+def build_index(verbose: bool = True) -> Path:
+    """libfracture_hip_index.so from tq_attn_index_host.cpp (host C++ only)."""
+    tmp = INDEX_LIB.with_suffix(".so.tmp")
+    cmd = [CXX, "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", f"-I{CSRC}", "-o", str(tmp),
+           str(CSRC / "tq_attn_index_host.cpp")]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError("index helper build failed:\n" + p.stdout + p.stderr)
+    os.replace(tmp, INDEX_LIB)
+    if verbose:
+        print(f"[build] {INDEX_LIB.relative_to(ROOT)}")
+    return INDEX_LIB
 
 
 if __name__ == "__main__":

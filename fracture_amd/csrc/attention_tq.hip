@@ -15,6 +15,7 @@
 //   2. split partials                  (the HBM stream over the pages)
 //   3. merge + unrotate -> fp16 output
 #include "fhip_internal.h"
+#include "tq_attn_index.h"
 #include "tq_quant.h"
 
 using namespace fhip;
@@ -554,6 +555,10 @@ constexpr int kSplitMfma = 256;  // positions per wave item (split)
 constexpr int kXcds = 8;         // MI355X: accelerator complex dies, each with its own L2
 constexpr int kSplitPages = kSplitMfma / FHIP_PAGE_TOKENS;
 constexpr int kWavesM = 4;      // waves per workgroup (independent work items)
+static_assert(kChunkM == fhip_idx::kChunk && kSplitMfma == fhip_idx::kSplitPositions &&
+                  kWavesM == fhip_idx::kBlockWaves && kXcds == fhip_idx::kXcdCount &&
+                  FHIP_PAGE_TOKENS == fhip_idx::kPageTokens,
+              "the kernel's shape is the one its index helpers describe");
 
 typedef int v2i_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
@@ -662,8 +667,9 @@ struct PageAddrs {
 template <class Pages>
 __device__ __forceinline__ uint64_t split_pages(const Pages& pg, const int32_t* table, int t_begin,
                                                 int t_end, int lane, PageAddrs* pages) {
-    const bool in = t_begin + FHIP_PAGE_TOKENS * lane < t_end;
-    const int id = in ? table[t_begin / FHIP_PAGE_TOKENS + lane] : -1;
+    int column;
+    const bool in = fhip_idx::split_page_column(t_begin, t_end, lane, column);
+    const int id = in ? table[column] : -1;
     const bool ok = in && pg.valid(id);
     const uint64_t vmask = __ballot(ok);
     if (vmask == 0) return 0;
@@ -718,10 +724,9 @@ __device__ __forceinline__ void dma16(const uint8_t* sbase, uint32_t voff, uint8
 // lane (n, rg); the lane's page is j0 + n / 4 and the four tiles are 4 rows apart.
 __device__ __forceinline__ void load_k(const PageAddrs* pages, int j0, int kvh, int g, int lane,
                                        u32x4 (&kc)[4]) {
-    const int n = lane & 15, rg = lane >> 4;
-    const uint8_t* src = pages[j0 + (n >> 2)].k + (uint32_t)(((4 * (n & 3)) * kvh + g) * 64 + 16 * rg);
+    const uint8_t* src = pages[j0 + fhip_idx::k_page(lane)].k + fhip_idx::k_offset(lane, kvh, g);
 #pragma unroll
-    for (int pt = 0; pt < 4; ++pt) kc[pt] = gld16(src + (uint32_t)(pt * kvh * 64));
+    for (int pt = 0; pt < 4; ++pt) kc[pt] = gld16(src + pt * fhip_idx::k_tile_stride(kvh));
 }
 // V codes by LDS DMA: copy i moves page j0 + i (positions 16i .. 16i + 15); lane L takes
 // position p = 16i + L / 4 and stores 16 bytes at 64p + 16(L % 4). The 16-byte segment it
@@ -750,8 +755,8 @@ struct NormRegs {
 };
 __device__ __forceinline__ NormRegs load_norms(const PageAddrs* pages, int j0, uint32_t pm, int t0,
                                                int t_end, int kvh, int g, int lane) {
-    const int k = lane >> 4;
-    const uint32_t row = (uint32_t)(((lane & 15) * kvh + g) * 2);
+    const int k = fhip_idx::norm_page(lane);
+    const uint32_t row = fhip_idx::norm_offset(lane, kvh, g);
     const bool ok = ((pm >> k) & 1u) && t0 + lane < t_end;
     const PageAddrs& pa = pages[j0 + k];
     return NormRegs{gld2(pa.kn + row), gld2(pa.vn + row), ok};
@@ -835,10 +840,9 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     // as workgroup (i / 8) (8 kvh) + 8 g + i % 8, and each line is filled into one L2 only.
     // A workgroup whose block holds no position leaves before the tables are built (the exit
     // is uniform, so no wave misses the barriers below).
-    const int64_t wg = blockIdx.x;
-    const int64_t per8 = (int64_t)kXcds * kvh;
-    const int64_t item = (wg / per8) * kXcds + wg % kXcds;
-    const int g = (int)((wg % per8) / kXcds);
+    int64_t item;
+    int g;
+    fhip_idx::wg_item(blockIdx.x, kvh, item, g);
     // Item (token group, block): a group is `tok` consecutive queries of one sequence (causal
     // prefill; 1 in decode), whose G query heads each fill MFMA columns h = G t + head.
     const int qg = (int)(item / nblk);
@@ -859,8 +863,7 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     }
     __syncthreads();
 
-    const int split = kWavesM * blk + wave;
-    const int t_begin = split * kSplitMfma;
+    const int t_begin = fhip_idx::split_begin(blk, wave);
     const int t_end = min(clen, t_begin + kSplitMfma);
     const int G = qh / kvh;
     const int32_t* table = qs.table + (int64_t)tq0 * qs.table_stride;
@@ -869,8 +872,9 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     const int ncols = tok * G;  // live head columns (at most 8)
     // this lane's column: token tq0 + ct, head ch; its causal length (0 for a column past the
     // queries, so that every position is masked for it)
-    const int ct = (n & 7) / G, ch = (n & 7) - ct * G;
-    const bool col_ok = (n & 7) < ncols && tq0 + ct < qs.seq_lens_count;
+    const int ct = (n & 7) / G;
+    bool col_ok;  // the column is head (n & 7) % G of a query of the group
+    const int64_t qvec = fhip_idx::q_vector(lane, tq0, tok, G, qs.seq_lens_count, qh, g, col_ok);
     const int col_len = col_ok ? qs.causal_len(tq0 + ct) : 0;
     // the shortest length of the group (its first query's): chunks below it need no mask
     const int min_len = tok > 1 ? qs.causal_len(tq0) : clen;
@@ -889,8 +893,7 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     const uint64_t vmask = t_begin < clen ? split_pages(pg, table, t_begin, t_end, lane, pages) : 0;
     if (vmask != 0) {
     // first chunk's copies go out before the Q set-up
-    const uint32_t v_lane_off =
-        (uint32_t)(((lane >> 2) * kvh + g) * 64 + 16 * ((lane & 3) ^ ((lane >> 3) & 3)));
+    const uint32_t v_lane_off = fhip_idx::v_offset(lane, kvh, g);
     uint32_t pmask = (uint32_t)vmask & 0xfu;  // pages of the current chunk to read
     dma_v(pages, 0, v_lane_off, vb, lane);  // chunk 0: buffer 0
     NormRegs nreg = load_norms(pages, 0, pmask, t_begin, t_end, kvh, g, lane);
@@ -903,12 +906,11 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     {
         // heads past G read head 0 and are zeroed by the multiplier
         // columns past the group's heads read the group's first vector and are zeroed
-        const float* qsrc =
-            qrot + ((int64_t)(col_ok ? tq0 + ct : tq0) * qh + (int64_t)g * G + (col_ok ? ch : 0)) * hd;
+        const float* qsrc = qrot + qvec * hd;
         const float qmul = col_ok ? scale * 1.4426950408889634f : 0.0f;
         f32x4_t qv[8];
 #pragma unroll
-        for (int s8 = 0; s8 < 8; ++s8) qv[s8] = *(const f32x4_t*)(qsrc + 32 * rg + 4 * s8);
+        for (int s8 = 0; s8 < 8; ++s8) qv[s8] = *(const f32x4_t*)(qsrc + fhip_idx::q_lane_offset(lane, s8));
 #pragma unroll
         for (int s8 = 0; s8 < 8; ++s8) {
 #pragma unroll
@@ -957,7 +959,7 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
 
     for (int t0 = t_begin, par = 0; t0 < t_end; t0 += kChunkM, par ^= 1) {
         const int tn = t0 + kChunkM;  // next chunk
-        const int jn = (tn - t_begin) >> 4;  // its first split page
+        const int jn = fhip_idx::chunk_first_page(tn, t_begin);  // its first split page
         const uint32_t pmask_n = tn < t_end ? (uint32_t)(vmask >> jn) & 0xfu : 0u;
         const bool full = pmask == 0xfu && tn <= t_end && tn <= min_len;
 
@@ -1223,10 +1225,9 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     // 16-byte reads per wave state and two 16-byte stores
     for (int it = lane; it < ncols * (hd / 8); it += 64) {
         const int h = it / (hd / 8), d0 = 8 * (it % (hd / 8));
-        const int ht = h / G;
-        if (tq0 + ht >= qs.seq_lens_count) continue;  // a column past the queries
-        // partial of vector (query tq0 + ht, q head G g + h - G ht)
-        const int64_t vec = (int64_t)(tq0 + ht) * qh + (int64_t)g * G + (h - ht * G);
+        if (tq0 + h / G >= qs.seq_lens_count) continue;  // a column past the queries
+        const int64_t vec = fhip_idx::partial_vector(h, tq0, G, qh, g);
+        const int64_t prow = fhip_idx::partial_row(vec, nsplit, blk);
         float mw[kWavesM], M = -__builtin_inff();
 #pragma unroll
         for (int w = 0; w < kWavesM; ++w) {
@@ -1250,13 +1251,12 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
                 }
             }
         }
-        float* pa = part_acc + (vec * nsplit + blk) * hd + d0;
+        float* pa = part_acc + prow * hd + d0;
         *(f32x4_t*)pa = A0;
         *(f32x4_t*)(pa + 4) = A1;
         if (d0 == 0) {  // m back in natural units
-            part_ml[(vec * nsplit + blk) * 2 + 0] =
-                M == -__builtin_inff() ? M : M * 0.6931471805599453f;
-            part_ml[(vec * nsplit + blk) * 2 + 1] = L;
+            part_ml[prow * 2 + 0] = M == -__builtin_inff() ? M : M * 0.6931471805599453f;
+            part_ml[prow * 2 + 1] = L;
         }
     }
 }

@@ -1,10 +1,12 @@
-"""CPU model of every global-memory address that the MFMA decode-attention kernel
+"""CPU check of every global-memory address that the MFMA decode-attention kernel
 (tq_attn_mfma_kernel in fracture_amd/csrc/attention_tq.hip) and its combine kernel form,
-checked against the buffers the launcher hands them.
+against the buffers the launcher hands them.
 
-The model restates the kernel's index arithmetic per workgroup (query, kv head, 1024-position
-block), per wave (one 256-position split of the block) and per 64-position chunk, vectorised
-over lanes with numpy:
+The MFMA kernel's addresses come from its own index functions (fracture_amd/csrc/
+tq_attn_index.h), called through their host build (libfracture_hip_index.so), for every
+workgroup of the launch grid, every wave (one 256-position split of the workgroup's
+1024-position block) and every 64-position chunk, with numpy over the 64 lanes. What they
+compute:
 
   split pages        entry j = table[t_begin / 16 + j] for pages holding positions of the split,
                      in the pool; every other entry is the split's first valid page (no valid
@@ -64,9 +66,79 @@ class Bounds:
         self.count[buf] += off.size
 
 
+class IndexLib:
+    """The kernel's own index arithmetic (fracture_amd/csrc/tq_attn_index.h), host build."""
+
+    def __init__(self):
+        import ctypes as C
+        from pathlib import Path
+        path = Path(__file__).resolve().parents[1] / "fracture_amd" / "libfracture_hip_index.so"
+        if not path.exists():
+            pytest.fail(f"{path} is missing: run __graft_entry__.build()")
+        self.C, self.lib = C, C.CDLL(str(path))
+        L = self.lib
+        L.fhip_idx_wg_item.argtypes = [C.c_int64, C.c_int, C.POINTER(C.c_int64), C.POINTER(C.c_int32)]
+        L.fhip_idx_split.argtypes = [C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int32), C.c_void_p,
+                                     C.c_void_p]
+        L.fhip_idx_chunk_first_page.argtypes = [C.c_int, C.c_int]
+        L.fhip_idx_chunk_first_page.restype = C.c_int32
+        L.fhip_idx_q_vectors.argtypes = [C.c_int] * 6 + [C.c_void_p, C.c_void_p]
+        L.fhip_idx_partial_row.argtypes = [C.c_int] * 7
+        L.fhip_idx_partial_row.restype = C.c_int64
+        L.fhip_idx_lane_tables.argtypes = [C.c_int, C.c_int] + [C.c_void_p] * 6
+        self._tables = {}
+
+    def lane_tables(self, kvh, g):
+        key = (kvh, g)
+        if key not in self._tables:
+            k_off = np.zeros((4, 64), np.uint32)
+            k_page = np.zeros(64, np.int32)
+            v_off = np.zeros(64, np.uint32)
+            n_off = np.zeros(64, np.uint32)
+            n_page = np.zeros(64, np.int32)
+            q_off = np.zeros((8, 64), np.int32)
+            assert self.lib.fhip_idx_lane_tables(kvh, g, *(a.ctypes.data for a in (
+                k_off, k_page, v_off, n_off, n_page, q_off))) == 0
+            self._tables[key] = (k_off.astype(np.int64), k_page, v_off.astype(np.int64),
+                                 n_off.astype(np.int64), n_page, q_off)
+        return self._tables[key]
+
+    def wg_item(self, wg, kvh):
+        item, g = self.C.c_int64(), self.C.c_int32()
+        assert self.lib.fhip_idx_wg_item(wg, kvh, self.C.byref(item), self.C.byref(g)) == 0
+        return item.value, g.value
+
+    def split(self, blk, wave, t_end):
+        t_begin = self.C.c_int32()
+        col = np.zeros(64, np.int32)
+        ins = np.zeros(64, np.uint8)
+        assert self.lib.fhip_idx_split(blk, wave, t_end, self.C.byref(t_begin), col.ctypes.data,
+                                       ins.ctypes.data) == 0
+        return t_begin.value, col, ins.astype(bool)
+
+    def q_vectors(self, tq0, tok, G, nq, qh, g):
+        vec = np.zeros(64, np.int64)
+        live = np.zeros(64, np.uint8)
+        assert self.lib.fhip_idx_q_vectors(tq0, tok, G, nq, qh, g, vec.ctypes.data,
+                                           live.ctypes.data) == 0
+        return vec, live.astype(bool)
+
+
+_IDX = None
+
+
+def index_lib():
+    global _IDX
+    if _IDX is None:
+        _IDX = IndexLib()
+    return _IDX
+
+
 def model_mfma_kernel(lens, table, num_pages, qh, kvh, page_bytes, pool_bytes, tok=1):
-    """Every access of tq_attn_mfma_kernel<PoolPages> for one launch (hd 128, K4/V4). With
-    tok > 1, `table` has one row that every query reads (causal prefill)."""
+    """Every access of tq_attn_mfma_kernel<PoolPages> for one launch (hd 128, K4/V4), from the
+    kernel's own index functions. With tok > 1, `table` has one row that every query reads
+    (causal prefill). Walks every workgroup of the launcher's grid."""
+    ix = index_lib()
     hd, pd = 128, 64
     B = len(lens)
     rows, max_blocks = table.shape
@@ -77,67 +149,63 @@ def model_mfma_kernel(lens, table, num_pages, qh, kvh, page_bytes, pool_bytes, t
     bnd = Bounds({"table": table.size * 4, "kp": pool_bytes["kp"], "kn": pool_bytes["kn"],
                   "vp": pool_bytes["vp"], "vn": pool_bytes["vn"], "qrot": B * qh * hd * 4,
                   "part_ml": ml_bytes, "part_acc": acc_bytes})
-    lane = np.arange(64)
-    n, rg = lane & 15, lane >> 4
-    for tq0 in range(0, B, tok):
+    items = (B + tok - 1) // tok
+    wgs = (items * nsplit + 7) // 8 * 8 * kvh  # launch_mfma_split's grid
+    seen = set()
+    for wg in range(wgs):
+        item, g = ix.wg_item(wg, kvh)
+        assert 0 <= g < kvh and (item, g) not in seen, "workgroup index map is not one-to-one"
+        seen.add((item, g))
+        tq0, blk = (item // nsplit) * tok, item % nsplit
+        if tq0 >= B:
+            continue  # padding workgroup: leaves at once
         tq_last = min(tq0 + tok, B) - 1
         clen = causal_len(lens[tq_last], max_blocks)
-        for blk in range(nsplit):
-            if blk * SPLIT >= clen:
-                continue  # the workgroup leaves before building its tables
-            for g in range(kvh):
-                for w in range(SPLIT // WAVE_SPLIT):
-                    t_begin = (4 * blk + w) * WAVE_SPLIT
-                    if t_begin >= clen:
-                        continue  # empty state, nothing read
-                    t_end = min(clen, t_begin + WAVE_SPLIT)
-                    has = t_begin + PAGE * lane < t_end
-                    tidx = t_begin // PAGE + lane[has]
-                    assert tidx.max() < max_blocks
-                    bnd.check("table", (tq0 * stride + tidx) * 4, 4)
-                    ids = np.full(64, -1, np.int64)
-                    ids[has] = table.reshape(-1)[tq0 * stride + tidx]
-                    ok = has & (ids >= 0) & (ids < num_pages)
-                    if not ok.any():
-                        continue
-                    entry = np.where(ok, ids, ids[np.flatnonzero(ok)[0]])[:WAVE_SPLIT // PAGE]
-                    assert ((entry >= 0) & (entry < num_pages)).all()
-                    for t0 in range(t_begin, t_end, CHUNK):
-                        j0 = (t0 - t_begin) // PAGE
-                        assert j0 + 3 < len(entry), "page entry index past the wave's table"
-                        # load_k: lane (n, rg), entry j0 + n / 4, tiles pt = 0..3
-                        e = entry[j0 + (n >> 2)]
-                        for pt in range(4):
-                            row = 4 * (n & 3) + pt
-                            inpage = (row * kvh + g) * pd + 16 * rg
-                            assert inpage.max() + 16 <= min(PAGE * kvh * pd, page_bytes["kp"])
-                            bnd.check("kp", e * page_bytes["kp"] + inpage, 16)
-                        # dma_v: copy i = entry j0 + i, lane L position 16 i + L / 4
-                        for i in range(4):
-                            inpage = ((lane >> 2) * kvh + g) * pd + 16 * ((lane & 3) ^ ((lane >> 3) & 3))
-                            assert inpage.max() + 16 <= min(PAGE * kvh * pd, page_bytes["vp"])
-                            bnd.check("vp", entry[j0 + i] * page_bytes["vp"] + inpage, 16)
-                        # load_norms: lane -> entry j0 + lane / 16, row lane % 16
-                        e = entry[j0 + (lane >> 4)]
-                        row = (lane & 15) * kvh + g
-                        for nm in ("kn", "vn"):
-                            assert (2 * row + 2).max() <= min(PAGE * kvh * 2, page_bytes[nm])
-                            bnd.check(nm, e * page_bytes[nm] + 2 * row, 2)
-                    # Q: column h = G ct + ch; columns past the group read its first vector
-                    h = n & 7
-                    ct, ch = h // G, h % G
-                    col_ok = (h < tok * G) & (tq0 + ct < B)
-                    qsrc = np.where(col_ok, tq0 + ct, tq0) * qh + g * G + np.where(col_ok, ch, 0)
-                    for s8 in range(8):
-                        bnd.check("qrot", (qsrc * hd + 32 * rg + 4 * s8) * 4, 16)
-                # the workgroup's merge: one partial per live column (query, head) of the group
-                for h in range(tok * G):
-                    ht = h // G
-                    if tq0 + ht >= B:
-                        continue
-                    vec = (tq0 + ht) * qh + g * G + (h - ht * G)
-                    bnd.check("part_ml", ((vec * nsplit + blk) * 2) * 4, 8)
-                    bnd.check("part_acc", ((vec * nsplit + blk) * hd + np.arange(hd)) * 4, 4)
+        if blk * SPLIT >= clen:
+            continue  # the workgroup leaves before building its tables
+        k_off, k_page, v_off, n_off, n_page, q_off = ix.lane_tables(kvh, g)
+        for k in range(4):
+            assert (k_off[k] + 16 <= PAGE * kvh * pd).all() and (k_off[k] + 16 <= page_bytes["kp"]).all()
+        assert (v_off + 16 <= min(PAGE * kvh * pd, page_bytes["vp"])).all()
+        for nm in ("kn", "vn"):
+            assert (n_off + 2 <= min(PAGE * kvh * 2, page_bytes[nm])).all()
+        for w in range(SPLIT // WAVE_SPLIT):
+            t_begin, col, has = ix.split(blk, w, SPLIT * nsplit)
+            if t_begin >= clen:
+                continue  # empty state, nothing read
+            t_end = min(clen, t_begin + WAVE_SPLIT)
+            _, col, has = ix.split(blk, w, t_end)
+            tidx = col[has]
+            assert tidx.max() < max_blocks
+            bnd.check("table", (tq0 * stride + tidx) * 4, 4)
+            ids = np.full(64, -1, np.int64)
+            ids[has] = table.reshape(-1)[tq0 * stride + tidx]
+            ok = has & (ids >= 0) & (ids < num_pages)
+            if not ok.any():
+                continue
+            entry = np.where(ok, ids, ids[np.flatnonzero(ok)[0]])[:WAVE_SPLIT // PAGE]
+            assert ((entry >= 0) & (entry < num_pages)).all()
+            for t0 in range(t_begin, t_end, CHUNK):
+                j0 = ix.lib.fhip_idx_chunk_first_page(t0, t_begin)
+                assert j0 + 3 < len(entry), "page entry index past the wave's table"
+                for pt in range(4):  # K codes
+                    bnd.check("kp", entry[j0 + k_page] * page_bytes["kp"] + k_off[pt], 16)
+                for i in range(4):  # V copies: copy i reads entry j0 + i
+                    bnd.check("vp", entry[j0 + i] * page_bytes["vp"] + v_off, 16)
+                for nm in ("kn", "vn"):  # norms
+                    bnd.check(nm, entry[j0 + n_page] * page_bytes[nm] + n_off, 2)
+            vec, live = ix.q_vectors(tq0, tok, G, B, qh, g)
+            assert (vec >= 0).all() and (vec < B * qh).all()
+            for s8 in range(8):
+                bnd.check("qrot", (vec * hd + q_off[s8]) * 4, 16)
+        # the workgroup's merge: one partial per live column (query, head) of the group
+        for h in range(tok * G):
+            if tq0 + h // G >= B:
+                continue
+            prow = ix.lib.fhip_idx_partial_row(h, tq0, G, qh, g, nsplit, blk)
+            bnd.check("part_ml", prow * 2 * 4, 8)
+            bnd.check("part_acc", (prow * hd + np.arange(hd)) * 4, 4)
+    assert len(seen) == wgs
     return bnd, nsplit
 
 
