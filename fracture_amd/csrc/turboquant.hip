@@ -11,7 +11,9 @@
 //               an fp16 operand; the norm is applied after the product by linearity:
 //               y = y_raw / (||x|| + 1e-8).
 //   dequantize: x_hat = Pi^T yhat = Pi_hi^T c_hi + 2^-12 (Pi_lo'^T c_hi + Pi_hi^T c_lo')
-// Each representation error is ~2^-22 relative, the level of the fp32 sums themselves.
+// In compress each representation error is ~2^-22 relative, the level of the fp32 sums
+// themselves. The dequantize runs its two correction products on fp8 MFMA (see there): ~2^-15
+// of each term, under the fp16 output's own rounding.
 //
 // Work mapping (head_dim 128, 2/3/4/8 bits): one workgroup of 8 (compress) or 12
 // (dequantize) waves per CU holds the rotation's hi/lo MFMA fragments in LDS (64 KB, staged
@@ -1074,8 +1076,8 @@ __device__ __forceinline__ void dequant_tile(const DequantLds& t, const DeqLds& 
 // ---------------------------------------------------------------------------------------
 // x = Pi^T y for fp32 rows y [rows, 128] -> fp16 (the attention combine's unrotation of the
 // merged outputs, attention_paged_tq.cu:245-257, for batches of many vectors): each lane's
-// 64 values of its row split into fp16 (hi, lo') operands as the dequantize tables split the
-// centroids (y = hi + 2^-12 lo'), then the dequantize kernel's three products per step.
+// 64 values of its row split into fp16 (hi, lo') operands (y = hi + 2^-12 lo'), then three
+// fp16 products per step (rotate_back_store), fp32-accurate.
 // ---------------------------------------------------------------------------------------
 struct RowHalf {
     f32x4 v[16];  // coordinates 64 h + 4 i .. + 3 of the lane's row
