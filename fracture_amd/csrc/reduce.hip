@@ -9,7 +9,7 @@
 // Pass 1 (row_stats_kernel) reduces each chunk to a record {max, sum exp(x - max), argmax,
 // flags}. argmax then folds each row's records with one wave per row (argmax_fold_kernel);
 // softmax reads the logits again in softmax_write_kernel (each XCD in the reverse of pass 1's
-// order, so that its first re-reads hit its L2 and the rest mostly the MALL), where
+// order, which measured faster), where
 // every workgroup of a row folds the row's records in the same fixed order (so all agree on
 // the row's max and sum) while its logits loads are in flight, and writes exp(x/T - M) / S.
 // No atomics or cross-workgroup fences: a device-scope fence on gfx9 writes back the L2.
@@ -259,9 +259,9 @@ __global__ __launch_bounds__(kBlock) void softmax_write_kernel(
     uint32_t* __restrict__ flags_out) {
     __shared__ float sMS[2];
     // Pass 1 ran workgroup w (w = chunk + nchunks row) on XCD w % 8, in order of w. Here each
-    // XCD takes the same chunks in the reverse order, so its first re-reads find the lines
-    // pass 1 read last still in its L2 (an XCD's share of [64, 128256] fp32 logits, ~4.1 MB, is
-    // about its L2's 4 MB): 15.6 -> 13.6 us at that shape.
+    // XCD takes the same chunks in the reverse order, so its re-reads start with the lines pass
+    // 1 read last. Measured at [64, 128256] fp32: 15.6 -> 13.6 us, with the same L2 miss bytes
+    // (FETCH_SIZE), so the gain is in how fast the misses are served, not in L2 hits.
     const int nchunks = gridDim.x;
     const int w = blockIdx.x + blockIdx.y * nchunks, nw = nchunks * gridDim.y;
     const int pw = nw % 8 == 0 ? (nw / 8 - 1 - w / 8) * 8 + w % 8 : w;
