@@ -697,7 +697,8 @@ __global__ __launch_bounds__(256) void tq_quantize_pack_kernel(const float* __re
 // of it, run on fp8 E4M3 MFMA (v_mfma_scale_f32_32x32x64_f8f6f4: 64 coordinates per
 // instruction at twice the fp16 rate), which cuts the kernel's MFMA time by a third. Their
 // operands are prescaled by powers of two into fp8's normal range when the tables are built
-// (f8_prescale) and the instruction's E8M0 operand scales undo that exactly. fp8 rounds a
+// (f8_prescale); the instruction's E8M0 operand scales undo that exactly and apply the 2^-12,
+// so the corrections accumulate straight into the main product's fp32 sum. fp8 rounds a
 // correction term to 2^-4 of itself: ~2^-15 of the term |Pi||c|, against 2^-11 (half an
 // fp16 ulp) for the stored output.
 // fp8 operand u (0, 1) of lane (i or r, h) is 8 registers: byte b is coordinate 64h + 32u + b.
@@ -714,8 +715,10 @@ __device__ inline int f8_prescale(float maxabs) {
     (void)frexpf(maxabs, &e);  // maxabs = f 2^e, f in [0.5, 1)
     return min(max(8 - e, -120), 120);
 }
-// The instruction's E8M0 scale that undoes a prescale by 2^p: 2^(scale - 127) = 2^-p.
-__device__ __forceinline__ int f8_scale(int p) { return 127 - p; }
+// The instruction's E8M0 scale that undoes a prescale by 2^p and applies 2^-6, half of the
+// corrections' 2^-12 (each product's two operand scales multiply): 2^(scale - 127) = 2^(-p-6).
+// With p in [-120, 120] (f8_prescale) the scale stays in [1, 241].
+__device__ __forceinline__ int f8_scale(int p) { return 127 - p - 6; }
 // fp8 E4M3 bytes of 2^p a and 2^p b (v_cvt_pk_fp8_f32, round to nearest even), in the low
 // (kHi = false) or high half of old.
 template <bool kHi>
@@ -984,19 +987,15 @@ __device__ __forceinline__ void decode_group(const DequantLds& t, const CodeHalf
 // Lane (r, h) ends block c holding coordinates 32c + 8g + 4h + e of row r; neighbouring
 // chunks are exchanged with the partner lane so every lane stores 16 contiguous bytes.
 // ---------------------------------------------------------------------------------------
-// Block c of the lane's row: fp16((acc1 + 2^-12 acc2) * nrm) to orow[32c .. 32c + 31].
-__device__ __forceinline__ void store_block(const f32x16& acc1, const f32x16& acc2, float nrm,
+// Block c of the lane's row: fp16(acc * nrm) to orow[32c .. 32c + 31].
+__device__ __forceinline__ void store_block(const f32x16& acc, float nrm,
                                             uint16_t* __restrict__ orow, int c, bool row_ok) {
     uint32_t ch[4][2];  // chunk g: coordinates 32c + 8g + 4h + 0..3 as fp16 pairs
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
+    for (int g = 0; g < 4; ++g)
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const float x0 = fmaf(acc2[4 * g + 2 * e], kLoInv, acc1[4 * g + 2 * e]) * nrm;
-            const float x1 = fmaf(acc2[4 * g + 2 * e + 1], kLoInv, acc1[4 * g + 2 * e + 1]) * nrm;
-            ch[g][e] = f2h(x0) | (f2h(x1) << 16);
-        }
-    }
+        for (int e = 0; e < 2; ++e)
+            ch[g][e] = f2h(acc[4 * g + 2 * e] * nrm) | (f2h(acc[4 * g + 2 * e + 1] * nrm) << 16);
     // chunks (2m, 2m+1): lane h = 0 takes coordinates 16m + 0..7, lane h = 1 16m + 8..15
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
@@ -1027,7 +1026,10 @@ __device__ __forceinline__ void rotate_back_store(const RotLds& L, const f16x8 (
             acc2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh[s], acc2, 0, 0, 0);
             acc2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bl[s], acc2, 0, 0, 0);
         }
-        store_block(acc1, acc2, nrm, orow, c, r < nvalid);
+        f32x16 x;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) x[v] = fmaf(acc2[v], kLoInv, acc1[v]);
+        store_block(x, nrm, orow, c, r < nvalid);
     }
 }
 
@@ -1053,23 +1055,23 @@ __device__ __forceinline__ void dequant_tile(const DequantLds& t, const DeqLds& 
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         __builtin_amdgcn_sched_barrier(0);  // keep each block's fragment loads within it
-        f32x16 acc1 = {}, acc2 = {};
+        f32x16 acc = {};
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             const f16x8 ah = __builtin_bit_cast(f16x8, L.hi[c][s][lane]);
-            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, ops.bh[s], acc1, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, ops.bh[s], acc, 0, 0, 0);
             if (s & 1) {  // one correction product every second step: (u, t) = (s / 4, s / 2 % 2)
                 const int u = s >> 2, tt = (s >> 1) & 1;
                 const i32x8 a8 = deq_a8(L, c, u, tt, lane);
                 if (tt == 0)  // Pi_lo' c_hi
-                    acc2 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                        a8, ops.b8[u][0], acc2, 0, 0, 0, sa_lo, 0, sb_hi);
+                    acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                        a8, ops.b8[u][0], acc, 0, 0, 0, sa_lo, 0, sb_hi);
                 else  // Pi_hi c_lo'
-                    acc2 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                        a8, ops.b8[u][1], acc2, 0, 0, 0, sa_hi, 0, sb_lo);
+                    acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                        a8, ops.b8[u][1], acc, 0, 0, 0, sa_hi, 0, sb_lo);
             }
         }
-        store_block(acc1, acc2, nrm, orow, c, r < nvalid);
+        store_block(acc, nrm, orow, c, r < nvalid);
     }
 }
 
