@@ -1052,27 +1052,45 @@ __device__ __forceinline__ void dequant_tile(const DequantLds& t, const DeqLds& 
     const int sb_hi = t.scale[kScaleBHi], sb_lo = t.scale[kScaleBLo];
     const float nrm = h2f(cw.norm);
     uint16_t* orow = out + m0 * kHd + (r * kHd + 8 * h);
+    // The 32 fp16 steps (block c = q / 8, step s = q % 8) run as one software pipeline: the
+    // fp16 fragment of step q + 2 and the fp8 operand of the next odd step are read while step q
+    // computes, and blocks alternate between two accumulators, so a block's stores overlap the
+    // next block's products.
+    constexpr int kAhead = 2;
+    f16x8 fh[kAhead + 1];
+    i32x8 f8r[2];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        __builtin_amdgcn_sched_barrier(0);  // keep each block's fragment loads within it
-        f32x16 acc = {};
+    for (int q = 0; q < kAhead; ++q) fh[q] = __builtin_bit_cast(f16x8, L.hi[q >> 3][q & 7][lane]);
+    f8r[0] = deq_a8(L, 0, 0, 0, lane);
+    f32x16 acc[2];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const f16x8 ah = __builtin_bit_cast(f16x8, L.hi[c][s][lane]);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, ops.bh[s], acc, 0, 0, 0);
-            if (s & 1) {  // one correction product every second step: (u, t) = (s / 4, s / 2 % 2)
-                const int u = s >> 2, tt = (s >> 1) & 1;
-                const i32x8 a8 = deq_a8(L, c, u, tt, lane);
-                if (tt == 0)  // Pi_lo' c_hi
-                    acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                        a8, ops.b8[u][0], acc, 0, 0, 0, sa_lo, 0, sb_hi);
-                else  // Pi_hi c_lo'
-                    acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                        a8, ops.b8[u][1], acc, 0, 0, 0, sa_hi, 0, sb_lo);
-            }
+    for (int q = 0; q < 32; ++q) {
+        const int c = q >> 3, s = q & 7, b = c & 1;
+        __builtin_amdgcn_sched_barrier(0);
+        if (q + kAhead < 32) {
+            const int n = q + kAhead;
+            fh[n % (kAhead + 1)] = __builtin_bit_cast(f16x8, L.hi[n >> 3][n & 7][lane]);
         }
-        store_block(acc, nrm, orow, c, r < nvalid);
+        if ((q & 1) == 0 && (q >> 1) + 1 < 16) {  // fp8 operand j = q / 2 + 1 (odd step q + 1)
+            const int j = (q >> 1) + 1;
+            f8r[j & 1] = deq_a8(L, j >> 2, (j >> 1) & 1, j & 1, lane);
+        }
+        if (s == 0) acc[b] = f32x16{};
+        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fh[q % (kAhead + 1)], ops.bh[s], acc[b], 0, 0, 0);
+        if (q & 1) {  // fp8 operand j = q / 2: block c, operand u = s / 4, part tt = s / 2 % 2
+            const int j = q >> 1, u = s >> 2, tt = (s >> 1) & 1;
+            if (tt == 0)  // Pi_lo' c_hi
+                acc[b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                    f8r[j & 1], ops.b8[u][0], acc[b], 0, 0, 0, sa_lo, 0, sb_hi);
+            else  // Pi_hi c_lo'
+                acc[b] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                    f8r[j & 1], ops.b8[u][1], acc[b], 0, 0, 0, sa_hi, 0, sb_lo);
+        }
+        // block c - 1's stores, two steps into block c (its last product has finished)
+        if (c > 0 && s == 2) store_block(acc[b ^ 1], nrm, orow, c - 1, r < nvalid);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    store_block(acc[1], nrm, orow, 3, r < nvalid);
 }
 
 // ---------------------------------------------------------------------------------------
