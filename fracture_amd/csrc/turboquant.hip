@@ -404,16 +404,34 @@ __device__ __forceinline__ void compress_tile(const Quantizer& qz, const RotLds&
     if constexpr (kMode == 0) {
         // Group j (< 8) and group j + 8: lane h = 0 gets both halves of group j, lane h = 1
         // both halves of group j + 8, as (first half, second half) in (half[j], half[j+8]).
-        uint32_t w[16] = {};
+        uint32_t w[16] = {}, G[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             uint32_t v = half[j], u = half[j + 8];
             swap_halves(v, u);
-            const uint64_t G = ((uint64_t)v << (4 * kBits)) | u;  // 8*kBits bits, MSB first
+            if constexpr (kBits == 4) {
+                // the group's 4 bytes are v's two then u's two, most significant first
+                w[j] = __builtin_amdgcn_perm(v, u, 0x00010405u);
+            } else if constexpr (kBits == 8) {
+                w[2 * j] = __builtin_amdgcn_perm(v, v, 0x00010203u);
+                w[2 * j + 1] = __builtin_amdgcn_perm(u, u, 0x00010203u);
+            } else {
+                G[j] = (v << (4 * kBits)) | u;  // 8*kBits bits, MSB first
+            }
+        }
+        if constexpr (kBits == 2 || kBits == 3) {
+            // output dword m holds bytes 4m..4m+3 of the stream of groups, each group j's
+            // kBits bytes most significant first: at most two groups per dword, one v_perm
 #pragma unroll
-            for (int k = 0; k < kBits; ++k) {
-                const int byte = j * kBits + k;
-                w[byte >> 2] |= (uint32_t)((G >> (8 * (kBits - 1 - k))) & 0xffu) << (8 * (byte & 3));
+            for (int m = 0; m < 2 * kBits; ++m) {
+                const int j0 = 4 * m / kBits, j1 = min(j0 + 1, 7);
+                uint32_t sel = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int b = 4 * m + i, j = b / kBits, k = b % kBits;
+                    sel |= (uint32_t)((j == j0 ? 4 : 0) + (kBits - 1 - k)) << (8 * i);
+                }
+                w[m] = __builtin_amdgcn_perm(G[j0], G[j1], sel);
             }
         }
         if (row_ok) {
