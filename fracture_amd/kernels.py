@@ -379,7 +379,8 @@ def attention_tq_decode(out: torch.Tensor, q: torch.Tensor, block_table: torch.T
     _need(q.dtype == torch.float16 and q.dim() == 3 and out.shape == q.shape, "q/out")
     B, qh, hd = q.shape
     _need(block_table.dtype == torch.int32 and block_table.dim() == 2 and
-          block_table.shape[0] == B, "block_table")
+          block_table.shape[0] == B and block_table.shape[1] >= 1,
+          "block_table [B, max_blocks >= 1]")
     _need(seq_lens.dtype == torch.int32 and seq_lens.numel() == B, "seq_lens")
     mb = block_table.shape[1]
     P = kp.shape[0]
@@ -414,7 +415,8 @@ def attention_paged_decode(out: torch.Tensor, q: torch.Tensor, block_table: torc
           out.dtype == torch.float16, "q/out")
     B, qh, hd = q.shape
     _need(block_table.dtype == torch.int32 and block_table.dim() == 2 and
-          block_table.shape[0] == B and block_table.is_contiguous(), "block_table")
+          block_table.shape[0] == B and block_table.is_contiguous() and
+          block_table.shape[1] >= 1, "block_table [B, max_blocks >= 1]")
     _need(seq_lens.dtype == torch.int32 and seq_lens.numel() == B, "seq_lens")
     mb = block_table.shape[1]
     P = k_pool.shape[0]

@@ -329,8 +329,10 @@ int fhip_launch_tq_dequant_kv_planned(const fhip_tq_plan* kplan, const fhip_tq_p
  * q [B, qh, hd] fp16, block_table [B, max_blocks] int32 (physical page ids), seq_lens [B]
  * int32; pages in contiguous pools (strides in bytes between pages, each at least one page:
  * 16 * kvh * packed_dim or 16 * kvh * 2 bytes); positions whose page id is outside
- * [0, num_pages) are masked out. max_blocks * 16 is at most 1,048,576. Output [B, qh, hd]
- * fp16; centroid tables hold 2^bits entries.
+ * [0, num_pages) are masked out. max_blocks is at least 1 (a zero-width table, a batch of
+ * empty sequences only, is refused with hipErrorInvalidValue) and max_blocks * 16 at most
+ * 1,048,576. Output [B, qh, hd] fp16 (zeros for an empty sequence); centroid tables hold
+ * 2^bits entries.
  * The workspace holds split-K partials; size it with fhip_attention_tq_workspace_bytes. */
 size_t fhip_attention_tq_workspace_bytes(int batch, int num_q_heads, int head_dim,
                                          int max_blocks);
@@ -362,7 +364,8 @@ int fhip_launch_attention_tq_decode_ptrs(void* output, const void* q, const int3
 /* Batched decode attention over an FP16 page pool (the FP16 form of the call above, for
  * batched decode): q [B, qh, hd] fp16, block_table [B, max_blocks] int32, seq_lens [B] int32;
  * page p of K at k_pool + p * page_k_bytes holds [16, kvh, hd] fp16, likewise V; positions
- * whose page id is outside [0, num_pages) are masked out. Output [B, qh, hd] fp16.
+ * whose page id is outside [0, num_pages) are masked out; max_blocks is at least 1, as above.
+ * Output [B, qh, hd] fp16.
  * The workspace holds split partials; size it with fhip_attention_paged_workspace_bytes. */
 size_t fhip_attention_paged_workspace_bytes(int batch, int num_q_heads, int head_dim,
                                             int max_blocks);
@@ -514,7 +517,7 @@ int fhip_tq_append_kv(fhip_backend* b, uint64_t pool, const fhip_tensor* keys,
  * sequence i attends seq_lens[i] positions through row i of block_tables (host,
  * [num_seqs, max_blocks]); seq_lens holds num_seqs entries; out [B, qh, hd] fp16. num_seqs
  * must equal B (q's first dimension): the host arrays are read only up to it. max_blocks is
- * at most 65536. */
+ * between 1 and 65536. */
 int fhip_attention_paged_tq_batched(fhip_backend* b, const fhip_tensor* q,
                                     const int32_t* block_tables, size_t num_seqs,
                                     size_t max_blocks, const uint32_t* seq_lens, uint64_t pool,

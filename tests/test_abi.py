@@ -126,6 +126,14 @@ def test_raw_launchers_reject_bad_arguments_on_host():
                                            None) == 0  # no tokens: nothing to do
     assert lib.fhip_launch_attention_paged_decode(1, 1, 1, 1, 1, 1 << 17, 1, 1, 1, 1, 1, 8, 2, 128,
                                                   1, None) == 1  # 2M positions > the 1M bound
+    # batched decode: a block table of zero width (a batch of empty sequences only) is refused
+    i64 = ctypes.c_int64
+    assert lib.fhip_launch_attention_paged_decode(1, 1, 1, 1, 2, 0, 1, 1, 1, i64(1), i64(1), 8, 2,
+                                                  128, 1, None) == 1
+    assert lib.fhip_launch_attention_tq_decode(1, 1, 1, 1, 2, 0, 4, 1, 1, 1, 1, i64(4096), i64(256),
+                                               i64(4096), i64(256), 1, 1, 1, 1, 8, 2, 128, 4, 4, 1,
+                                               None) == 1
+    assert lib.fhip_attention_tq_workspace_bytes(2, 8, 128, 0) == 0
     # split partials: (m, l) and hd floats per (query, head, 1024-position split), 256-aligned
     ml = 4 * 32 * 32 * 2 * 4
     assert lib.fhip_attention_paged_workspace_bytes(4, 32, 128, 2048) == ml + 4 * 32 * 32 * 128 * 4
