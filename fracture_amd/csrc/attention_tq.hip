@@ -532,7 +532,8 @@ __global__ __launch_bounds__(256) void tq_attn_combine_kernel(
 // ---------------------------------------------------------------------------------------
 // 2'. MFMA split kernel: head_dim 128, 4-bit K and V codes, G <= 8 query heads per kv head.
 //
-// One wave per (query, kv head, 1024-position split) walks 64-position chunks:
+// A workgroup owns one (query, kv head, 1024-position block); each of its two waves walks
+// one 512-position split of it in 64-position chunks:
 //   QK  D[pos][col] = sum_k A[pos][k] B[k][col] on v_mfma_f32_16x16x32_f16. The K slots come
 //       in (hi, lo') pairs per coordinate: A = (c_hi, c_lo*2^12) of the position's centroid,
 //       B = (q_hi, 0) in column h and (q_lo*2^12, q_hi) in column 8+h, so one MFMA gives
@@ -551,10 +552,10 @@ __global__ __launch_bounds__(256) void tq_attn_combine_kernel(
 // Online softmax per head (lanes n = h), lazily rescaling the accumulators.
 // ---------------------------------------------------------------------------------------
 constexpr int kChunkM = 64;     // positions per chunk
-constexpr int kSplitMfma = 256;  // positions per wave item (split)
+constexpr int kSplitMfma = 512;  // positions per wave item (split)
 constexpr int kXcds = 8;         // MI355X: accelerator complex dies, each with its own L2
 constexpr int kSplitPages = kSplitMfma / FHIP_PAGE_TOKENS;
-constexpr int kWavesM = 4;      // waves per workgroup (independent work items)
+constexpr int kWavesM = 2;      // waves per workgroup (independent work items)
 static_assert(kChunkM == fhip_idx::kChunk && kSplitMfma == fhip_idx::kSplitPositions &&
                   kWavesM == fhip_idx::kBlockWaves && kXcds == fhip_idx::kXcdCount &&
                   FHIP_PAGE_TOKENS == fhip_idx::kPageTokens,
@@ -830,7 +831,6 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, rg = lane >> 4;  // MFMA column / row group
-    static_assert(64 * kWavesM == 256, "one table byte per thread");
     static_assert(kWavesM * kSplitMfma == kSplit, "a workgroup's splits make one partial's block");
 
     // Workgroup (query, kv head, block of kWavesM consecutive splits); wave w takes split
@@ -852,8 +852,7 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     const int blk = (int)(item % nblk);
     const int clen = qs.causal_len(tq_last);  // the group's longest causal length
     if (blk * kSplit >= clen) return;
-    {
-        const int b = threadIdx.x;
+    for (int b = threadIdx.x; b < 256; b += 64 * kWavesM) {
         float hf;
         const uint32_t kh = hi_lo_pair(kcent[b >> 4], hf), kl = hi_lo_pair(kcent[b & 15], hf);
         const uint32_t vh = hi_lo_pair(vcent[b >> 4], hf), vl = hi_lo_pair(vcent[b & 15], hf);

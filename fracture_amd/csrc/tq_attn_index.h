@@ -18,8 +18,8 @@ namespace fhip_idx {
 constexpr int kPageTokens = 16;      // positions per page
 constexpr int kCodeRow = 64;         // bytes of one position's 4-bit codes for one kv head
 constexpr int kChunk = 64;           // positions per chunk of a wave's loop
-constexpr int kSplitPositions = 256; // positions per wave (one split)
-constexpr int kBlockWaves = 4;       // waves per workgroup: one 1024-position block
+constexpr int kSplitPositions = 512; // positions per wave (one split)
+constexpr int kBlockWaves = 2;       // waves per workgroup: one 1024-position block
 constexpr int kXcdCount = 8;         // MI355X: workgroup b runs on XCD b % 8
 
 // Workgroup wg -> (item, kv head g). An item is a (query group, block); the 8 kv heads of one
@@ -40,7 +40,7 @@ FHIP_IDX bool split_page_column(int t_begin, int t_end, int lane, int& column) {
     return t_begin + kPageTokens * lane < t_end;
 }
 
-// The split page (0..15) holding the first position of the chunk starting at t0.
+// The split page (0..31) holding the first position of the chunk starting at t0.
 FHIP_IDX int chunk_first_page(int t0, int t_begin) { return (t0 - t_begin) / kPageTokens; }
 
 // K codes of a chunk: lane (n = lane & 15, rg = lane >> 4) reads split page

@@ -4,7 +4,7 @@ against the buffers the launcher hands them.
 
 The MFMA kernel's addresses come from its own index functions (fracture_amd/csrc/
 tq_attn_index.h), called through their host build (libfracture_hip_index.so), for every
-workgroup of the launch grid, every wave (one 256-position split of the workgroup's
+workgroup of the launch grid, every wave (one 512-position split of the workgroup's
 1024-position block) and every 64-position chunk, with numpy over the 64 lanes. What they
 compute:
 
@@ -33,7 +33,7 @@ import pytest
 PAGE = 16
 CHUNK = 64
 SPLIT = 1024       # positions per partial (the MFMA kernel's workgroup block, the VALU kernel's split)
-WAVE_SPLIT = 256   # positions per MFMA wave
+WAVE_SPLIT = 512   # positions per MFMA wave
 
 
 def ws_layout(nq, qh, hd, max_tokens):
