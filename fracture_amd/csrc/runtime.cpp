@@ -128,8 +128,9 @@ struct StageSlot {
     void* host = nullptr;
     void* dev = nullptr;
     size_t cap = 0;
-    hipEvent_t ev = nullptr;
+    hipEvent_t ev = nullptr;  // recorded on the group's last slot only
     bool pending = false;
+    bool dirty = false;       // handed out since its group's event was last recorded
 };
 
 // Device memory for small tensors. Tensors of at most kMaxBytes are carved out of large
@@ -240,6 +241,8 @@ struct fhip_backend {
     // launch lock: staging ring and workspace are per backend
     std::mutex launch_mu;
     static constexpr int kSlots = 16;
+    static constexpr int kGroup = 4;  // slots guarded by one event
+    static_assert(kSlots % kGroup == 0 && (kGroup & (kGroup - 1)) == 0, "slot groups");
     StageSlot slots[kSlots];
     // side stream for staging copies that may run ahead of `stream` (default priority)
     hipStream_t copy_stream = nullptr;
@@ -326,17 +329,28 @@ struct fhip_backend {
         return FHIP_OK;
     }
 
-    // Copy `bytes` of host data to a device staging slot; returns the slot index. Callers
-    // hold launch_mu and call stage_done(slot) after enqueuing the consumer kernel.
     // The next slot, free (its last reader has completed) and at least `bytes` large.
+    // Slots are handed out in ring order and guarded in groups of kGroup: stage_done of a
+    // group's last slot records one event after that call's kernels, which follow the
+    // kernels of the group's other slots in stream order. An event is a queue packet between
+    // two calls' kernels, so one per kGroup calls costs the compute queue less idle time than
+    // one per call. A slot handed out again without its group's event recorded since (a call
+    // that returned an error before stage_done) waits for both streams instead.
     int next_free_slot(size_t bytes, int* slot_out) {
         const int si = next_slot;
         next_slot = (next_slot + 1) % kSlots;
         StageSlot& s = slots[si];
-        if (s.pending) {
-            HIP_TRY(hipEventSynchronize(s.ev));
-            s.pending = false;
+        StageSlot& last = slots[si | (kGroup - 1)];
+        if (last.pending) {
+            HIP_TRY(hipEventSynchronize(last.ev));
+            last.pending = false;
         }
+        if (s.dirty) {
+            HIP_TRY(hipStreamSynchronize(stream));
+            if (copy_stream) HIP_TRY(hipStreamSynchronize(copy_stream));
+            for (StageSlot& o : slots) o.dirty = o.pending = false;
+        }
+        s.dirty = true;
         if (!s.ev) HIP_TRY(hipEventCreateWithFlags(&s.ev, hipEventDisableTiming));
         if (bytes > s.cap) {
             if (s.host) HIP_TRY(hipHostFree(s.host));
@@ -368,11 +382,13 @@ struct fhip_backend {
         return FHIP_OK;
     }
     // A slot of at least `bytes` whose host side the caller fills (host_out), then
-    // stage_ahead_copy(slot, bytes): the copy runs on the backend's copy stream, so it can
-    // proceed while `stream` still runs earlier calls' kernels (a copy queued on `stream`
+    // stage_ahead_copy(slot, bytes): the copy runs on the backend's copy stream, so it
+    // proceeds while `stream` still runs earlier calls' kernels (a copy queued on `stream`
     // itself costs the copy plus two hand-offs between the copy engine and the compute queue
-    // in the call's own time), and `stream` waits for it. Callers hold launch_mu and call
-    // stage_done(slot) after enqueuing the last kernel that reads the slot.
+    // in the call's own time), and the host waits for it before the caller enqueues the
+    // kernels that read the slot: a cross-stream wait on `stream` would be one more packet
+    // between two calls' kernels. Callers hold launch_mu and call stage_done(slot) after
+    // enqueuing the last kernel that reads the slot.
     int stage_ahead_begin(size_t bytes, void** host_out, void** dev_out, int* slot_out) {
         int si;
         int r = next_free_slot(bytes, &si);
@@ -388,12 +404,14 @@ struct fhip_backend {
         HIP_TRY(hipMemcpyAsync(slots[si].dev, slots[si].host, bytes, hipMemcpyHostToDevice,
                                copy_stream));
         HIP_TRY(hipEventRecord(copy_ev[si], copy_stream));
-        HIP_TRY(hipStreamWaitEvent(stream, copy_ev[si], 0));
+        HIP_TRY(hipEventSynchronize(copy_ev[si]));
         return FHIP_OK;
     }
     int stage_done(int si) {
+        if ((si & (kGroup - 1)) != kGroup - 1) return FHIP_OK;
         HIP_TRY(hipEventRecord(slots[si].ev, stream));
         slots[si].pending = true;
+        for (int i = si - (kGroup - 1); i <= si; ++i) slots[i].dirty = false;
         return FHIP_OK;
     }
     // Backend-owned scratch (softmax partials, attention split partials). Callers hold
