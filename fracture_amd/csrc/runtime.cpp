@@ -241,7 +241,9 @@ struct fhip_backend {
     // launch lock: staging ring and workspace are per backend
     std::mutex launch_mu;
     static constexpr int kSlots = 16;
-    static constexpr int kGroup = 4;  // slots guarded by one event
+    // slots guarded by one event: reusing a group's first slot waits for the call
+    // kSlots - kGroup + 1 calls back, so kSlots - kGroup calls stay queued on the GPU
+    static constexpr int kGroup = 8;
     static_assert(kSlots % kGroup == 0 && (kGroup & (kGroup - 1)) == 0, "slot groups");
     StageSlot slots[kSlots];
     // side stream for staging copies that may run ahead of `stream` (default priority)
