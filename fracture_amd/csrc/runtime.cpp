@@ -384,13 +384,14 @@ struct fhip_backend {
         return FHIP_OK;
     }
     // A slot of at least `bytes` whose host side the caller fills (host_out), then
-    // stage_ahead_copy(slot, bytes): the copy runs on the backend's copy stream, so it
+    // stage_ahead_copy(slot, bytes) issues its copy on the backend's copy stream, so it
     // proceeds while `stream` still runs earlier calls' kernels (a copy queued on `stream`
     // itself costs the copy plus two hand-offs between the copy engine and the compute queue
-    // in the call's own time), and the host waits for it before the caller enqueues the
-    // kernels that read the slot: a cross-stream wait on `stream` would be one more packet
-    // between two calls' kernels. Callers hold launch_mu and call stage_done(slot) after
-    // enqueuing the last kernel that reads the slot.
+    // in the call's own time), and stage_ahead_wait(slot) waits for it on the host before the
+    // caller enqueues the kernels that read the slot (host work can run in between): a
+    // cross-stream wait on `stream` would be one more packet between two calls' kernels.
+    // Callers hold launch_mu and call stage_done(slot) after enqueuing the last kernel that
+    // reads the slot.
     int stage_ahead_begin(size_t bytes, void** host_out, void** dev_out, int* slot_out) {
         int si;
         int r = next_free_slot(bytes, &si);
@@ -406,6 +407,9 @@ struct fhip_backend {
         HIP_TRY(hipMemcpyAsync(slots[si].dev, slots[si].host, bytes, hipMemcpyHostToDevice,
                                copy_stream));
         HIP_TRY(hipEventRecord(copy_ev[si], copy_stream));
+        return FHIP_OK;
+    }
+    int stage_ahead_wait(int si) {
         HIP_TRY(hipEventSynchronize(copy_ev[si]));
         return FHIP_OK;
     }
@@ -1866,16 +1870,27 @@ int fhip_attention_paged_tq_batched(fhip_backend* b, const fhip_tensor* q,
     PoolView pp;
     int r = find_pool(b, pool, 4, needs, dts, &pp);
     if (r) return r;
+    // Errors are reported in row order: the first sequence whose length or one of whose block
+    // ids is out of range. id_error(n) scans the ids of sequences [0, n) for the first bad one
+    // (the error path only: on the way to a launch the ids are checked once staged, below).
+    auto id_error = [&](uint64_t n) -> int {
+        for (uint64_t i = 0; i < n; ++i) {
+            const uint64_t nb = (seq_lens[i] + FHIP_PAGE_TOKENS - 1) / FHIP_PAGE_TOKENS;
+            for (uint64_t j = 0; j < nb; ++j) {
+                const int32_t id = block_tables[i * max_blocks + j];
+                if (id < 0 || (uint64_t)id >= pp.pool_len)
+                    return fail(FHIP_ERR_INVALID_SHAPE, "sequence %llu: block id %d outside the "
+                                "pool of %zu", (unsigned long long)i, id, pp.pool_len);
+            }
+        }
+        return FHIP_OK;
+    };
     for (uint64_t i = 0; i < B; ++i) {
-        if (seq_lens[i] > max_blocks * FHIP_PAGE_TOKENS)
+        if (seq_lens[i] > max_blocks * FHIP_PAGE_TOKENS) {
+            r = id_error(i);
+            if (r) return r;
             return fail(FHIP_ERR_INVALID_SHAPE, "sequence %llu: %u positions in %zu blocks",
                         (unsigned long long)i, seq_lens[i], max_blocks);
-        const uint64_t nb = (seq_lens[i] + FHIP_PAGE_TOKENS - 1) / FHIP_PAGE_TOKENS;
-        for (uint64_t j = 0; j < nb; ++j) {
-            const int32_t id = block_tables[i * max_blocks + j];
-            if (id < 0 || (uint64_t)id >= pp.pool_len)
-                return fail(FHIP_ERR_INVALID_SHAPE, "sequence %llu: block id %d outside the "
-                            "pool of %zu", (unsigned long long)i, id, pp.pool_len);
         }
     }
     if (B == 0) return FHIP_OK;
@@ -1904,6 +1919,23 @@ int fhip_attention_paged_tq_batched(fhip_backend* b, const fhip_tensor* q,
     }
     r = b->stage_ahead_copy(s1, staged);
     if (r) return r;
+    // The block ids, checked in the slot while its copy runs: one unsigned compare per id,
+    // OR-reduced without branches (the compiler vectorizes it; a loop that leaves at the
+    // first bad id does not, and cost ~4x as much at 64 sequences of up to 2048 blocks).
+    // Ids are int32, so with a pool of 2^31 blocks or more only the negative ones are out.
+    const uint32_t lim = pp.pool_len < 0x80000000ull ? (uint32_t)pp.pool_len : 0x80000000u;
+    uint32_t bad = 0;
+    for (uint64_t i = 0; i < B; ++i) {
+        const uint64_t nb = (seq_lens[i] + FHIP_PAGE_TOKENS - 1) / FHIP_PAGE_TOKENS;
+        const int32_t* row = htable + i * stride;
+        uint32_t m = 0;
+        for (uint64_t j = 0; j < nb; ++j) m |= (uint32_t)((uint32_t)row[j] >= lim);
+        bad |= m;
+    }
+    r = b->stage_ahead_wait(s1);
+    if (r) return r;
+    // nothing reads the slot: its next reuse waits for both streams (it stays handed out)
+    if (bad) return id_error(B);
     const void** dp = pp.dev;
     const size_t n = pp.pool_len;
     int e = fhip_internal::attention_tq_decode_ptrs_staged(
