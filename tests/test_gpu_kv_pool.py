@@ -257,6 +257,50 @@ def test_attention_batched_pool(backend, hd, kb, vb):
         backend.free(t)
 
 
+def test_batched_pool_error_order(backend):
+    """fhip_attention_paged_tq_batched names the first failing sequence in row order, whether
+    its failure is a block id outside the pool or a length past the table's width; block ids
+    past a sequence's used blocks are neither read nor checked; and after a rejected call
+    (an id error is found once the table is staged, so it holds a slot of the staging ring)
+    more than a turn of the ring later every call still gives the first call's output."""
+    kvh, hd, qh, kb, vb, P = 2, 64, 4, 4, 4, 8
+    lists, pool = make_pool(backend, P, kvh, hd, kb, vb)
+    krot, vrot = tq.rotation_matrix(hd, 42), tq.rotation_matrix(hd, 542)
+    kc = tq.codebook(hd, kb)[0]
+    tkr, tvr, tc = (backend.upload(a) for a in (krot, vrot, kc))
+    rng = np.random.default_rng(3)
+    q = backend.upload(rng.standard_normal((3, qh, hd)).astype(np.float16))
+    out = backend.alloc([3, qh, hd], DType.FP16)
+    good = np.array([[0, 1], [2, 3], [4, 5]], np.int32)
+    lens = np.array([20, 32, 5], np.uint32)
+
+    def call(table, ls):
+        backend.attention_paged_tq_batched(q, table, ls, pool, tkr, tvr, tc, tc, kb, vb, kvh, out)
+
+    call(good, lens)
+    ref = backend.download(out).view(np.uint16).copy()
+    bad = good.copy()
+    bad[0, 1] = P  # sequence 0: an id outside the pool; sequence 1: 33 positions in 2 blocks
+    with pytest.raises(InvalidShape, match=r"sequence 0: block id 8 outside the pool of 8"):
+        call(bad, np.array([20, 33, 5], np.uint32))
+    bad = good.copy()
+    bad[1, 0] = -1  # sequence 0: 33 positions in 2 blocks; sequence 1: a negative id
+    with pytest.raises(InvalidShape, match=r"sequence 0: 33 positions in 2 blocks"):
+        call(bad, np.array([33, 32, 5], np.uint32))
+    bad = good.copy()
+    bad[2, 0] = P + 5  # the last sequence only
+    with pytest.raises(InvalidShape, match=r"sequence 2: block id 13 outside the pool of 8"):
+        call(bad, lens)
+    loose = good.copy()
+    loose[2, 1] = -7  # 5 positions use block 0 of the row only
+    for i in range(20):
+        call(loose, lens)
+        assert np.array_equal(backend.download(out).view(np.uint16), ref), f"call {i}"
+    backend.page_pool_destroy(pool)
+    for t in [x for l in lists for x in l] + [q, out, tkr, tvr, tc]:
+        backend.free(t)
+
+
 def test_batched_pool_c5_workload(backend):
     """The decode-attention benchmark workload through the handle runtime, as the engine would
     drive it: per-block tensors registered as a pool, each sequence's K/V written with
