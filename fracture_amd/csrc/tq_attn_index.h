@@ -24,9 +24,15 @@ constexpr int kXcdCount = 8;         // MI355X: workgroup b runs on XCD b % 8
 
 // Workgroup wg -> (item, kv head g). An item is a (query group, block); the 8 kv heads of one
 // item land on one XCD, whose L2 then holds the 128-byte lines that those heads' code rows share.
+// Item i runs on XCD (i + i / 8) % 8: each group of 8 consecutive items is rotated by its group
+// index. With XCD i % 8 instead, a query's blocks b, b + 8, b + 16, ... all land on XCD b % 8
+// whenever the block count per query is a multiple of 8 (32 at 32768 positions), and as the
+// later blocks exist only for the longer sequences, XCD 0 got up to 1.6x the work of XCD 7.
 FHIP_IDX void wg_item(int64_t wg, int kvh, int64_t& item, int& g) {
     const int64_t per8 = (int64_t)kXcdCount * kvh;
-    item = (wg / per8) * kXcdCount + wg % kXcdCount;
+    const int64_t a = wg / per8;              // the group of 8 items
+    const int x = (int)(wg % kXcdCount);      // the XCD
+    item = a * kXcdCount + (x - (int)(a % kXcdCount) + kXcdCount) % kXcdCount;
     g = (int)((wg % per8) / kXcdCount);
 }
 

@@ -316,3 +316,30 @@ def test_page_stride_smaller_than_page_is_caught():
         small[key] //= 2
         with pytest.raises(AssertionError):
             model_mfma_kernel(lens, table, 3, 32, 8, small, pool)
+
+
+def test_wg_item_balances_xcds():
+    """The MFMA kernel's workgroup -> item map (wg_item) on the decode-attention benchmark's
+    grid: workgroup wg runs on XCD wg % 8; every kv head of an item lands on one XCD (the L2 that
+    holds their shared code lines), and the positions the 8 XCDs process are within 5% of their
+    mean. Placing item i on XCD i % 8 instead puts every query's blocks b, b + 8, ... on one XCD
+    (32 blocks per query here), and since later blocks exist only for longer sequences, that
+    placement is off by more than 20%: the check tells the two apart."""
+    ix = index_lib()
+    lens, table, _ = c5_workload()
+    kvh, max_blocks = 8, table.shape[1]
+    nsplit = ws_layout(len(lens), 32, 128, max_blocks * PAGE)[0]
+    assert nsplit % 8 == 0
+    items = len(lens) * nsplit
+    wgs = (items + 7) // 8 * 8 * kvh
+    work = lambda it: (max(0, min(SPLIT, causal_len(lens[it // nsplit], max_blocks) - (it % nsplit) * SPLIT))
+                       if it < items else 0)
+    xcd_of_item, load, naive = {}, np.zeros(8), np.zeros(8)
+    for wg in range(wgs):
+        item, g = ix.wg_item(wg, kvh)
+        assert xcd_of_item.setdefault(item, wg % 8) == wg % 8, "an item's kv heads on two XCDs"
+        load[wg % 8] += work(item)
+        naive[item % 8] += work(item)
+    assert load.sum() == naive.sum() == kvh * sum(causal_len(n, max_blocks) for n in lens)
+    assert load.max() / load.mean() < 1.05, load / load.mean()
+    assert naive.max() / naive.mean() > 1.20, naive / naive.mean()
