@@ -170,7 +170,10 @@ __global__ __launch_bounds__(256) void tq_attn_split_kernel(
     const float* __restrict__ qrot, Queries qs, Pages pg, const float* __restrict__ kcent,
     const float* __restrict__ vcent, int kbits_rt, int vbits_rt, int qh, int kvh, int hd,
     float scale, float* __restrict__ part_ml, float* __restrict__ part_acc, int nsplit) {
-    const int split = blockIdx.x, kvhead = blockIdx.y, qi = blockIdx.z;
+    int split, kvhead, qi;  // grid (nsplit, kvh, queries), placed on the XCDs by split_grid_item
+    fhip_idx::split_grid_item(
+        blockIdx.x + (int64_t)gridDim.x * (blockIdx.y + (int64_t)gridDim.y * blockIdx.z),
+        (int64_t)gridDim.x * gridDim.y * gridDim.z, nsplit, kvh, split, kvhead, qi);
     const int clen = qs.causal_len(qi);
     const int t0 = split * kSplit;
     if (t0 >= clen) return;

@@ -36,6 +36,24 @@ FHIP_IDX void wg_item(int64_t wg, int kvh, int64_t& item, int& g) {
     g = (int)((wg % per8) / kXcdCount);
 }
 
+// The VALU split kernel's grid (nsplit, kvh, queries): workgroup `lin` in linear dispatch order
+// (of `total`) -> (split, kv head, query). In the grid's own order split s of every (kv head,
+// query) would run on XCD s % 8 whenever nsplit is a multiple of 8, loading XCD 0 most (later
+// splits exist only for longer sequences). Each full group of 8 consecutive workgroups is
+// rotated by its group index instead, as in wg_item; a partial last group keeps its order.
+// The rotated index is then decoded split fastest.
+FHIP_IDX void split_grid_item(int64_t lin, int64_t total, int nsplit, int kvh, int& split,
+                              int& kvhead, int& qi) {
+    const int64_t grp = lin / kXcdCount;
+    const int64_t eff =
+        (grp + 1) * kXcdCount <= total
+            ? grp * kXcdCount + ((int)(lin % kXcdCount) - (int)(grp % kXcdCount) + kXcdCount) % kXcdCount
+            : lin;
+    split = (int)(eff % nsplit);
+    kvhead = (int)((eff / nsplit) % kvh);
+    qi = (int)(eff / ((int64_t)nsplit * kvh));
+}
+
 // First position of wave `wave`'s split in block blk.
 FHIP_IDX int split_begin(int blk, int wave) { return (kBlockWaves * blk + wave) * kSplitPositions; }
 

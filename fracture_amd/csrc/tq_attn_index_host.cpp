@@ -35,6 +35,20 @@ int fhip_idx_wg_item(int64_t wg, int kvh, int64_t* item, int32_t* g) {
     return 0;
 }
 
+// Workgroup lin of the VALU split kernel's grid (nsplit, kvh, nq) -> (split, kv head, query).
+int fhip_idx_split_grid_item(int64_t lin, int nsplit, int kvh, int nq, int32_t* split,
+                             int32_t* kvhead, int32_t* qi) {
+    const int64_t total = (int64_t)nsplit * kvh * nq;
+    if (nsplit < 1 || kvh < 1 || nq < 1 || lin < 0 || lin >= total || !split || !kvhead || !qi)
+        return -1;
+    int s, h, q;
+    fhip_idx::split_grid_item(lin, total, nsplit, kvh, s, h, q);
+    *split = s;
+    *kvhead = h;
+    *qi = q;
+    return 0;
+}
+
 // Wave `wave` of block blk: its split's first position, and per lane the block-table column
 // of split page `lane` and whether that page holds positions of [t_begin, t_end).
 int fhip_idx_split(int blk, int wave, int t_end, int32_t* t_begin, int32_t* column,

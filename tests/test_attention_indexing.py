@@ -86,6 +86,7 @@ class IndexLib:
         L.fhip_idx_partial_row.argtypes = [C.c_int] * 7
         L.fhip_idx_partial_row.restype = C.c_int64
         L.fhip_idx_lane_tables.argtypes = [C.c_int, C.c_int] + [C.c_void_p] * 6
+        L.fhip_idx_split_grid_item.argtypes = [C.c_int64, C.c_int, C.c_int, C.c_int] + [C.POINTER(C.c_int32)] * 3
         self._tables = {}
 
     def lane_tables(self, kvh, g):
@@ -102,6 +103,12 @@ class IndexLib:
             self._tables[key] = (k_off.astype(np.int64), k_page, v_off.astype(np.int64),
                                  n_off.astype(np.int64), n_page, q_off)
         return self._tables[key]
+
+    def split_grid_item(self, lin, nsplit, kvh, nq):
+        s, h, q = self.C.c_int32(), self.C.c_int32(), self.C.c_int32()
+        assert self.lib.fhip_idx_split_grid_item(lin, nsplit, kvh, nq, self.C.byref(s), self.C.byref(h),
+                                                 self.C.byref(q)) == 0
+        return s.value, h.value, q.value
 
     def wg_item(self, wg, kvh):
         item, g = self.C.c_int64(), self.C.c_int32()
@@ -341,5 +348,30 @@ def test_wg_item_balances_xcds():
         load[wg % 8] += work(item)
         naive[item % 8] += work(item)
     assert load.sum() == naive.sum() == kvh * sum(causal_len(n, max_blocks) for n in lens)
+    assert load.max() / load.mean() < 1.05, load / load.mean()
+    assert naive.max() / naive.mean() > 1.20, naive / naive.mean()
+
+
+def test_split_grid_item_covers_grid_and_balances_xcds():
+    """The VALU split kernel's workgroup map (split_grid_item, grid (nsplit, kvh, queries)):
+    every (split, kv head, query) exactly once, on grids with and without a partial last group
+    of 8 workgroups; and on the decode benchmark's lengths (32 splits per query) the positions
+    the 8 XCDs process (workgroup lin on XCD lin % 8) are within 5% of their mean, where the
+    grid's own order leaves them over 20% apart."""
+    ix = index_lib()
+    for nsplit, kvh, nq in [(32, 8, 3), (3, 1, 5), (7, 2, 3), (1, 1, 1), (8, 4, 9), (5, 3, 7)]:
+        total = nsplit * kvh * nq
+        got = {ix.split_grid_item(lin, nsplit, kvh, nq) for lin in range(total)}
+        assert got == {(s, h, q) for s in range(nsplit) for h in range(kvh) for q in range(nq)}
+    lens, _, _ = c5_workload()
+    nsplit, kvh, nq = 32, 8, len(lens)
+    assert (lens <= nsplit * SPLIT).all()
+    work = lambda s, q: max(0, min(SPLIT, int(lens[q]) - s * SPLIT))
+    load, naive = np.zeros(8), np.zeros(8)
+    for lin in range(nsplit * kvh * nq):
+        s, _, q = ix.split_grid_item(lin, nsplit, kvh, nq)
+        load[lin % 8] += work(s, q)
+        naive[lin % 8] += work(lin % nsplit, lin // (nsplit * kvh))
+    assert load.sum() == naive.sum()
     assert load.max() / load.mean() < 1.05, load / load.mean()
     assert naive.max() / naive.mean() > 1.20, naive / naive.mean()
