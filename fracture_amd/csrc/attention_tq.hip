@@ -742,6 +742,31 @@ __device__ __forceinline__ void dma_v(const PageAddrs* pages, int j0, uint32_t v
 #pragma unroll
     for (int i = 0; i < 4; ++i) dma16(addr_of_lane(v4, i), voff, vb + 1024 * i);
 }
+// 2-bit V codes (kV2): the same segments as dma_v, from rows of 32 bytes. Lane L takes 8 bytes of
+// position 16i + L / 4 of page j0 + i (v2_offset), and once they have arrived store_v2 widens
+// each 2-bit code to a 4-bit one and writes the 16 bytes that dma_v would have copied, so the
+// transposed reads and the pair table serve both widths (its V entries map codes 0..3).
+typedef __attribute__((address_space(1))) const u32x2 g_u32x2;
+__device__ __forceinline__ void load_v2(const PageAddrs* pages, int j0, uint32_t voff,
+                                        u32x2 (&r)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = *(g_u32x2*)(pages[j0 + i].v + voff);
+}
+// Bytes sel of w (two code bytes, four codes each, the first in the top bits) as four bytes
+// of 4-bit codes, the first in the high nibble: byte b -> (c0 << 4 | c1), (c2 << 4 | c3).
+__device__ __forceinline__ uint32_t widen2(uint32_t w, uint32_t sel) {
+    const uint32_t x = __builtin_amdgcn_perm(w, w, sel);  // b0, b0, b1, b1
+    return ((x & 0x00C000C0u) >> 2) | ((x & 0x00300030u) >> 4) | ((x & 0x0C000C00u) << 2) |
+           (x & 0x03000300u);
+}
+__device__ __forceinline__ void store_v2(const u32x2 (&r)[4], uint8_t* vb, int lane) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        *(u32x4*)(vb + 1024 * i + 16 * lane) =
+            u32x4{widen2(r[i][0], 0x01010000u), widen2(r[i][0], 0x03030202u),
+                  widen2(r[i][1], 0x01010000u), widen2(r[i][1], 0x03030202u)};
+}
+
 // Norms of position t0 + lane, loaded raw (fp16 bits): pack() gives (knorm, vnorm) in fp32
 // once they are needed (0 where there is none), so each norm is converted once, by the lane
 // that loaded it. Packing later keeps the wait for them away from the copies issued after them.
@@ -813,7 +838,7 @@ __device__ __forceinline__ void expand_weights(uint32_t (&b)[4], const uint32_t 
     }
 }
 
-template <class Pages, bool kG4>
+template <class Pages, bool kG4, bool kV2>
 __global__ __launch_bounds__(64 * kWavesM) __attribute__((amdgpu_waves_per_eu(3))) void
 tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
                     const float* __restrict__ kcent, const float* __restrict__ vcent, int qh,
@@ -858,7 +883,8 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     for (int b = threadIdx.x; b < 256; b += 64 * kWavesM) {
         float hf;
         const uint32_t kh = hi_lo_pair(kcent[b >> 4], hf), kl = hi_lo_pair(kcent[b & 15], hf);
-        const uint32_t vh = hi_lo_pair(vcent[b >> 4], hf), vl = hi_lo_pair(vcent[b & 15], hf);
+        const int v0 = kV2 ? min(b >> 4, 3) : b >> 4, v1 = kV2 ? min(b & 15, 3) : b & 15;
+        const uint32_t vh = hi_lo_pair(vcent[v0], hf), vl = hi_lo_pair(vcent[v1], hf);
         pk[b] = u32x2{kh, kl};
         pv[b] = u32x2{vl, vh};
         if (b == 0) waves_done = 0;
@@ -895,9 +921,13 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
     const uint64_t vmask = t_begin < clen ? split_pages(pg, table, t_begin, t_end, lane, pages) : 0;
     if (vmask != 0) {
     // first chunk's copies go out before the Q set-up
-    const uint32_t v_lane_off = fhip_idx::v_offset(lane, kvh, g);
+    const uint32_t v_lane_off = kV2 ? fhip_idx::v2_offset(lane, kvh, g) : fhip_idx::v_offset(lane, kvh, g);
     uint32_t pmask = (uint32_t)vmask & 0xfu;  // pages of the current chunk to read
-    dma_v(pages, 0, v_lane_off, vb, lane);  // chunk 0: buffer 0
+    u32x2 v2reg[kV2 ? 4 : 1];  // kV2: the next chunk's V codes, widened into LDS when it starts
+    if constexpr (kV2)
+        load_v2(pages, 0, v_lane_off, v2reg);
+    else
+        dma_v(pages, 0, v_lane_off, vb, lane);  // chunk 0: buffer 0
     NormRegs nreg = load_norms(pages, 0, pmask, t_begin, t_end, kvh, g, lane);
     u32x4 kreg[4];
     load_k(pages, 0, kvh, g, lane, kreg);
@@ -970,6 +1000,9 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
         float scc[4];    // kG4 [e]: position 16rg + 4e + ptc, head n & 3
         // all loads of this chunk are in (the V copies included)
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // the V buffer PV reads below (the sync after the norm records orders these writes
+        // before the transposed reads)
+        if constexpr (kV2) store_v2(v2reg, vb + par * (kChunkM * 64), lane);
         const u32x4 kcs[4] = {kreg[0], kreg[1], kreg[2], kreg[3]};
         // 32 MFMA steps t = (tile pt, word s2, half): the A operand of step t holds the table
         // entries of bytes 2 half, 2 half + 1 of word s2 (coordinates 8 s2 + 4 half + 0..3).
@@ -1028,7 +1061,10 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
         wave_lds_sync();
         uint8_t* vnext = vb + (par ^ 1) * (kChunkM * 64);
         if (tn < t_end) {
-            dma_v(pages, jn, v_lane_off, vnext, lane);
+            if constexpr (kV2)
+                load_v2(pages, jn, v_lane_off, v2reg);
+            else
+                dma_v(pages, jn, v_lane_off, vnext, lane);
             nreg = load_norms(pages, jn, pmask_n, tn, t_end, kvh, g, lane);
             load_k(pages, jn, kvh, g, lane, kreg);
         }
@@ -1266,7 +1302,7 @@ tq_attn_mfma_kernel(const float* __restrict__ qrot, Queries qs, Pages pg,
 template <class Pages>
 void launch_mfma_split(const float* qrot, const Queries& qsv, const Pages& pg,
                        const float* kcent, const float* vcent, int nq, int qh, int kvh,
-                       int nsplit, float* ml, float* acc, hipStream_t s) {
+                       int nsplit, bool v2, float* ml, float* acc, hipStream_t s) {
     // Causal prefill (queries at consecutive positions of one sequence: one shared block table,
     // lengths from start_pos) groups 8 / G consecutive queries per item so that they share the
     // MFMA columns and every code lookup; decode keeps one query per item.
@@ -1279,8 +1315,9 @@ void launch_mfma_split(const float* qrot, const Queries& qsv, const Pages& pg,
     const int64_t wgs = ceil_div(items * nsplit, kXcds) * kXcds * kvh;
     Queries q2 = qsv;
     q2.seq_lens_count = nq;
-    auto kern = G <= 4 && tok == 1 ? tq_attn_mfma_kernel<Pages, true>
-                                   : tq_attn_mfma_kernel<Pages, false>;
+    const bool g4 = G <= 4 && tok == 1;
+    auto kern = v2 ? (g4 ? tq_attn_mfma_kernel<Pages, true, true> : tq_attn_mfma_kernel<Pages, false, true>)
+                   : (g4 ? tq_attn_mfma_kernel<Pages, true, false> : tq_attn_mfma_kernel<Pages, false, false>);
     hipLaunchKernelGGL(kern, dim3((unsigned)wgs), dim3(64 * kWavesM), 0, s, qrot, q2, pg, kcent,
                        vcent, qh, kvh, 1.0f / sqrtf(128.0f), ml, acc, nsplit, nsplit, tok);
 }
@@ -1342,8 +1379,9 @@ int launch_attention(const AttnArgs& a, const Pages& pg, hipStream_t s) {
         hipLaunchKernelGGL(tq_attn_prerotate_kernel, dim3(rot_groups), dim3(256), 0, s,
                            (const uint16_t*)a.q, a.krot, qrot, a.hd, nvec);
     }
-    if (a.kbits == 4 && a.vbits == 4 && a.hd == 128 && a.qh / a.kvh <= 8)
-        launch_mfma_split(qrot, a.qs, pg, a.kcent, a.vcent, a.nq, a.qh, a.kvh, nsplit, ml, acc, s);
+    if (a.kbits == 4 && (a.vbits == 4 || a.vbits == 2) && a.hd == 128 && a.qh / a.kvh <= 8)
+        launch_mfma_split(qrot, a.qs, pg, a.kcent, a.vcent, a.nq, a.qh, a.kvh, nsplit,
+                          a.vbits == 2, ml, acc, s);
     else if (a.kbits == 4 && a.vbits == 4)
         launch_split<4, 4>(a, pg, nsplit, ml, acc, s);
     else if (a.kbits == 4 && a.vbits == 2)

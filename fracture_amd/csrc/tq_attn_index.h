@@ -1,5 +1,5 @@
 // Index arithmetic of the MFMA decode-attention kernel (tq_attn_mfma_kernel, head_dim 128,
-// 4-bit K and V codes), shared by the kernel and by a host build of the same functions
+// 4-bit K codes, 4- or 2-bit V codes), shared by the kernel and by a host build of the functions
 // (tq_attn_index_host.cpp). The CPU bounds check of every global access the kernel makes
 // calls the host build, so it covers the arithmetic the kernel runs rather than a restatement
 // of it. Page layout (quantized_paged_kv_cache.rs:86-128): a page holds 16 positions; its K
@@ -81,6 +81,11 @@ FHIP_IDX uint32_t k_tile_stride(int kvh) { return (uint32_t)(kvh * kCodeRow); }
 // code row (the XOR swizzle spreads a transposed read of one dim range over the banks).
 FHIP_IDX uint32_t v_offset(int lane, int kvh, int g) {
     return (uint32_t)(((lane >> 2) * kvh + g) * kCodeRow + 16 * ((lane & 3) ^ ((lane >> 3) & 3)));
+}
+// The same with 2-bit V codes (rows of kCodeRow / 2 bytes): lane L loads the 8 bytes that hold
+// the codes of the 16-byte segment v_offset names, and widens them to it.
+FHIP_IDX uint32_t v2_offset(int lane, int kvh, int g) {
+    return (uint32_t)(((lane >> 2) * kvh + g) * (kCodeRow / 2) + 8 * ((lane & 3) ^ ((lane >> 3) & 3)));
 }
 
 // Norms of a chunk: lane L reads split page chunk_first_page + norm_page(L), the fp16 norm of

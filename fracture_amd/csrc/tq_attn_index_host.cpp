@@ -26,6 +26,13 @@ int fhip_idx_lane_tables(int kvh, int g, uint32_t* k_off, int32_t* k_page, uint3
     return 0;
 }
 
+// 2-bit V codes: the per-lane load offsets v2_off[lane] for kv head g of kvh.
+int fhip_idx_v2_offsets(int kvh, int g, uint32_t* v2_off) {
+    if (kvh < 1 || g < 0 || g >= kvh || !v2_off) return -1;
+    for (int lane = 0; lane < 64; ++lane) v2_off[lane] = fhip_idx::v2_offset(lane, kvh, g);
+    return 0;
+}
+
 // Workgroup wg of a launch with kvh kv heads -> its item and kv head.
 int fhip_idx_wg_item(int64_t wg, int kvh, int64_t* item, int32_t* g) {
     if (kvh < 1 || wg < 0 || !item || !g) return -1;

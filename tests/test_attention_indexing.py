@@ -86,6 +86,7 @@ class IndexLib:
         L.fhip_idx_partial_row.argtypes = [C.c_int] * 7
         L.fhip_idx_partial_row.restype = C.c_int64
         L.fhip_idx_lane_tables.argtypes = [C.c_int, C.c_int] + [C.c_void_p] * 6
+        L.fhip_idx_v2_offsets.argtypes = [C.c_int, C.c_int, C.c_void_p]
         L.fhip_idx_split_grid_item.argtypes = [C.c_int64, C.c_int, C.c_int, C.c_int] + [C.POINTER(C.c_int32)] * 3
         self._tables = {}
 
@@ -103,6 +104,11 @@ class IndexLib:
             self._tables[key] = (k_off.astype(np.int64), k_page, v_off.astype(np.int64),
                                  n_off.astype(np.int64), n_page, q_off)
         return self._tables[key]
+
+    def v2_offsets(self, kvh, g):
+        out = np.zeros(64, np.uint32)
+        assert self.lib.fhip_idx_v2_offsets(kvh, g, out.ctypes.data) == 0
+        return out.astype(np.int64)
 
     def split_grid_item(self, lin, nsplit, kvh, nq):
         s, h, q = self.C.c_int32(), self.C.c_int32(), self.C.c_int32()
@@ -141,10 +147,10 @@ def index_lib():
     return _IDX
 
 
-def model_mfma_kernel(lens, table, num_pages, qh, kvh, page_bytes, pool_bytes, tok=1):
-    """Every access of tq_attn_mfma_kernel<PoolPages> for one launch (hd 128, K4/V4), from the
-    kernel's own index functions. With tok > 1, `table` has one row that every query reads
-    (causal prefill). Walks every workgroup of the launcher's grid."""
+def model_mfma_kernel(lens, table, num_pages, qh, kvh, page_bytes, pool_bytes, tok=1, vbits=4):
+    """Every access of tq_attn_mfma_kernel<PoolPages> for one launch (hd 128, K4 and V4 or V2),
+    from the kernel's own index functions. With tok > 1, `table` has one row that every query
+    reads (causal prefill). Walks every workgroup of the launcher's grid."""
     ix = index_lib()
     hd, pd = 128, 64
     B = len(lens)
@@ -173,7 +179,10 @@ def model_mfma_kernel(lens, table, num_pages, qh, kvh, page_bytes, pool_bytes, t
         k_off, k_page, v_off, n_off, n_page, q_off = ix.lane_tables(kvh, g)
         for k in range(4):
             assert (k_off[k] + 16 <= PAGE * kvh * pd).all() and (k_off[k] + 16 <= page_bytes["kp"]).all()
-        assert (v_off + 16 <= min(PAGE * kvh * pd, page_bytes["vp"])).all()
+        vpd, vw = (pd, 16) if vbits == 4 else (pd // 2, 8)  # V row bytes, bytes per V load
+        if vbits == 2:
+            v_off = ix.v2_offsets(kvh, g)
+        assert (v_off + vw <= min(PAGE * kvh * vpd, page_bytes["vp"])).all()
         for nm in ("kn", "vn"):
             assert (n_off + 2 <= min(PAGE * kvh * 2, page_bytes[nm])).all()
         for w in range(SPLIT // WAVE_SPLIT):
@@ -198,7 +207,7 @@ def model_mfma_kernel(lens, table, num_pages, qh, kvh, page_bytes, pool_bytes, t
                 for pt in range(4):  # K codes
                     bnd.check("kp", entry[j0 + k_page] * page_bytes["kp"] + k_off[pt], 16)
                 for i in range(4):  # V copies: copy i reads entry j0 + i
-                    bnd.check("vp", entry[j0 + i] * page_bytes["vp"] + v_off, 16)
+                    bnd.check("vp", entry[j0 + i] * page_bytes["vp"] + v_off, vw)
                 for nm in ("kn", "vn"):  # norms
                     bnd.check(nm, entry[j0 + n_page] * page_bytes[nm] + n_off, 2)
             vec, live = ix.q_vectors(tq0, tok, G, B, qh, g)
@@ -257,8 +266,9 @@ def pools(P, kvh, pd=64):
     return page, {k: v * P for k, v in page.items()}
 
 
+@pytest.mark.parametrize("vbits", [4, 2])
 @pytest.mark.parametrize("which", ["c5", "edges", "long"])
-def test_mfma_decode_accesses_in_bounds(which):
+def test_mfma_decode_accesses_in_bounds(which, vbits):
     if which == "long":
         # a context of 270,000 positions (264 partial blocks) over a permuted table
         lens = np.array([270000, 5], np.int32)
@@ -286,7 +296,10 @@ def test_mfma_decode_accesses_in_bounds(which):
         table[3, 1] = P + 5      # a page id past the pool: masked, never read
     qh, kvh = 32, 8
     page, pool = pools(P, kvh)
-    bnd, nsplit = model_mfma_kernel(lens, table, P, qh, kvh, page, pool)
+    if vbits == 2:  # V pages of 32-byte rows
+        page["vp"] //= 2
+        pool["vp"] //= 2
+    bnd, nsplit = model_mfma_kernel(lens, table, P, qh, kvh, page, pool, vbits=vbits)
     assert bnd.count["kp"] > 0 and bnd.count["vp"] > 0
     _, _, ml, acc = ws_layout(len(lens), qh, 128, table.shape[1] * PAGE)
     model_combine(lens, table.shape[1], qh, 128, nsplit, ml, acc)

@@ -188,15 +188,16 @@ def test_reference_interface_mfma_long(dev, kv_len, T):
 @pytest.mark.parametrize("qh,kvh,T,kv_len", [(32, 8, 40, 2060), (16, 8, 13, 1030),
                                              (8, 8, 20, 530), (64, 8, 6, 300),
                                              (32, 8, 131, 1500)])
-def test_prefill_token_groups_vs_oracle(dev, qh, kvh, T, kv_len):
-    """Causal prefill through fhip_launch_attention_paged_tq (K4/V4, head_dim 128): the MFMA
+@pytest.mark.parametrize("vbits", [4, 2])
+def test_prefill_token_groups_vs_oracle(dev, qh, kvh, T, kv_len, vbits):
+    """Causal prefill through fhip_launch_attention_paged_tq (K4 with V4 or V2, head_dim 128): the MFMA
     kernel gives 8 / G consecutive queries one set of MFMA columns (G = 4, 2 and 1; G = 8
     keeps one query per item), with a ragged last group and causal lengths that cross a
     1024-position block, a 256-position wave split or a page inside one group. At 131 x 32
     query vectors (at least 4096) the query rotation and the unrotation of the merged outputs
     run as batched MFMA products instead of the per-8-vector kernels."""
     hd = 128
-    pool = gpu_pool(dev, 7 * T + kv_len, [kv_len], kvh, hd, 4, 4, extra_pages=4)
+    pool = gpu_pool(dev, 7 * T + kv_len + vbits, [kv_len], kvh, hd, 4, vbits, extra_pages=4)
     ptrs = _ptr_table(pool, dev)
     g = torch.Generator(device=dev)
     g.manual_seed(T + qh)
@@ -208,13 +209,14 @@ def test_prefill_token_groups_vs_oracle(dev, qh, kvh, T, kv_len):
     assert K._L().fhip_launch_attention_paged_tq(
         out.data_ptr(), q.data_ptr(), table.data_ptr(), ptrs[0].data_ptr(), ptrs[1].data_ptr(),
         ptrs[2].data_ptr(), ptrs[3].data_ptr(), d["krot"].data_ptr(), d["vrot"].data_ptr(),
-        d["kc"].data_ptr(), d["vc"].data_ptr(), T, qh, kvh, hd, kv_len, start, 4, 4, 64, 64,
+        d["kc"].data_ptr(), d["vc"].data_ptr(), T, qh, kvh, hd, kv_len, start, 4, vbits, 64,
+        hd * vbits // 8,
         torch.cuda.current_stream().cuda_stream) == 0
     torch.cuda.synchronize()
     got, qn = out.cpu().numpy(), q.cpu().numpy()
 
     def run(t):
-        return t, oracle_attention(pool, qn[t], 0, min(start + t + 1, kv_len), 4, 4, kvh)
+        return t, oracle_attention(pool, qn[t], 0, min(start + t + 1, kv_len), 4, vbits, kvh)
 
     with ThreadPoolExecutor(THREADS) as ex:
         for t, want in ex.map(run, range(T)):
