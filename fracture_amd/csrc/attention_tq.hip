@@ -533,7 +533,8 @@ __global__ __launch_bounds__(256) void tq_attn_combine_kernel(
 }
 
 // ---------------------------------------------------------------------------------------
-// 2'. MFMA split kernel: head_dim 128, 4-bit K and V codes, G <= 8 query heads per kv head.
+// 2'. MFMA split kernel: head_dim 128, 4-bit K codes and 4- or 2-bit V codes (kV2: widened to
+//     4 bits on their way into LDS), G <= 8 query heads per kv head.
 //
 // A workgroup owns one (query, kv head, 1024-position block); each of its two waves walks
 // one 512-position split of it in 64-position chunks:
