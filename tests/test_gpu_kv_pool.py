@@ -160,7 +160,7 @@ def host_pool(lists, backend):
     return [np.stack([backend.download(t) for t in lst]) for lst in lists]
 
 
-@pytest.mark.parametrize("hd,kb,vb", [(128, 4, 4), (64, 3, 3)])
+@pytest.mark.parametrize("hd,kb,vb", [(128, 4, 4), (128, 4, 2), (64, 3, 3)])
 def test_attention_batched_pool(backend, hd, kb, vb):
     """One batched call over a registered pool equals the oracle and, bit for bit, one pooled
     call per sequence (T=1 at its last position); calls that alternate two batches for more
