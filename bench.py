@@ -797,6 +797,13 @@ def run_attention(args, torch, K, dev):
         "frac_of_peak": round(gbs(nb, us) / PEAK_HBM_GBS, 4), "bytes": nb,
         "context_tokens": tok, "mean_ctx": mean,
         "traffic": traffic_of("attention_tq_decode")}}
+    fn, nb, _, _ = attention_inputs(torch, K, dev, vb=2)
+    us = Timer(torch).time_us(fn, 10, warmup=2)
+    kernels["attention_tq_decode_k4v2"] = {
+        "us": round(us, 1), "GB/s": round(gbs(nb, us), 1),
+        "frac_of_peak": round(gbs(nb, us) / PEAK_HBM_GBS, 4), "bytes": nb,
+        "note": "the same batch with 2-bit V codes: K4/V2 is TurboQuantConfig's default"}
+    del fn
     for T, kv_len in ((2048, 2048), (512, 8192)):
         pfn, pnb, scored = prefill_attention_inputs(torch, K, dev, T, kv_len)
         pus = Timer(torch).time_us(pfn, 5, warmup=2)
@@ -808,8 +815,8 @@ def run_attention(args, torch, K, dev):
             "note": "causal prefill through fhip_launch_attention_paged_tq_ws; bytes are the "
                     "distinct K/V pages, queries and outputs (each page is re-read by every "
                     "group of 8 / G queries)"}
-    return {"workload": "TurboQuant K4/V4 paged decode attention, B=64, 32/8 heads, hd 128; "
-                        "causal prefill of one sequence", "kernels": kernels}
+    return {"workload": "TurboQuant K4/V4 (and K4/V2) paged decode attention, B=64, 32/8 heads, "
+                        "hd 128; causal prefill of one sequence", "kernels": kernels}
 
 
 def paged_inputs(torch, K, dev):
@@ -900,13 +907,15 @@ CAL_BYTES = 1 << 30
 ATT_SHAPE = dict(B=64, QH=32, KVH=8, HD=128, kb=4, vb=4)
 
 
-def attention_inputs(torch, K, dev):
-    """The decode-attention workload: returns (fn, algorithmic bytes, context tokens, mean)."""
+def attention_inputs(torch, K, dev, vb=None):
+    """The decode-attention workload (V codes of ATT_SHAPE's width unless vb is given): returns
+    (fn, algorithmic bytes, context tokens, mean)."""
     import numpy as np
 
     from fracture_amd import turboquant as tq
 
-    B, QH, KVH, HD, kb, vb = (ATT_SHAPE[k] for k in ("B", "QH", "KVH", "HD", "kb", "vb"))
+    B, QH, KVH, HD, kb = (ATT_SHAPE[k] for k in ("B", "QH", "KVH", "HD", "kb"))
+    vb = ATT_SHAPE["vb"] if vb is None else vb
     lens = attention_lens()
     rng = np.random.default_rng(5)
     rng.integers(1024, 32769, B)  # the lengths' draw: the page permutation comes next
